@@ -1,0 +1,297 @@
+"""Benchmark of the gfx950 fused softplus-MLP forward megakernel.
+
+Default workload (throughput point): 3-layer
+D=H=OUT=128 fp16 forward at M = 1,048,576 rows, seeded synthetic inputs
+(x ~ N(0,1), W_l ~ N(0, 1/in)) resident in HBM before timing.  A "step" is one
+launch over the whole batch.  Two input/output buffer pairs alternate so the
+1 GiB working set cannot sit in the 256 MB Infinity Cache.
+
+Prints ONE JSON line (the driver's contract) with the headline throughput,
+the roofline fraction of the forward kernel, and the CPU baseline (the numpy
+oracle on the host cores, bounded sample).  ``--config`` / ``--m`` select
+other BASELINE configs, ``--sweep`` adds the latency sweep M = 64..4096.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fwd rows/s + % of fp16 MFMA/HBM roofline, 3-layer 128-wide MLP, M=64..1M"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense fp16, published (2.5 PF)
+
+CONFIG_DIMS = {
+    "3l128": (128, 128, 128, 128),
+    "5l128": (128, 128, 128, 128, 128, 128),
+    "narrow": (32, 64, 64, 16),
+}
+DEFAULT_M = {"3l128": 1048576, "5l128": 1048576, "narrow": 4194304}
+
+
+def algorithmic(dims, m):
+    """(bytes, flops) of one forward launch: x + out rows once, weights once."""
+    wbytes = 2 * sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
+    rbytes = 2 * (dims[0] + dims[-1])
+    flops = 2 * sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
+    return rbytes * m + wbytes, flops * m
+
+
+def make_device_inputs(torch, dims, m, seed, uniform):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    if uniform:
+        x = (torch.rand((m, dims[0]), generator=g, device="cuda") * 2 - 1).half()
+    else:
+        x = torch.randn((m, dims[0]), generator=g, device="cuda").half()
+    ws = [
+        (torch.randn((dims[i], dims[i + 1]), generator=g, device="cuda") / dims[i] ** 0.5).half()
+        for i in range(len(dims) - 1)
+    ]
+    return x, ws
+
+
+def time_launches(torch, fn, steps, warmup):
+    """Average ms per launch over `steps` back-to-back launches, bracketed by
+    HIP events on the launch stream (torch's current stream)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_graph(torch, fn, iters=100, warmup=20):
+    """Median ms per graph replay of one launch (launch overhead removed),
+    as /root/reference/profile.py:50-80 measures."""
+    for i in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn(0)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    for _ in range(iters):
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_threads():
+    try:
+        from threadpoolctl import threadpool_info
+
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(orc, dims, uniform, budget_s=10.0, chunk=65536):
+    """The numpy oracle's forward (fp32, BLAS matmuls) on host cores over a
+    bounded sample: repeated `chunk`-row batches until `budget_s` has elapsed."""
+    x, ws = orc.make_inputs(dims, chunk, seed=7, x_dist="uniform" if uniform else "normal")
+    orc.forward(x[:1024], ws)  # warm the BLAS threads
+    rows = 0
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        orc.forward(x, ws)
+        rows += chunk
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and reps >= 2:
+            break
+    return {
+        "value": rows / el,
+        "unit": "rows/s",
+        "cores": cpu_threads(),
+        "kind": "port",
+        "sample": f"numpy oracle fp32 forward, {reps} x {chunk} rows of the same config in {el:.1f} s "
+        f"(BLAS matmuls threaded, softplus single-threaded numpy)",
+    }
+
+
+def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
+    """The reference's eager math (kernel.py:168-171) in PyTorch on the CPU, fp32."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.rand((chunk, dims[0]), generator=g) * 2 - 1) if uniform else torch.randn((chunk, dims[0]), generator=g)
+    ws = [torch.randn((dims[i], dims[i + 1]), generator=g) / dims[i] ** 0.5 for i in range(len(dims) - 1)]
+    F = torch.nn.functional
+
+    def run():
+        a = x
+        for i, w in enumerate(ws):
+            a = a @ w
+            if i < len(ws) - 1:
+                a = F.softplus(a)
+        return a
+
+    run()
+    rows, reps, t0 = 0, 0, time.perf_counter()
+    while True:
+        run()
+        rows += chunk
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and reps >= 2:
+            break
+    return {"value": rows / el, "unit": "rows/s", "threads": torch.get_num_threads(), "sample": f"{reps} x {chunk} rows fp32"}
+
+
+def load_traffic(workload):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", choices=sorted(CONFIG_DIMS), default="3l128")
+    ap.add_argument("--m", type=int, default=None)
+    ap.add_argument("--sweep", action="store_true", help="add the M=64..4096 latency sweep")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py: this build measures ONE GPU; the forward shards rows with zero exchange and "
+            "no multi-GPU figure is produced (run with --gpus 1)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+    import _mlpmk  # noqa: F401
+    from mlpmk import ops
+    from oracle import mlp_oracle as orc
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    dims = CONFIG_DIMS[args.config]
+    uniform = args.config == "narrow"
+    m = args.m or DEFAULT_M[args.config]
+    workload = f"{args.config} fwd fp16 M={m}"
+
+    # --- inputs resident in HBM: two buffer pairs rotate -------------------
+    x0, ws = make_device_inputs(torch, dims, m, seed=0, uniform=uniform)
+    x1, _ = make_device_inputs(torch, dims, m, seed=1, uniform=uniform)
+    xs = [x0, x1]
+    outs = [torch.empty((m, dims[-1]), device="cuda", dtype=torch.float16) for _ in range(2)]
+
+    def step(i):
+        ops.fwd_into(xs[i & 1], ws, outs[i & 1])
+
+    # --- parity gate (sampled rows vs the CPU oracle) ----------------------
+    step(0)
+    torch.cuda.synchronize()
+    idx = torch.randperm(m, device="cuda")[:4096]
+    ok, maxerr, _ = orc.allclose_report(
+        outs[0][idx].float().cpu().numpy(),
+        orc.forward(x0[idx].cpu().numpy(), [w.cpu().numpy() for w in ws]),
+        1e-2,
+        1e-2,
+    )
+
+    # --- timed region -------------------------------------------------------
+    ms = time_launches(torch, step, args.steps, args.warmup)
+    nbytes, nflops = algorithmic(dims, m)
+    achieved_gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = nflops / (ms * 1e-3) / 1e12
+    ai = nflops / nbytes
+    roof_tflops = min(MFMA_F16_PEAK_TFLOPS, HBM_PEAK_GBS * ai / 1e3)
+    bound = "hbm" if HBM_PEAK_GBS * ai / 1e3 < MFMA_F16_PEAK_TFLOPS else "mfma"
+    if bound == "hbm":
+        roofline = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved_gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roofline = {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    roofline["traffic"] = load_traffic(workload)
+    roofline["kernel"] = "mlpmk::fwd_kernel"
+    roofline["algorithmic_bytes_per_launch"] = nbytes
+
+    # achievable-HBM reference: the library's 16-byte copy over 512 MiB
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    cms = time_launches(torch, lambda i: ops.copy_bytes(src, dst), 20, 5)
+    copy_gbs = 2 * src.numel() / (cms * 1e-3) / 1e9
+    del src, dst
+
+    result = {
+        "metric": METRIC,
+        "value": m / (ms * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) x, N(0,1/in) fp16 weights, resident in HBM)",
+        "config": {"workload": workload, "dims": list(dims), "M": m, "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "tflops": round(tflops, 2),
+        "roofline_tflops": round(roof_tflops, 1),
+        "frac_of_min_mfma_hbm_roofline": round(tflops / roof_tflops, 4),
+        "copy_kernel_gbs": round(copy_gbs, 1),
+        "parity": {"ok": ok, "max_abs_err": maxerr, "atol": 1e-2, "rtol": 1e-2, "rows_checked": 4096},
+        "device": torch.cuda.get_device_properties(0).name,
+    }
+
+    if args.sweep:
+        sweep = {}
+        for ms_m in (64, 128, 256, 512, 1024, 2048, 4096):
+            xx, ww = make_device_inputs(torch, dims, ms_m, seed=0, uniform=uniform)
+            oo = torch.empty((ms_m, dims[-1]), device="cuda", dtype=torch.float16)
+            ev = time_launches(torch, lambda i: ops.fwd_into(xx, ww, oo), 200, 20)
+            gr = time_graph(torch, lambda i: ops.fwd_into(xx, ww, oo))
+            sweep[str(ms_m)] = {"event_ms": round(ev, 5), "graph_ms": round(gr, 5)}
+        result["latency_sweep"] = sweep
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(orc, dims, uniform, budget_s=args.cpu_budget)
+        result["cpu_eager_torch_fp32"] = torch_eager_cpu(torch, dims, uniform, budget_s=args.cpu_budget / 2)
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,139 @@
+/*
+ * mlpmk.h -- C ABI of the MI355X (gfx950) fused softplus-MLP megakernel library
+ * (libmlpmk.so).  Plain pointers and sizes only: no C++ types, no exceptions,
+ * no torch types cross this boundary.
+ *
+ * Network: out = softplus(... softplus(x @ W1) ... @ W_{L-1}) @ W_L, no bias,
+ * softplus with beta = 1 and threshold = 20, fp16 operands, fp32 accumulation,
+ * fp16 output.  Weights are [in, out] row-major fp16, as the reference indexes
+ * them (/root/reference/kernel.py:105,109,113-114).
+ *
+ * Conventions (every entry point):
+ *   - Returns an mlpmk_status (0 = success).  Arguments are validated on the
+ *     host before anything touches the device; a failed validation launches
+ *     nothing.  mlpmk_last_error() gives a per-thread message for the last
+ *     failure.
+ *   - dims[] has num_layers + 1 entries: dims[0] = D (input features),
+ *     dims[1 .. num_layers-1] = hidden widths, dims[num_layers] = OUT.
+ *   - All device memory is caller-owned; the library allocates nothing.
+ *     Launches are asynchronous on `stream` (a hipStream_t, NULL = the legacy
+ *     default stream); nothing synchronises the host.
+ *   - Device pointers must be 16-byte aligned (128-bit loads and stores);
+ *     every tensor is dense row-major.
+ *   - M == 0 is a successful no-op.
+ *   - Functions are reentrant; device properties are read lazily, per device.
+ */
+#ifndef MLPMK_H
+#define MLPMK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mlpmk_status {
+  MLPMK_OK = 0,
+  MLPMK_ERR_INVALID_ARG = 1,       /* null pointer, negative size, bad dtype */
+  MLPMK_ERR_UNSUPPORTED_SHAPE = 2, /* no kernel instantiated for these dims */
+  MLPMK_ERR_MISALIGNED = 3,        /* a pointer is not 16-byte aligned */
+  MLPMK_ERR_HIP = 4,               /* a HIP runtime call failed */
+  MLPMK_ERR_NO_DEVICE = 5          /* no usable gfx950 device */
+} mlpmk_status;
+
+/* Parameter dtypes of the weight-norm entry points. */
+enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1 };
+
+/* Library ABI version (major * 100 + minor). */
+int mlpmk_version(void);
+
+/* Static description of a status code. */
+const char* mlpmk_status_string(int status);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* mlpmk_last_error(void);
+
+/* 1 if a forward kernel exists for (num_layers, dims), else 0.  Host only. */
+int mlpmk_fwd_supported(int num_layers, const int* dims);
+
+/* 1 if the backward kernel exists for (num_layers, dims), else 0.  Host only. */
+int mlpmk_bwd_supported(int num_layers, const int* dims);
+
+/*
+ * Forward megakernel (one launch).
+ *
+ * Replaces the reference's inference launcher `_fused_mlp_fwd(x, w1, w2, w3)`
+ * (/root/reference/kernel.py:130-156, kernel /root/reference/kernel.py:60-123)
+ * and its training-forward variant that stores the hidden activations
+ * (/root/reference/mlp_fused.md:52-61, fp32 storage README.md:30).
+ *
+ *   x      [M, dims[0]]            fp16, device
+ *   w[l]   [dims[l], dims[l+1]]    fp16, device, l = 0 .. num_layers-1
+ *   out    [M, dims[num_layers]]   fp16, device (written)
+ *   stash  NULL for inference, or an array of num_layers-1 device pointers,
+ *          stash[l] = h_{l+1} [M, dims[l+1]] fp32 (post-activation, written)
+ */
+int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const* w, void* out,
+              float* const* stash, int64_t M, void* stream);
+
+/*
+ * Backward megakernel (one launch): data gradients with MFMA, weight gradients
+ * as split-K partials reduced in LDS and then added with global fp32 atomics.
+ *
+ * Replaces the fused backward of the reference's `FusedMLPSoftplus` autograd
+ * function (/root/reference/mlp_fused.md:88-112, README.md:32) -- the file that
+ * held it (fused_mlp.py, README.md:18) is not in the reference snapshot.
+ *
+ *   x                [M, dims[0]] fp16
+ *   w[l]             as in mlpmk_fwd
+ *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd
+ *   dout             dL/dout, fp16, row l at dout + l * dout_row_stride
+ *                    elements; dout_row_stride = 0 broadcasts one row
+ *                    (the expanded ones of loss = out.sum())
+ *   dx               NULL, or [M, dims[0]] fp16 (written)
+ *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
+ *                    caller zeroes them for a fresh gradient
+ */
+int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
+              const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+              float* const* dw, int64_t M, void* stream);
+
+/*
+ * Weight-norm forward for all layers in ONE launch:
+ *   W_l[:, j] = g_l[j] * v_l[:, j] / ||v_l[:, j]||,   inv_norm_l[j] = 1 / ||v_l[:, j]||
+ * Replaces `_wn_fwd_kernel` (/root/reference/mlp_fused.md:473-477; code absent
+ * from the snapshot).  v and g live in two contiguous blocks, layer after layer
+ * (v_all / g_all, mlp_fused.md:478-480):
+ *   v      sum_l dims[l]*dims[l+1] elements of param_dtype, layer l = [dims[l], dims[l+1]]
+ *   g      sum_l dims[l+1] elements of param_dtype
+ *   w_out  same element layout as v, fp16 (written)
+ *   inv_norm  sum_l dims[l+1] fp32 (written)
+ */
+int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, const void* v, const void* g,
+                 void* w_out, float* inv_norm, void* stream);
+
+/*
+ * Weight-norm backward for all layers in ONE launch, reading the fp32 weight
+ * gradient in its [in, out] layout column-wise (no transposed copy):
+ *   u = v * inv_norm,  dg[j] = <dW[:, j], u[:, j]>,
+ *   dv[:, j] = g[j] * inv_norm[j] * (dW[:, j] - dg[j] * u[:, j])
+ * Replaces `_wn_bwd_from_dw_T_kernel` (/root/reference/mlp_fused.md:474,481-483).
+ *   dw        fp32, same element layout as v (one block, layer after layer)
+ *   dv, dg    param_dtype, layouts of v and g (written)
+ */
+int mlpmk_wn_bwd(int num_layers, const int* dims, int param_dtype, const float* dw, const void* v,
+                 const void* g, const float* inv_norm, void* dv, void* dg, void* stream);
+
+/*
+ * Diagnostic: a plain streaming copy of `bytes` bytes (multiple of 16) with the
+ * same 128-bit load/store width as the megakernels.  Used only to calibrate
+ * hardware byte counters (FETCH_SIZE / WRITE_SIZE) against a known size.  No
+ * counterpart in the reference.
+ */
+int mlpmk_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLPMK_H */

@@ -1,0 +1,125 @@
+// Device-side building blocks shared by the gfx950 megakernels.
+//
+// Orientation used by every kernel ("transposed" chaining): a layer computes
+// H^T = W^T . A^T with v_mfma_f32_32x32x16_f16, so the MFMA M dimension is the
+// layer's output features, K its input features and N the batch (rows of x).
+// With this orientation the fp32 C/D registers of one layer are, after the
+// activation and an fp16 pack, exactly the B operand of the next layer: no LDS
+// round trip and no cross-lane shuffle between layers.
+//
+// Lane layouts of v_mfma_f32_32x32x16_f16 (64 lanes, lane = 32*g + n):
+//   A (32 x 16): lane holds row n, k-group g, 8 fp16 values (k = 8g + j)
+//   B (16 x 32): lane holds column n, k-group g, 8 fp16 values (k = 8g + j)
+//   D (32 x 32): lane holds column n, rows 8a + 4g + b in register 4a + b
+// Only the A/B symmetry of the k assignment matters for correctness (the sum
+// over k is order free); the D layout fixes which features a lane owns.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlpmk {
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer resource over [base, base + bytes).  Buffer loads past `bytes`
+// return zero and buffer stores past it are dropped by the hardware range
+// check, which is how every kernel handles ragged row tails without branches.
+// 0x00020000 is the gfx9-family word 3 (32-bit data format, no swizzle).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <class T>
+__device__ __forceinline__ T buf_load16(rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+template <class T>
+__device__ __forceinline__ void buf_store16(T v, rsrc_t r, uint32_t byte_off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, (int)byte_off, 0, 0);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+
+constexpr int kMaxLayers = 8;
+
+__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Output-feature permutation of an MFMA row block.  Row i = 8a + 4g + b of
+// block mb computes feature outfeat(mb, i).  With it, D registers 0..7 of lane
+// (n, g) hold features 32mb + 8g + [0..7] and registers 8..15 hold
+// 32mb + 16 + 8g + [0..7]: i.e. the 8 consecutive features that the B operand
+// of K-step s = 2mb (resp. 2mb+1) wants at lane (n, g) under the k map
+// k(s, g, j) = 16s + 8g + j.  Every layer uses that same k map, which is also
+// the natural one for loading rows of x with one 16-byte load per K-step.
+__host__ __device__ constexpr int outfeat(int mb, int i) {
+  return 32 * mb + 16 * ((i >> 3) >> 1) + 8 * ((i >> 2) & 1) + 4 * ((i >> 3) & 1) + (i & 3);
+}
+
+// Softplus in base-2 units: sp2(u) = log2(1 + 2^u) = max(u, 0) + log2(1 + 2^-|u|).
+// For u = z*log2(e): softplus(z) = ln2 * sp2(u) for every z, and for z > 20 it
+// equals z to fp32 rounding (the 2^-|u| term is below 3e-9), which is the
+// reference's threshold branch (kernel.py:108).  One v_exp_f32 and one
+// v_log_f32 (hardware base-2 transcendentals), no range reduction needed.
+__device__ __forceinline__ float sp2(float u) {
+  float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(u));
+  float l = __builtin_amdgcn_logf(1.0f + e);
+  return __builtin_amdgcn_fmed3f(u, 0.0f, __builtin_inff()) + l;
+}
+
+__device__ __forceinline__ f16x2 cvt2(float a, float b) {
+  return __builtin_convertvector((f32x2){a, b}, f16x2);  // v_cvt_pk_f16_f32 (RNE)
+}
+
+__device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, float a4, float a5,
+                                       float a6, float a7) {
+  f16x2 p0 = cvt2(a0, a1), p1 = cvt2(a2, a3), p2 = cvt2(a4, a5), p3 = cvt2(a6, a7);
+  f16x4 q0 = __builtin_shufflevector(p0, p1, 0, 1, 2, 3);
+  f16x4 q1 = __builtin_shufflevector(p2, p3, 0, 1, 2, 3);
+  return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Compile-time description of a network: widths d[0] (input) .. d[L] (output).
+template <int... Ds>
+struct Net {
+  static constexpr int L = sizeof...(Ds) - 1;
+  static constexpr int d[sizeof...(Ds)] = {Ds...};
+  // K-steps (16 input features each) and 32-row output blocks of layer l.
+  static constexpr int ks(int l) { return d[l] / 16; }
+  static constexpr int mbs(int l) { return (d[l + 1] + 31) / 32; }
+  // First LDS fragment (1 KiB = 64 lanes x 16 B) of layer l.
+  static constexpr int frag_off(int l) {
+    int o = 0;
+    for (int i = 0; i < l; ++i) o += mbs(i) * ks(i);
+    return o;
+  }
+  static constexpr int nfrag() { return frag_off(L); }
+  // Largest K-step count over all layer inputs (register buffer size).
+  static constexpr int ksmax() {
+    int m = 0;
+    for (int i = 0; i < L; ++i) m = ks(i) > m ? ks(i) : m;
+    return m;
+  }
+  static constexpr bool valid() {
+    for (int i = 0; i <= L; ++i)
+      if (d[i] <= 0 || d[i] % 16 != 0) return false;
+    return L >= 2;
+  }
+  static constexpr int64_t weight_elems() {
+    int64_t s = 0;
+    for (int i = 0; i < L; ++i) s += (int64_t)d[i] * d[i + 1];
+    return s;
+  }
+};
+
+}  // namespace mlpmk

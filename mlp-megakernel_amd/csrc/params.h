@@ -1,0 +1,32 @@
+// Kernel parameter blocks shared by the host dispatch and the kernels.
+#pragma once
+#include <stdint.h>
+
+namespace mlpmk {
+
+constexpr int kMaxLayersHost = 8;
+
+struct FwdParams {
+  const _Float16* x;
+  _Float16* out;
+  const _Float16* w[kMaxLayersHost];
+  float* stash[kMaxLayersHost];  // stash[l] = h_{l+1}, fp32 [M, d[l+1]]; unused if no stash
+  int64_t M;
+};
+
+}  // namespace mlpmk
+
+namespace mlpmk {
+
+struct BwdParams {
+  const _Float16* x;
+  const _Float16* w[kMaxLayersHost];
+  const float* stash[kMaxLayersHost];  // stash[l] = h_{l+1}, fp32 [M, d[l+1]]
+  const _Float16* dout;                // dL/dout; row r at dout + r * dout_stride
+  int64_t dout_stride;                 // elements; 0 broadcasts row 0
+  _Float16* dx;                        // nullable
+  float* dw[kMaxLayersHost];           // fp32 [d[l], d[l+1]], accumulated with atomics
+  int64_t M;
+};
+
+}  // namespace mlpmk

@@ -1,0 +1,160 @@
+// Weight-norm kernels (one launch per direction for ALL layers) and the
+// byte-counter calibration copy.
+//
+// Replaces `_wn_fwd_kernel` and `_wn_bwd_from_dw_T_kernel` of the reference's
+// training path (/root/reference/mlp_fused.md:466-486; the code itself is not
+// in the snapshot).  Parameters are contiguous blocks v_all / g_all, layer
+// after layer (mlp_fused.md:478-480).  Each thread owns one output column j of
+// one layer and walks its `in` rows; adjacent threads take adjacent columns, so
+// every row access of a wave is one contiguous segment of the [in, out]
+// row-major matrix (the column-wise read of fp32 dW needs no transposed copy).
+#include "device_common.h"
+#include "host_common.h"
+
+namespace mlpmk {
+
+struct WnLayout {
+  int L;
+  int in[kMaxLayers], out[kMaxLayers];
+  int64_t v_off[kMaxLayers];  // element offset of layer l in v / w / dw
+  int g_off[kMaxLayers];      // element offset of layer l in g / inv_norm
+  int blk_off[kMaxLayers + 1];  // first workgroup of layer l
+};
+
+constexpr int kWnThreads = 64;
+
+template <class P>
+__device__ __forceinline__ float ldp(const P* p, int64_t i) {
+  return (float)p[i];
+}
+
+__device__ __forceinline__ int wn_layer_of(const WnLayout& lay, int blk) {
+  int l = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxLayers; ++i)
+    if (i < lay.L && blk >= lay.blk_off[i]) l = i;
+  return l;
+}
+
+template <class P>
+__global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const P* __restrict__ v,
+                                                            const P* __restrict__ g, f16* __restrict__ w,
+                                                            float* __restrict__ inv_norm) {
+  const int l = wn_layer_of(lay, blockIdx.x);
+  const int j = (blockIdx.x - lay.blk_off[l]) * kWnThreads + threadIdx.x;
+  const int K = lay.in[l], N = lay.out[l];
+  if (j >= N) return;
+  const P* vl = v + lay.v_off[l] + j;
+  float ss = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const float t = ldp(vl, (int64_t)k * N);
+    ss = fmaf(t, t, ss);
+  }
+  const float inv = 1.0f / sqrtf(ss);
+  const float scale = ldp(g + lay.g_off[l], j) * inv;
+  f16* wl = w + lay.v_off[l] + j;
+  for (int k = 0; k < K; ++k) wl[(int64_t)k * N] = (f16)(ldp(vl, (int64_t)k * N) * scale);
+  inv_norm[lay.g_off[l] + j] = inv;
+}
+
+template <class P>
+__global__ __launch_bounds__(kWnThreads) void wn_bwd_kernel(WnLayout lay, const float* __restrict__ dw,
+                                                            const P* __restrict__ v, const P* __restrict__ g,
+                                                            const float* __restrict__ inv_norm,
+                                                            P* __restrict__ dv, P* __restrict__ dg) {
+  const int l = wn_layer_of(lay, blockIdx.x);
+  const int j = (blockIdx.x - lay.blk_off[l]) * kWnThreads + threadIdx.x;
+  const int K = lay.in[l], N = lay.out[l];
+  if (j >= N) return;
+  const int64_t base = lay.v_off[l] + j;
+  const float inv = inv_norm[lay.g_off[l] + j];
+  float dot = 0.0f;  // <dW_j, v_j>
+  for (int k = 0; k < K; ++k) dot = fmaf(dw[base + (int64_t)k * N], ldp(v, base + (int64_t)k * N), dot);
+  const float dgj = dot * inv;  // <dW_j, u_j>, u = v * inv
+  const float gs = ldp(g + lay.g_off[l], j) * inv;
+  for (int k = 0; k < K; ++k) {
+    const int64_t e = base + (int64_t)k * N;
+    dv[e] = (P)(gs * (dw[e] - dgj * ldp(v, e) * inv));
+  }
+  dg[lay.g_off[l] + j] = (P)dgj;
+}
+
+static int wn_layout(int L, const int* dims, WnLayout* lay) {
+  if (L > kMaxLayers) return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "num_layers=%d too large", L);
+  lay->L = L;
+  int64_t vo = 0;
+  int go = 0, bo = 0;
+  for (int l = 0; l < L; ++l) {
+    lay->in[l] = dims[l];
+    lay->out[l] = dims[l + 1];
+    lay->v_off[l] = vo;
+    lay->g_off[l] = go;
+    lay->blk_off[l] = bo;
+    vo += (int64_t)dims[l] * dims[l + 1];
+    go += dims[l + 1];
+    bo += (dims[l + 1] + kWnThreads - 1) / kWnThreads;
+  }
+  lay->blk_off[L] = bo;
+  return MLPMK_OK;
+}
+
+int wn_fwd_dispatch(int L, const int* dims, int dtype, const void* v, const void* g, void* w_out,
+                    float* inv_norm, hipStream_t st) {
+  WnLayout lay;
+  int rc = wn_layout(L, dims, &lay);
+  if (rc) return rc;
+  int cus = 0;
+  if ((rc = current_device_cus(&cus))) return rc;
+  (void)hipGetLastError();
+  if (dtype == MLPMK_DTYPE_F32)
+    hipLaunchKernelGGL(wn_fwd_kernel<float>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay,
+                       (const float*)v, (const float*)g, (f16*)w_out, inv_norm);
+  else
+    hipLaunchKernelGGL(wn_fwd_kernel<f16>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay,
+                       (const f16*)v, (const f16*)g, (f16*)w_out, inv_norm);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MLPMK_OK : hip_fail(e, "wn_fwd kernel launch");
+}
+
+int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const void* v, const void* g,
+                    const float* inv_norm, void* dv, void* dg, hipStream_t st) {
+  WnLayout lay;
+  int rc = wn_layout(L, dims, &lay);
+  if (rc) return rc;
+  int cus = 0;
+  if ((rc = current_device_cus(&cus))) return rc;
+  (void)hipGetLastError();
+  if (dtype == MLPMK_DTYPE_F32)
+    hipLaunchKernelGGL(wn_bwd_kernel<float>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay, dw,
+                       (const float*)v, (const float*)g, inv_norm, (float*)dv, (float*)dg);
+  else
+    hipLaunchKernelGGL(wn_bwd_kernel<f16>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay, dw,
+                       (const f16*)v, (const f16*)g, inv_norm, (f16*)dv, (f16*)dg);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MLPMK_OK : hip_fail(e, "wn_bwd kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// Calibration copy: 16-byte loads/stores, grid-stride, same access width as the
+// megakernels.  Used only to scale FETCH_SIZE / WRITE_SIZE counters.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void copy_kernel(const f32x4* __restrict__ src, f32x4* __restrict__ dst,
+                                                   int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    dst[i] = src[i];
+}
+
+int copy_dispatch(const void* src, void* dst, int64_t bytes, hipStream_t st) {
+  int cus = 0;
+  int rc = current_device_cus(&cus);
+  if (rc) return rc;
+  const int64_t n16 = bytes / 16;
+  int64_t grid = (n16 + 255) / 256;
+  if (grid > (int64_t)cus * 8) grid = (int64_t)cus * 8;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const f32x4*)src, (f32x4*)dst, n16);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MLPMK_OK : hip_fail(e, "copy kernel launch");
+}
+
+}  // namespace mlpmk

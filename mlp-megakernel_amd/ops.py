@@ -1,0 +1,238 @@
+"""Torch-facing launch wrappers over the C ABI of ``libmlpmk.so``.
+
+Tensors only supply device pointers and the stream: every launch goes through
+``include/mlpmk.h`` on the caller's current torch stream of the tensor's
+device.  Validation errors of the library surface as ``MlpmkError``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+class MlpmkError(RuntimeError):
+    """A non-zero ``mlpmk_status`` returned by the library."""
+
+    def __init__(self, fn, status, detail):
+        self.status = status
+        name = _lib.STATUS.get(status, f"status {status}")
+        super().__init__(f"{fn} failed: {name}: {detail}")
+
+
+def library_path():
+    return _lib.LIB_PATH
+
+
+def _check(fn, rc):
+    if rc != 0:
+        lib = _lib.get()
+        detail = lib.mlpmk_last_error().decode(errors="replace")
+        raise MlpmkError(fn, rc, detail)
+
+
+def _dims_of(x, weights):
+    dims = [int(x.shape[1])] + [int(w.shape[1]) for w in weights]
+    for i, w in enumerate(weights):
+        if w.dim() != 2 or int(w.shape[0]) != dims[i]:
+            raise ValueError(
+                f"weight {i} has shape {tuple(w.shape)}; expected [{dims[i]}, out] chained on x {tuple(x.shape)}"
+            )
+    return dims
+
+
+def fwd_supported(dims):
+    lib = _lib.get()
+    p, _keep = _lib.int_array(dims)
+    return bool(lib.mlpmk_fwd_supported(len(dims) - 1, p))
+
+
+def bwd_supported(dims):
+    lib = _lib.get()
+    p, _keep = _lib.int_array(dims)
+    return bool(lib.mlpmk_bwd_supported(len(dims) - 1, p))
+
+
+def _require(t, name, dtype, device):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def fwd_into(x, weights, out, stash=None):
+    """Run the forward megakernel writing ``out`` (and ``stash`` if given).
+
+    ``x`` [M, D] fp16, ``weights`` list of [in, out] fp16, ``out`` [M, OUT]
+    fp16, ``stash`` list of L-1 fp32 [M, H_l] tensors or None.  All contiguous
+    on one CUDA (HIP) device.
+    """
+    dev = x.device
+    if dev.type != "cuda":
+        raise ValueError(f"x must be on a GPU device, got {dev}")
+    _require(x, "x", torch.float16, dev)
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
+    for i, w in enumerate(weights):
+        _require(w, f"w{i + 1}", torch.float16, dev)
+    dims = _dims_of(x, weights)
+    M = int(x.shape[0])
+    _require(out, "out", torch.float16, dev)
+    if tuple(out.shape) != (M, dims[-1]):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {(M, dims[-1])}")
+    stash_ptrs = None
+    if stash is not None:
+        if len(stash) != len(weights) - 1:
+            raise ValueError(f"stash needs {len(weights) - 1} tensors, got {len(stash)}")
+        for i, s in enumerate(stash):
+            _require(s, f"stash[{i}]", torch.float32, dev)
+            if tuple(s.shape) != (M, dims[i + 1]):
+                raise ValueError(f"stash[{i}] has shape {tuple(s.shape)}, expected {(M, dims[i + 1])}")
+        stash_ptrs = [s.data_ptr() for s in stash]
+    lib = _lib.get()
+    pd, _k1 = _lib.int_array(dims)
+    pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
+    ps, _k3 = (_lib.ptr_array(stash_ptrs) if stash_ptrs is not None else (None, None))
+    with torch.cuda.device(dev):
+        rc = lib.mlpmk_fwd(len(weights), pd, x.data_ptr(), pw, out.data_ptr(), ps, M, _stream(dev))
+    _check("mlpmk_fwd", rc)
+    return out
+
+
+def fwd(x, weights, stash=False):
+    """Allocate ``out`` (and the fp32 stash when ``stash``) and run the forward.
+
+    Returns ``out`` or ``(out, [h1, ..., h_{L-1}])``.
+    """
+    dims = _dims_of(x, weights)
+    M = int(x.shape[0])
+    out = torch.empty((M, dims[-1]), device=x.device, dtype=torch.float16)
+    hs = None
+    if stash:
+        hs = [torch.empty((M, d), device=x.device, dtype=torch.float32) for d in dims[1:-1]]
+    fwd_into(x, weights, out, hs)
+    return (out, hs) if stash else out
+
+
+def bwd(x, weights, stash, dout, dws, dx=None):
+    """Backward megakernel: accumulates fp32 weight gradients into ``dws``
+    (callers zero them first) and writes ``dx`` if given.
+
+    ``dout`` is [M, OUT] fp16 with unit column stride; a row stride of 0
+    (``t.expand(M, OUT)`` of one row) is passed through as a broadcast.
+    """
+    dev = x.device
+    _require(x, "x", torch.float16, dev)
+    for i, w in enumerate(weights):
+        _require(w, f"w{i + 1}", torch.float16, dev)
+    dims = _dims_of(x, weights)
+    M = int(x.shape[0])
+    if len(stash) != len(weights) - 1:
+        raise ValueError(f"stash needs {len(weights) - 1} tensors, got {len(stash)}")
+    for i, s in enumerate(stash):
+        _require(s, f"stash[{i}]", torch.float32, dev)
+        if tuple(s.shape) != (M, dims[i + 1]):
+            raise ValueError(f"stash[{i}] has shape {tuple(s.shape)}, expected {(M, dims[i + 1])}")
+    for i, d in enumerate(dws):
+        _require(d, f"dw[{i}]", torch.float32, dev)
+        if tuple(d.shape) != (dims[i], dims[i + 1]):
+            raise ValueError(f"dw[{i}] has shape {tuple(d.shape)}, expected {(dims[i], dims[i + 1])}")
+    if dout.dtype != torch.float16 or dout.device != dev:
+        raise TypeError("dout must be fp16 on the same device as x")
+    if tuple(dout.shape) != (M, dims[-1]) or dout.stride(1) != 1:
+        raise ValueError(f"dout must be [M, OUT]={M, dims[-1]} with unit column stride")
+    row_stride = int(dout.stride(0)) if M > 1 else dims[-1]
+    if dx is not None:
+        _require(dx, "dx", torch.float16, dev)
+        if tuple(dx.shape) != (M, dims[0]):
+            raise ValueError(f"dx has shape {tuple(dx.shape)}, expected {(M, dims[0])}")
+    lib = _lib.get()
+    pd, _k1 = _lib.int_array(dims)
+    pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
+    ps, _k3 = _lib.ptr_array([s.data_ptr() for s in stash])
+    pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
+    with torch.cuda.device(dev):
+        rc = lib.mlpmk_bwd(
+            len(weights), pd, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
+            dx.data_ptr() if dx is not None else None, pg, M, _stream(dev),
+        )
+    _check("mlpmk_bwd", rc)
+    return dws, dx
+
+
+def _param_dtype(t):
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    if t.dtype == torch.float16:
+        return _lib.DTYPE_F16
+    raise TypeError(f"weight-norm parameters must be fp32 or fp16, got {t.dtype}")
+
+
+def wn_fwd(dims, v_all, g_all, w_all, inv_all):
+    """``W = g v / ||v||`` for all layers in one launch (flat contiguous blocks)."""
+    dev = v_all.device
+    dt = _param_dtype(v_all)
+    _require(v_all, "v_all", v_all.dtype, dev)
+    _require(g_all, "g_all", v_all.dtype, dev)
+    _require(w_all, "w_all", torch.float16, dev)
+    _require(inv_all, "inv_all", torch.float32, dev)
+    nw = sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
+    ng = sum(dims[1:])
+    if v_all.numel() != nw or w_all.numel() != nw or g_all.numel() != ng or inv_all.numel() != ng:
+        raise ValueError("weight-norm block sizes do not match dims")
+    lib = _lib.get()
+    pd, _k = _lib.int_array(dims)
+    with torch.cuda.device(dev):
+        rc = lib.mlpmk_wn_fwd(
+            len(dims) - 1, pd, dt, v_all.data_ptr(), g_all.data_ptr(), w_all.data_ptr(),
+            inv_all.data_ptr(), _stream(dev),
+        )
+    _check("mlpmk_wn_fwd", rc)
+    return w_all, inv_all
+
+
+def wn_bwd(dims, dw_all, v_all, g_all, inv_all, dv_all, dg_all):
+    """``dW -> (dv, dg)`` for all layers in one launch."""
+    dev = v_all.device
+    dt = _param_dtype(v_all)
+    _require(dw_all, "dw_all", torch.float32, dev)
+    _require(v_all, "v_all", v_all.dtype, dev)
+    _require(g_all, "g_all", v_all.dtype, dev)
+    _require(inv_all, "inv_all", torch.float32, dev)
+    _require(dv_all, "dv_all", v_all.dtype, dev)
+    _require(dg_all, "dg_all", v_all.dtype, dev)
+    nw = sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
+    ng = sum(dims[1:])
+    if dw_all.numel() != nw or v_all.numel() != nw or dv_all.numel() != nw:
+        raise ValueError("weight-norm block sizes do not match dims")
+    if g_all.numel() != ng or inv_all.numel() != ng or dg_all.numel() != ng:
+        raise ValueError("weight-norm block sizes do not match dims")
+    lib = _lib.get()
+    pd, _k = _lib.int_array(dims)
+    with torch.cuda.device(dev):
+        rc = lib.mlpmk_wn_bwd(
+            len(dims) - 1, pd, dt, dw_all.data_ptr(), v_all.data_ptr(), g_all.data_ptr(),
+            inv_all.data_ptr(), dv_all.data_ptr(), dg_all.data_ptr(), _stream(dev),
+        )
+    _check("mlpmk_wn_bwd", rc)
+    return dv_all, dg_all
+
+
+def copy_bytes(src, dst):
+    """Calibration copy of ``src`` into ``dst`` (same byte size, multiple of 16)."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("copy size mismatch")
+    lib = _lib.get()
+    with torch.cuda.device(src.device):
+        rc = lib.mlpmk_copy(src.data_ptr(), dst.data_ptr(), nbytes, _stream(src.device))
+    _check("mlpmk_copy", rc)
+    return dst

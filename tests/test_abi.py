@@ -1,0 +1,145 @@
+"""The C ABI of libmlpmk.so on the CPU: it loads, exports every symbol that
+include/mlpmk.h declares, and its host-side validation rejects bad arguments
+with the documented status codes before anything touches a device.  No
+compute is launched here (this container has no GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import mlpmk
+from mlpmk import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mlpmk.h")
+
+OK, INVALID, UNSUPPORTED, MISALIGNED, HIPERR, NODEV = 0, 1, 2, 3, 4, 5
+A = 0x10000  # a fake, 16-byte aligned device address (never dereferenced)
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    # function declarations: a return type at the start of a line, then the name
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(mlpmk_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol():
+    lib = _lib.get()
+    names = declared_symbols()
+    assert "mlpmk_fwd" in names and "mlpmk_bwd" in names and "mlpmk_wn_fwd" in names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_version_and_status_strings():
+    lib = _lib.get()
+    assert lib.mlpmk_version() >= 100
+    for code, text in [(0, b"ok"), (2, b"unsupported shape"), (5, b"no usable gfx950 device")]:
+        assert lib.mlpmk_status_string(code) == text
+    assert lib.mlpmk_status_string(99) == b"unknown status"
+
+
+@pytest.mark.parametrize(
+    "dims,ok",
+    [((128, 128, 128, 128), True), ((128,) * 6, True), ((32, 64, 64, 16), True),
+     ((128, 64, 128, 128), False), ((128, 128), False), ((100, 128, 128, 128), False)],
+)
+def test_forward_support_table(dims, ok):
+    assert ops.fwd_supported(list(dims)) is ok
+
+
+def _fwd(dims, x=A, w=(A, A, A), out=A, stash=None, m=256):
+    lib = _lib.get()
+    pd, _k1 = _lib.int_array(dims)
+    pw, _k2 = _lib.ptr_array(list(w))
+    ps, _k3 = (_lib.ptr_array(list(stash)) if stash is not None else (None, None))
+    return lib.mlpmk_fwd(len(dims) - 1, pd, x, pw, out, ps, m, None)
+
+
+def test_fwd_validation_codes():
+    lib = _lib.get()
+    d = [128, 128, 128, 128]
+    assert _fwd(d, m=-1) == INVALID
+    assert _fwd([128, 64, 128, 128]) == UNSUPPORTED
+    assert _fwd([128, 128]) == UNSUPPORTED  # one layer
+    assert _fwd(d, x=A + 2) == MISALIGNED
+    assert _fwd(d, out=None) == INVALID
+    assert _fwd(d, w=(A, A + 8, A)) == MISALIGNED
+    assert _fwd(d, stash=(A, None)) == INVALID
+    assert b"stash[1]" in lib.mlpmk_last_error()
+    assert lib.mlpmk_fwd(3, None, A, None, A, None, 1, None) == INVALID
+    # M == 0 succeeds without touching a device (x/out may even be NULL)
+    assert _fwd(d, x=None, out=None, m=0) == OK
+    # valid arguments reach the device query, which fails without a GPU
+    if not torch.cuda.is_available():
+        assert _fwd(d) in (NODEV, HIPERR)
+        assert lib.mlpmk_last_error() != b""
+
+
+def test_bwd_validation_codes():
+    lib = _lib.get()
+    d = [128, 128, 128, 128]
+    pd, _k1 = _lib.int_array(d)
+    pw, _k2 = _lib.ptr_array([A, A, A])
+    ps, _k3 = _lib.ptr_array([A, A])
+    pg, _k4 = _lib.ptr_array([A, A, A])
+    call = lambda **kw: lib.mlpmk_bwd(  # noqa: E731
+        3, pd, kw.get("x", A), pw, kw.get("stash", ps), kw.get("dout", A), kw.get("stride", 128),
+        kw.get("dx", None), kw.get("dw", pg), kw.get("m", 256), None)
+    assert call(m=-1) == INVALID
+    assert call(stride=-1) == INVALID
+    assert call(dw=None) == INVALID
+    if ops.bwd_supported(d):
+        assert call(stride=64) == INVALID  # below the output width
+        assert call(stride=130) == MISALIGNED
+        assert call(dout=A + 4) == MISALIGNED
+        assert call(m=0) == OK
+    else:
+        assert call() == UNSUPPORTED
+
+
+def test_wn_and_copy_validation_codes():
+    lib = _lib.get()
+    pd, _k = _lib.int_array([128, 128, 128, 128])
+    assert lib.mlpmk_wn_fwd(3, pd, 7, A, A, A, A, None) == INVALID  # bad dtype
+    assert lib.mlpmk_wn_fwd(3, pd, 0, A, None, A, A, None) == INVALID
+    assert lib.mlpmk_wn_bwd(3, pd, 1, A, A, A, A, A + 2, A, None) == MISALIGNED
+    pbad, _k2 = _lib.int_array([128, 100, 128, 128])
+    assert lib.mlpmk_wn_fwd(3, pbad, 0, A, A, A, A, None) == UNSUPPORTED
+    assert lib.mlpmk_copy(A, A, 17, None) == INVALID
+    assert lib.mlpmk_copy(A, A, 0, None) == OK
+
+
+def test_python_wrappers_validate_before_the_library():
+    x = torch.zeros((4, 128), dtype=torch.float16)
+    ws = [torch.zeros((128, 128), dtype=torch.float16) for _ in range(3)]
+    out = torch.empty((4, 128), dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.fwd_into(x, ws, out)
+    with pytest.raises(ValueError, match="weight 1"):
+        ops._dims_of(x, [ws[0], torch.zeros((64, 128), dtype=torch.float16), ws[2]])
+
+
+def test_drop_in_modules_import_without_gpu():
+    import kernel
+
+    assert kernel._pick_config(4096, 128, 128, 128, 128) == (64, 128, 16, 16, 16, 8)
+    with pytest.raises(TypeError):
+        kernel._pick_config(4096, 128, 128, 128, 128, fp32=True)
+    assert callable(kernel._fused_mlp_fwd) and kernel.Model and kernel.ModelNew
+
+
+def test_model_reference_matches_oracle_on_cpu():
+    # kernel.Model is the eager reference (kernel.py:163-171); on the CPU in
+    # fp32 it must agree with the oracle.
+    import numpy as np
+
+    import kernel
+    from oracle import mlp_oracle as orc
+
+    x, ws = orc.make_inputs((128, 128, 128, 128), 64, seed=0)
+    got = kernel.Model()(*[torch.from_numpy(a.astype(np.float32)) for a in [x] + ws]).numpy()
+    np.testing.assert_allclose(got, orc.forward(x, ws), rtol=1e-4, atol=1e-5)

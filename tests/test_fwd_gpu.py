@@ -1,0 +1,162 @@
+"""Forward megakernel parity on the GPU: HIP path (through the C ABI) vs the
+CPU oracle on the same seeded inputs.
+
+Tolerance: fp16 outputs within atol = rtol = 1e-2 of the fp32 CPU evaluation
+(the reference's own gate, /root/reference/profile.py:92, and BASELINE.json's
+north_star).  Large M is checked on a random sample of rows (rows are
+independent) plus exact row-permutation equivariance.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mlp_oracle as orc
+import mlpmk
+from mlpmk import ops
+
+pytestmark = pytest.mark.gpu
+
+ATOL = RTOL = 1e-2
+
+
+def _to_dev(x, ws):
+    return torch.from_numpy(x).cuda(), [torch.from_numpy(w).cuda() for w in ws]
+
+
+def _check(out, ref, what):
+    ok, err, excess = orc.allclose_report(out, ref, ATOL, RTOL)
+    assert ok, f"{what}: max|err|={err:.4g}, worst excess over atol+rtol*|ref| = {excess:.4g}"
+    return err
+
+
+def test_library_is_the_native_one():
+    assert ops.library_path().endswith("libmlpmk.so")
+    lib = mlpmk._lib.get()
+    assert lib.mlpmk_version() >= 100
+
+
+@pytest.mark.parametrize("m", [256, 64, 128, 512, 1024, 2048, 4096])
+def test_3l128_latency_sweep_sizes(m):
+    x, ws = orc.make_inputs((128, 128, 128, 128), m, seed=0)
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    _check(out, orc.forward(x, ws), f"3L-128 M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 31, 63, 65, 255, 257, 1000, 4097])
+def test_3l128_ragged_tails(m):
+    x, ws = orc.make_inputs((128, 128, 128, 128), m, seed=m)
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    _check(out, orc.forward(x, ws), f"3L-128 M={m}")
+
+
+def test_3l128_matches_fp16_rounding_variant_tightly():
+    # Against the oracle that rounds hidden activations to fp16 like the
+    # reference megakernel (kernel.py:110,117) the error is a few fp16 ulps.
+    x, ws = orc.make_inputs((128, 128, 128, 128), 4096, seed=3)
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    ref = orc.forward(x, ws, round_hidden=True)
+    ok, err, _ = orc.allclose_report(out, ref, 4e-3, 4e-3)
+    assert ok, err
+
+
+def test_m0_is_noop():
+    x = torch.empty((0, 128), dtype=torch.float16, device="cuda")
+    ws = [torch.randn(128, 128, device="cuda").half() for _ in range(3)]
+    out = ops.fwd(x, ws)
+    assert out.shape == (0, 128)
+
+
+def test_5l128_forward():
+    x, ws = orc.make_inputs((128,) * 6, 65536, seed=0)
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    _check(out, orc.forward(x, ws), "5L-128 M=65536")
+
+
+@pytest.mark.parametrize("m", [64, 1000, 65536])
+def test_narrow_forward(m):
+    x, ws = orc.make_inputs((32, 64, 64, 16), m, seed=0, x_dist="uniform")
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    _check(out, orc.forward(x, ws), f"narrow M={m}")
+
+
+def _device_inputs(dims, m, seed, uniform=False):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    if uniform:
+        x = (torch.rand((m, dims[0]), generator=g, device="cuda") * 2 - 1).half()
+    else:
+        x = torch.randn((m, dims[0]), generator=g, device="cuda").half()
+    ws = [
+        (torch.randn((dims[i], dims[i + 1]), generator=g, device="cuda") / dims[i] ** 0.5).half()
+        for i in range(len(dims) - 1)
+    ]
+    return x, ws
+
+
+@pytest.mark.parametrize(
+    "dims,m,uniform",
+    [
+        ((128, 128, 128, 128), 1048576, False),
+        ((128,) * 6, 1048576, False),
+        ((32, 64, 64, 16), 4194304, True),
+    ],
+)
+def test_full_size_sampled_rows_and_permutation(dims, m, uniform):
+    x, ws = _device_inputs(dims, m, seed=0, uniform=uniform)
+    out = ops.fwd(x, ws)
+    # 1) 4096 random rows against the oracle
+    idx = torch.randperm(m, device="cuda")[:4096]
+    xs = x[idx].cpu().numpy()
+    wn = [w.cpu().numpy() for w in ws]
+    _check(out[idx].float().cpu().numpy(), orc.forward(xs, wn), f"{dims} M={m} sampled")
+    # 2) row independence: a permuted input gives the permuted output, bit for bit
+    perm = torch.randperm(m, device="cuda")
+    out_p = ops.fwd(x[perm].contiguous(), ws)
+    assert torch.equal(out_p, out[perm])
+    # 3) the last rows (tail of the persistent walk) are right too
+    xs = x[-300:].cpu().numpy()
+    _check(out[-300:].float().cpu().numpy(), orc.forward(xs, wn), f"{dims} M={m} last rows")
+
+
+def test_stash_matches_hidden_activations():
+    x, ws = orc.make_inputs((128, 128, 128, 128), 3000, seed=5)
+    xd, wd = _to_dev(x, ws)
+    out, hs = ops.fwd(xd, wd, stash=True)
+    ref, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    _check(out.float().cpu().numpy(), ref, "stash-mode out")
+    for i, (h, rh) in enumerate(zip(hs, ref_h)):
+        ok, err, _ = orc.allclose_report(h.cpu().numpy(), rh, 2e-3, 2e-3)
+        assert ok, f"h{i + 1}: {err}"
+    out2 = ops.fwd(xd, wd)
+    assert torch.equal(out, out2)
+
+
+def test_threshold_edges_through_identity_weights():
+    # W1 = W2 = I makes out = softplus(softplus(x)) @ W3; with W3 = I the
+    # output is the activation itself on chosen pre-activations, including the
+    # threshold neighbourhood of kernel.py:108.
+    z = np.array([-100, -20, -5, -1, 0, 0.5, 1, 5, 19.99, 20, 20.01, 30, 60], dtype=np.float32)
+    x = np.zeros((64, 128), dtype=np.float16)
+    x[:, : z.size] = z.astype(np.float16)
+    eye = np.eye(128, dtype=np.float16)
+    xd, wd = _to_dev(x, [eye, eye, eye])
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    ref = orc.forward(x, [eye, eye, eye])
+    _check(out, ref, "identity-weight softplus(softplus(z))")
+    assert abs(out[0, 4] - np.log(3.0)) < 2e-3  # z = 0: softplus(softplus(0)) = log(1 + 2)
+
+
+def test_zero_first_layer_closed_form():
+    x, ws = orc.make_inputs((128, 128, 128, 128), 512, seed=1)
+    ws[0] = np.zeros_like(ws[0])
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    w2 = ws[1].astype(np.float64)
+    w3 = ws[2].astype(np.float64)
+    h2 = np.log1p(np.exp(np.log(2.0) * w2.sum(axis=0)))
+    row = h2 @ w3
+    _check(out, np.broadcast_to(row, out.shape), "W1 = 0 closed form")
