@@ -55,6 +55,19 @@ def make_device_inputs(torch, dims, m, seed, uniform):
     return x, ws
 
 
+def ramp_clock(torch, fn, seconds=0.4):
+    """Untimed back-to-back launches for `seconds`: the GPU starts a process at
+    a low shader clock (about 1 GHz measured with s_memtime/s_memrealtime) and
+    needs a few hundred ms of load to reach its sustained clock."""
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def time_launches(torch, fn, steps, warmup):
     """Average ms per launch over `steps` back-to-back launches, bracketed by
     HIP events on the launch stream (torch's current stream)."""
@@ -164,12 +177,16 @@ def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
 
 
 def load_traffic(workload):
+    """HBM bytes per launch of the workload's kernel, from the calibrated
+    rocprofv3 FETCH_SIZE + WRITE_SIZE runs recorded in profiles/traffic.json
+    (None when that workload has not been profiled)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(workload)
+            entry = json.load(f).get(workload)
     except (OSError, ValueError):
         return None
+    return entry.get("bytes") if isinstance(entry, dict) else None
 
 
 def main():
@@ -227,6 +244,7 @@ def main():
     )
 
     # --- timed region -------------------------------------------------------
+    ramp_clock(torch, step)
     ms = time_launches(torch, step, args.steps, args.warmup)
     nbytes, nflops = algorithmic(dims, m)
     achieved_gbs = nbytes / (ms * 1e-3) / 1e9

@@ -74,7 +74,11 @@ __host__ __device__ constexpr int outfeat(int mb, int i) {
 __device__ __forceinline__ float sp2(float u) {
   float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(u));
   float l = __builtin_amdgcn_logf(1.0f + e);
-  return __builtin_amdgcn_fmed3f(u, 0.0f, __builtin_inff()) + l;
+  // med3 with a finite upper bound stays one v_med3_f32; an infinite bound is
+  // rewritten to max(), which IEEE mode precedes with a canonicalising v_max
+  // of the MFMA result (one extra VALU op per element).  The two differ only
+  // for u = +inf, where FLT_MAX still rounds to fp16 +inf.
+  return __builtin_amdgcn_fmed3f(u, 0.0f, 3.40282347e38f) + l;
 }
 
 __device__ __forceinline__ f16x2 cvt2(float a, float b) {

@@ -16,10 +16,14 @@
 //    the next layer's B operand (see device_common.h).  No intermediate goes to
 //    LDS or HBM unless the training stash is requested.
 //  * x rows are read with 16-byte loads, out rows written with 16-byte stores.
-//  * Activations run in base-2 units: layer 0's accumulator is scaled by log2(e),
-//    hidden layers then chain with no scaling at all (ln2 and log2e cancel
-//    between W^T h' and the next exp2), and the last accumulator is scaled by
-//    ln2.  The stash stores natural-unit h = ln2 * h'.
+//  * Activations run in base-2 units: W_1 is staged pre-scaled by log2(e) and
+//    W_L by ln(2), hidden layers chain with no scaling at all (ln2 and log2e
+//    cancel between W^T h' and the next exp2), so the epilogue is exp2, add,
+//    log2, max, add and a pack per element.  The stash stores natural-unit
+//    h = ln2 * h'.
+//  * Each layer is software-pipelined by 32-feature output block: the MFMA
+//    chain of block mb+1 is issued ahead of block mb's activation, so the
+//    matrix core and the VALU work concurrently within one wave.
 #include "device_common.h"
 #include "params.h"
 
@@ -34,6 +38,16 @@ namespace mlpmk {
 // layer's output width).  Consecutive threads take consecutive lanes of one
 // fragment, so for each j the 32 gathers of a half-wave fall in one 64-byte
 // segment of a W row.
+// Scale folded into the staged copy of W_l: log2(e) on layer 0 (its
+// accumulator is then directly in base-2 units), ln(2) on the last layer
+// (which converts base-2 activations back); hidden layers need none because
+// ln 2 and log2 e cancel between consecutive layers.  The product is rounded
+// to fp16 once, a relative change below 2^-11 per weight.
+template <class N>
+__device__ __forceinline__ float wscale(int l) {
+  return (l == 0 ? kLog2e : 1.0f) * (l == N::L - 1 ? kLn2 : 1.0f);
+}
+
 template <class N, int NT>
 __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
 #pragma unroll
@@ -51,7 +65,7 @@ __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
       if (of < Nout) {
         const f16* src = w + (int64_t)(16 * s + 8 * g) * Nout + of;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = src[(int64_t)j * Nout];
+        for (int j = 0; j < 8; ++j) v[j] = (f16)((float)src[(int64_t)j * Nout] * wscale<N>(l));
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = (f16)0.0f;
@@ -67,6 +81,50 @@ __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
 struct BlockIO {
   rsrc_t x, out;
   rsrc_t stash[kMaxLayers];
+  i32x4* stage;  // this wave's LDS staging tile for the output rows (STAGE only)
+};
+
+// Output staging: whether the last layer's rows go through an LDS tile per
+// wave so that they leave as whole 128-byte cache lines.  A lane of the MFMA
+// result layout holds one row, so direct stores write 32 bytes into each of
+// 32 rows per instruction and complete a row's lines piecemeal, which costs
+// HBM write efficiency once rows are wider than 64 bytes.  The tile holds two
+// 32-feature output blocks (128 bytes per row); it is flushed after every
+// second block.  Needs output rows of a multiple of 64 features and LDS room
+// next to the staged weights.
+template <class N, int NB, int NW>
+struct OutStage {
+  static constexpr int kRowChunks = 8;  // 16-byte chunks per staged row segment
+  static constexpr int kTileChunks = 32 * NB * kRowChunks;
+  static constexpr bool enabled =
+      N::d[N::L] % 64 == 0 && N::nfrag() * 1024 + NW * kTileChunks * 16 + 16 <= 163840;
+  static constexpr int bytes = enabled ? NW * kTileChunks * 16 : 0;
+};
+
+// Whether the workgroup's waves claim row blocks from an LDS counter (needs
+// 16 bytes of LDS next to the weights and the staging tiles).
+template <class N, int NB, int NW>
+struct Claim {
+  static constexpr bool enabled = N::nfrag() * 1024 + OutStage<N, NB, NW>::bytes + 16 <= 163840;
+};
+
+// LDS chunk slot of (row, chunk): the chunk index is XORed with the row so that
+// the 16-byte writes of 8 consecutive rows (one per lane) and the reads of one
+// row's chunks both fall on distinct banks.
+__device__ __forceinline__ int stage_slot(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+// The workgroup's claim counter in LDS; the specialisation without one
+// allocates nothing.
+template <bool E>
+struct ClaimSlot {
+  __device__ static unsigned int* get() {
+    __shared__ unsigned int ctr;
+    return &ctr;
+  }
+};
+template <>
+struct ClaimSlot<false> {
+  __device__ static unsigned int* get() { return nullptr; }
 };
 
 template <class N, bool STASH, int ROWS>
@@ -84,130 +142,261 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
   return io;
 }
 
+// Rows of x as raw dwords: kept as i32x4 until the MFMA reads them, because an
+// f16x8 destination makes the compiler re-pack the halves right after the load
+// (v_bfi copies), which waits for the load at the point of issue.
 template <int KS, int NB>
-__device__ __forceinline__ void load_rows(f16x8 (&xa)[KS][NB], rsrc_t xr, int n, int g) {
+__device__ __forceinline__ void load_rows(i32x4 (&xa)[KS][NB], rsrc_t xr, int n, int g) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      xa[s][nb] = buf_load16<f16x8>(xr, (uint32_t)(((nb * 32 + n) * (KS * 16) + 16 * s + 8 * g) * 2));
+      xa[s][nb] = __builtin_amdgcn_raw_buffer_load_b128(
+          xr, (int)(((nb * 32 + n) * (KS * 16) + 16 * s + 8 * g) * 2), 0, 0);
 }
 
-// One layer l over NB batch blocks.  `in` holds the B operands of the layer's
-// KS input K-steps; hidden layers write the next layer's B operands to `nxt`,
-// the last layer stores fp16 rows of `out`.
-template <class N, int l, int NB, bool STASH, int KSM>
-__device__ __forceinline__ void run_layer(const BlockIO& io, const f16x8* __restrict__ lds,
-                                          const f16x8 (&in)[KSM][NB], f16x8 (&nxt)[KSM][NB], int lane) {
-  constexpr int KS = N::ks(l);
-  constexpr int MB = N::mbs(l);
+__device__ __forceinline__ f16x8 as_f16x8(f16x8 v) { return v; }
+__device__ __forceinline__ f16x8 as_f16x8(i32x4 v) { return __builtin_bit_cast(f16x8, v); }
+
+// An opaque copy of a wave-uniform offset.  Weight fragments never change
+// after staging, so without this the compiler would hoist every fragment read
+// out of the persistent row loop (and spill); routing the LDS address through
+// a volatile asm statement pins each block's reads inside the loop while
+// leaving the scheduler free to interleave everything else.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("; opaque %0" : "+v"(v));
+  return v;
+}
+
+// MFMA chain of output block mb of layer l: acc[nb] = W_l[:, block mb]^T . in.
+template <int KS, int NB, class T, int KIN>
+__device__ __forceinline__ void mma_block(f32x16 (&acc)[NB], const f16x8* __restrict__ frag,
+                                          const T (&in)[KIN][NB]) {
+  f16x8 a[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) a[s] = frag[s * 64];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x16){};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16(a[s], as_f16x8(in[s][nb]), acc[nb]);
+}
+
+// Activation and hand-off of output block mb: hidden layers apply softplus
+// (base-2 units), optionally store the fp32 stash, and pack the next layer's
+// B operands; the last layer stores fp16 rows of `out`.
+template <class N, int l, int NB, bool STASH, bool STAGE, int KSM>
+__device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[NB], int mb,
+                                         f16x8 (&nxt)[KSM][NB], int lane) {
   constexpr int Nout = N::d[l + 1];
   constexpr bool LAST = (l == N::L - 1);
   const int n = lane & 31, g = lane >> 5;
-  const f16x8* frag = lds + N::frag_off(l) * 64 + lane;
+  // Registers 0..7 -> features 32mb + 8g + [0..7]; 8..15 -> 32mb + 16 + 8g + [0..7].
+  const bool lo_ok = (32 * mb + 16 <= Nout);  // folded after unrolling
+  const bool hi_ok = (32 * mb + 32 <= Nout);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const uint32_t elem = (uint32_t)((nb * 32 + n) * Nout + 32 * mb + 8 * g);
+    if constexpr (LAST && STAGE) {
+      const f32x16& v = acc[nb];  // ln 2 is folded into the staged W_L
+      const int row = nb * 32 + n;
+      const int c = 4 * (mb & 1) + g;  // chunk within the staged 128-byte row segment
+      io.stage[stage_slot(row, c)] =
+          __builtin_bit_cast(i32x4, pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]));
+      io.stage[stage_slot(row, c + 2)] =
+          __builtin_bit_cast(i32x4, pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]));
+    } else if constexpr (LAST) {
+      const f32x16& v = acc[nb];  // ln 2 is folded into the staged W_L
+      if (lo_ok) buf_store16(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
+      if (hi_ok)
+        buf_store16(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
+    } else {
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = sp2(acc[nb][e]);  // log2 e is folded into the staged W_1
+      if constexpr (STASH) {
+        const rsrc_t sr = io.stash[l];
+        float h[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) h[e] = v[e] * kLn2;
+        if (lo_ok) {
+          buf_store16((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
+          buf_store16((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
+        }
+        if (hi_ok) {
+          buf_store16((f32x4){h[8], h[9], h[10], h[11]}, sr, elem * 4 + 64);
+          buf_store16((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
+        }
+      }
+      if (2 * mb < KSM) nxt[2 * mb][nb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+      if (2 * mb + 1 < KSM)
+        nxt[2 * mb + 1][nb] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+    }
+  }
+}
+
+// Stores the staged 128-byte row segments of output features
+// [64 seg, 64 seg + 64) with 16-byte stores, 8 rows x 128 bytes (8 whole cache
+// lines) per instruction.
+template <class N, int NB>
+__device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane) {
+  constexpr int Nout = N::d[N::L];
+  constexpr int TC = OutStage<N, NB, 1>::kTileChunks;
+  // The tile was written by other lanes of this wave; LDS executes one wave's
+  // operations in order, so only the compiler needs a fence here.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int i = 0; i < TC / 64; ++i) {
+    const int q = 64 * i + lane;  // linear 16-byte chunk of the tile
+    const int row = q >> 3, c = q & 7;
+    const i32x4 v = io.stage[stage_slot(row, c)];
+    __builtin_amdgcn_raw_buffer_store_b128(v, io.out, row * Nout * 2 + seg * 128 + c * 16, 0, 0);
+  }
+  // The next writes into the tile must stay behind these reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// One layer l over NB batch blocks, software-pipelined by output block: the
+// MFMA chain of block mb+1 is issued before the epilogue of block mb, so one
+// wave keeps the matrix core busy while its VALU runs the activation.  `in`
+// holds the B operands of the layer's input K-steps; `nxt` receives the next
+// layer's.
+template <class N, int l, int NB, bool STASH, bool STAGE, int KIN, int KSM, class T>
+__device__ __forceinline__ void run_layer(const BlockIO& io, const f16x8* __restrict__ lds,
+                                          const T (&in)[KIN][NB], f16x8 (&nxt)[KSM][NB], int lane) {
+  static_assert(KIN >= N::ks(l), "input K-steps");
+  constexpr int KS = N::ks(l);
+  constexpr int MB = N::mbs(l);
+  const int fbase = (N::frag_off(l) * 64 + lane) * 16;  // byte offset of this lane's fragments
+  const char* lds_b = reinterpret_cast<const char*>(lds);
+  f32x16 acc[2][NB];
+  mma_block<KS, NB>(acc[0], reinterpret_cast<const f16x8*>(lds_b + opaque(fbase)), in);
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    // The weight fragments never change after staging; without this fence the
-    // compiler hoists every ds_read of the layer out of the row loop and spills.
-    asm volatile("" ::: "memory");
-    MLPMK_SCHED_FENCE();
-    f32x16 acc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x16){};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const f16x8 a = frag[(mb * KS + s) * 64];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16(a, in[s][nb], acc[nb]);
-    }
-    // Registers 0..7 -> features 32mb + 8g + [0..7]; 8..15 -> 32mb + 16 + 8g + [0..7].
-    const bool lo_ok = (32 * mb + 16 <= Nout);  // folded after unrolling
-    const bool hi_ok = (32 * mb + 32 <= Nout);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const uint32_t elem = (uint32_t)((nb * 32 + n) * Nout + 32 * mb + 8 * g);
-      float v[16];
-      if constexpr (LAST) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = acc[nb][e] * kLn2;
-        if (lo_ok) buf_store16(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
-        if (hi_ok)
-          buf_store16(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
-      } else {
-        const float scale = (l == 0) ? kLog2e : 1.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = sp2(acc[nb][e] * scale);
-        if constexpr (STASH) {
-          const rsrc_t sr = io.stash[l];
-          if (lo_ok) {
-            buf_store16((f32x4){v[0], v[1], v[2], v[3]} * kLn2, sr, elem * 4);
-            buf_store16((f32x4){v[4], v[5], v[6], v[7]} * kLn2, sr, elem * 4 + 16);
-          }
-          if (hi_ok) {
-            buf_store16((f32x4){v[8], v[9], v[10], v[11]} * kLn2, sr, elem * 4 + 64);
-            buf_store16((f32x4){v[12], v[13], v[14], v[15]} * kLn2, sr, elem * 4 + 80);
-          }
-        }
-        if (2 * mb < KSM) nxt[2 * mb][nb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-        if (2 * mb + 1 < KSM)
-          nxt[2 * mb + 1][nb] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
-      }
+    if (mb + 1 < MB)
+      mma_block<KS, NB>(acc[(mb + 1) & 1],
+                        reinterpret_cast<const f16x8*>(lds_b + opaque(fbase + (mb + 1) * KS * 1024)), in);
+    epilogue<N, l, NB, STASH, STAGE, KSM>(io, acc[mb & 1], mb, nxt, lane);
+    if constexpr (l == N::L - 1 && STAGE) {
+      if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
     }
   }
 }
 
-// Layers l .. L-1, ping-ponging between two register buffers.  The x rows of
-// the wave's next block are requested when the last layer starts (the layer-0
-// buffer is dead by then), so their latency hides behind the last layer.
-template <class N, int l, int NB, bool STASH, int KSM>
+// Layers l .. L-1, ping-ponging between two register buffers.
+template <class N, int l, int NB, bool STASH, bool STAGE, int KSM>
 __device__ __forceinline__ void run_chain(const BlockIO& io, const f16x8* __restrict__ lds,
-                                          f16x8 (&xa)[N::ks(0)][NB], f16x8 (&cur)[KSM][NB],
-                                          f16x8 (&oth)[KSM][NB], rsrc_t next_x, int lane) {
-  if constexpr (l == N::L - 1) {
-    MLPMK_SCHED_FENCE();  // keep the prefetch from being hoisted into layer L-2
-    load_rows<N::ks(0), NB>(xa, next_x, lane & 31, lane >> 5);
-    run_layer<N, l, NB, STASH, KSM>(io, lds, cur, oth, lane);
-  } else {
-    run_layer<N, l, NB, STASH, KSM>(io, lds, cur, oth, lane);
-    run_chain<N, l + 1, NB, STASH, KSM>(io, lds, xa, oth, cur, next_x, lane);
-  }
+                                          f16x8 (&cur)[KSM][NB], f16x8 (&oth)[KSM][NB], int lane) {
+  run_layer<N, l, NB, STASH, STAGE, KSM, KSM>(io, lds, cur, oth, lane);
+  if constexpr (l + 1 < N::L) run_chain<N, l + 1, NB, STASH, STAGE, KSM>(io, lds, oth, cur, lane);
 }
 
-template <class N, int NB, bool STASH, int NW>
+// One row block: layer 0 from the x rows in `xa`, then the refill of `xa` with
+// the rows of block `next` (its latency hides behind layers 1..L-1), then the
+// rest of the chain and the stores.
+template <class N, int NB, bool STASH, bool STAGE, int KSM>
+__device__ __forceinline__ void fwd_block(const FwdParams& p, const f16x8* __restrict__ lds,
+                                          i32x4* stage, int64_t b, int64_t next,
+                                          i32x4 (&xa)[N::ks(0)][NB], f16x8 (&b0)[KSM][NB],
+                                          f16x8 (&b1)[KSM][NB], int lane) {
+  constexpr int KS0 = N::ks(0);
+  constexpr int ROWS = 32 * NB;
+  BlockIO io = block_io<N, STASH, ROWS>(p, b * ROWS);
+  io.stage = stage;
+  run_layer<N, 0, NB, STASH, STAGE, KS0, KSM>(io, lds, xa, b0, lane);
+  MLPMK_SCHED_FENCE();  // the refill must not be hoisted above layer 0
+  // Past the end the resource is empty: the refill then reads zeros.
+  load_rows<KS0, NB>(xa, block_io<N, false, ROWS>(p, next * ROWS).x, lane & 31, lane >> 5);
+  run_chain<N, 1, NB, STASH, STAGE, KSM>(io, lds, b0, b1, lane);
+}
+
+// Persistent forward.  Workgroup b owns row blocks b, b + G, b + 2G, ...
+// (G = grid size, 32*NB rows per block); its waves claim them one at a time
+// from a counter in LDS.  Claiming (rather than a fixed wave-to-block map)
+// matters because the SIMD arbiter favours the older of two waves: with a
+// static split one wave of each pair finishes early and the other runs the
+// tail alone.  The x rows of a wave's next D claimed blocks are in flight in
+// a ring of D register buffers: once layer 0 has consumed a buffer, the
+// wave's next claim is requested into it.
+//
+// The first D blocks are peeled off the loop so that the loop header is
+// entered from two paths with the same outstanding memory operations (ring
+// refills, then stores).  vmcnt counts loads and stores in issue order; with
+// an unpeeled loop the prologue path (loads only) forces the waits for a
+// refilled buffer to also wait for the preceding stores.
+template <class N, int NB, bool STASH, int NW, int D>
 __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   static_assert(N::valid(), "unsupported widths");
+  static_assert(D >= 1 && D <= 4, "prefetch depth");
   constexpr int KSM = N::ksmax();
   constexpr int KS0 = N::ks(0);
   constexpr int ROWS = 32 * NB;
+  constexpr bool STAGE = OutStage<N, NB, NW>::enabled;
+  constexpr int TC = OutStage<N, NB, NW>::kTileChunks;
   __shared__ f16x8 lds[N::nfrag() * 64];
+  __shared__ i32x4 stage_tiles[STAGE ? NW * TC : 1];
+  constexpr bool CLAIM = Claim<N, NB, NW>::enabled;
+  unsigned int* const claim_ctr = ClaimSlot<CLAIM>::get();
+  if constexpr (CLAIM) {
+    if (threadIdx.x == 0) *claim_ctr = 0;
+  }
   stage_weights<N, NW * 64>(p, lds);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  // readfirstlane marks the wave index as wave-uniform, so the block index and
+  // every buffer resource derived from it live in SGPRs (a per-lane resource
+  // would force a readfirstlane/exec waterfall loop around each buffer access).
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nblk = (p.M + ROWS - 1) / ROWS;
-  const int64_t stride = (int64_t)gridDim.x * NW;
-  int64_t blk = (int64_t)blockIdx.x * NW + wid;
-  if (blk >= nblk) return;  // no barrier follows
-
-  f16x8 xa[KS0][NB];
-  f16x8 b0[KSM][NB], b1[KSM][NB];
-  load_rows<KS0, NB>(xa, block_io<N, false, ROWS>(p, blk * ROWS).x, lane & 31, lane >> 5);
-  for (; blk < nblk; blk += stride) {
-    const BlockIO io = block_io<N, STASH, ROWS>(p, blk * ROWS);
-    // Past the end the resource is empty: the prefetch then reads zeros.
-    const rsrc_t next_x = block_io<N, false, ROWS>(p, (blk + stride) * ROWS).x;
-    if constexpr (KS0 == KSM) {
-      run_layer<N, 0, NB, STASH, KSM>(io, lds, xa, b0, lane);
+  const int64_t G = gridDim.x;
+  i32x4* stage = stage_tiles + (STAGE ? wid * TC : 0);
+  // Next block of this workgroup (>= nblk once its share is exhausted).  Without
+  // LDS room for the counter, wave w takes the workgroup's blocks w, w + NW, ...
+  unsigned int seq = (unsigned int)wid;
+  auto claim = [&]() -> int64_t {
+    unsigned int j;
+    if constexpr (CLAIM) {
+      j = 0;
+      if (lane == 0)
+        j = __hip_atomic_fetch_add(claim_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      j = __builtin_amdgcn_readfirstlane(j);
     } else {
-      f16x8 xin[KSM][NB];
-#pragma unroll
-      for (int s = 0; s < KS0; ++s)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) xin[s][nb] = xa[s][nb];
-      run_layer<N, 0, NB, STASH, KSM>(io, lds, xin, b0, lane);
+      j = seq;
+      seq += NW;
     }
-    run_chain<N, 1, NB, STASH, KSM>(io, lds, xa, b0, b1, next_x, lane);
+    return (int64_t)blockIdx.x + (int64_t)j * G;
+  };
+
+  // Past the end a block's resource is empty: its prefetch reads zeros.
+  i32x4 xa[D][KS0][NB];
+  int64_t q[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    q[d] = claim();
+    load_rows<KS0, NB>(xa[d], block_io<N, false, ROWS>(p, q[d] * ROWS).x, lane & 31, lane >> 5);
+  }
+  f16x8 b0[KSM][NB], b1[KSM][NB];
+  // Claims are increasing per wave, so once one is past the end all later are.
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (q[d] >= nblk) return;  // no barrier follows
+    const int64_t nxt = claim();
+    fwd_block<N, NB, STASH, STAGE, KSM>(p, lds, stage, q[d], nxt, xa[d], b0, b1, lane);
+    q[d] = nxt;
+  }
+  for (;;) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (q[d] >= nblk) return;
+      const int64_t nxt = claim();
+      fwd_block<N, NB, STASH, STAGE, KSM>(p, lds, stage, q[d], nxt, xa[d], b0, b1, lane);
+      q[d] = nxt;
+    }
   }
 }
 
@@ -232,7 +421,7 @@ static bool dims_match(int L, const int* dims) {
   return true;
 }
 
-template <class N, int NB, bool STASH, int NW>
+template <class N, int NB, bool STASH, int NW, int D>
 static int launch_fwd(const FwdParams& p, hipStream_t st) {
   constexpr int kMaxDev = 64;
   static int occ_cache[kMaxDev];  // 0 = unknown; benign race (idempotent value)
@@ -242,7 +431,7 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  const void* kern = reinterpret_cast<const void*>(&fwd_kernel<N, NB, STASH, NW>);
+  const void* kern = reinterpret_cast<const void*>(&fwd_kernel<N, NB, STASH, NW, D>);
   int occ = (dev >= 0 && dev < kMaxDev) ? occ_cache[dev] : 0;
   if (occ <= 0) {
     rc = kernel_occupancy(kern, NW * 64, &occ);
@@ -255,15 +444,15 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
   const int64_t cap = (int64_t)cus * occ;
   const int grid = (int)(wgs < cap ? wgs : cap);
   (void)hipGetLastError();
-  hipLaunchKernelGGL((fwd_kernel<N, NB, STASH, NW>), dim3(grid), dim3(NW * 64), 0, st, p);
+  hipLaunchKernelGGL((fwd_kernel<N, NB, STASH, NW, D>), dim3(grid), dim3(NW * 64), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fwd kernel launch");
   return MLPMK_OK;
 }
 
-template <class N, int NB, int NW>
+template <class N, int NB, int NW, int D>
 static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
-  return stash ? launch_fwd<N, NB, true, NW>(p, st) : launch_fwd<N, NB, false, NW>(p, st);
+  return stash ? launch_fwd<N, NB, true, NW, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
 }
 
 bool fwd_supported_dims(int L, const int* dims) {
@@ -272,9 +461,9 @@ bool fwd_supported_dims(int L, const int* dims) {
 }
 
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
-  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 2, 8>(p, stash, st);
-  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 2, 8>(p, stash, st);
-  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 8>(p, stash, st);
+  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 8, 1>(p, stash, st);
+  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 8, 1>(p, stash, st);
+  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 8, 1>(p, stash, st);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
 }
 
