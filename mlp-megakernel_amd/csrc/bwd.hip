@@ -1,14 +1,385 @@
-// Backward megakernel (placeholder until the kernel lands): reports every
-// shape as unsupported so callers fail loudly instead of computing anything.
+// Backward megakernel for gfx950 (MI355X): data gradients and weight
+// gradients of the softplus MLP in one persistent launch.
+//
+// Replaces the fused backward of the reference's FusedMLPSoftplus autograd
+// function (/root/reference/mlp_fused.md:80-112; README.md:30-32 -- the file
+// that held it, fused_mlp.py, is not in the reference snapshot).  Math, with
+// a_0 = x, a_l = h_l = softplus(z_{l-1}) read from the fp32 stash and
+// dz_{L-1} = dL/dout:
+//
+//     dW_l     = a_l^T . dz_l                      (every layer)
+//     dz_{l-1} = (dz_l . W_l^T) * (1 - exp(-h_l))  (l >= 1; sigmoid(z) = 1 - exp(-h))
+//     dx       = dz_0 . W_0^T                      (optional)
+//
+// Machine mapping (one workgroup of NW waves, R = 32*NW rows per round):
+//
+//  * dgrad runs in registers exactly like the forward chain, in the
+//    transposed orientation (MFMA M = features of a_l, N = 32 rows, K =
+//    features of dz_l): W_l is staged once per workgroup into LDS as A
+//    fragments (16 contiguous bytes of a W_l row per lane), dz_l is the B
+//    operand, and the fp32 accumulator times (1 - exp(-h_l)), packed to fp16,
+//    is directly the next layer's B operand.
+//  * wgrad reduces over rows, so it needs rows in the MFMA K dimension while
+//    the dgrad layout holds one row per lane.  Every layer, each wave writes
+//    its rows of a_l and dz_l (fp16) into LDS exchange tiles laid out
+//    [feature][row]; after a workgroup barrier each wave reads 16-byte A/B
+//    fragments (8 rows of one feature per lane) for the 32x32 tiles of dW_l
+//    it owns and accumulates them over all R rows -- the split-K partial sums
+//    of the R rows are reduced in the MFMA accumulators across the waves'
+//    contributions through LDS.
+//  * The owned dW tiles stay in registers (AGPRs) across all rounds of the
+//    workgroup; at the end each wave adds them to the fp32 dW in global memory
+//    with hardware float atomics (one add per element per workgroup).
+//
+// The exchange tiles are XOR-swizzled, element (f, r) at f*R + (r ^ 8*(f & 15)):
+// the 2-byte writes of one half-wave (32 consecutive rows of one feature) hit
+// one 64-byte window, the two half-waves (features f and f+8) land 128 bytes
+// apart, and the 16-byte fragment reads of 16 lanes (16 consecutive features,
+// same 8 rows) fall on 16 distinct chunks -- all bank-conflict free.
 #include "device_common.h"
 #include "host_common.h"
 #include "params.h"
 
 namespace mlpmk {
 
-bool bwd_supported_dims(int, const int*) { return false; }
+template <class N, int NW, bool DX>
+struct BwdGeom {
+  static constexpr int L = N::L;
+  static constexpr int R = 32 * NW;  // rows per round
+  static constexpr bool has_dgrad(int l) { return l >= 1 || DX; }
+  // dgrad of layer l: 32-feature output blocks over d[l], K-steps over d[l+1].
+  static constexpr int dmb(int l) { return N::d[l] / 32; }
+  static constexpr int dks(int l) { return N::d[l + 1] / 16; }
+  static constexpr int dfrag_off(int l) {
+    int o = 0;
+    for (int i = 0; i < l; ++i)
+      if (has_dgrad(i)) o += dmb(i) * dks(i);
+    return o;
+  }
+  static constexpr int ndfrag() { return dfrag_off(L); }
+  // wgrad: 32x32 tiles of dW_l, dealt round-robin to the waves.
+  static constexpr int wib(int l) { return (N::d[l] + 31) / 32; }
+  static constexpr int wob(int l) { return (N::d[l + 1] + 31) / 32; }
+  static constexpr int tiles(int l) { return wib(l) * wob(l); }
+  static constexpr int tpw(int l) { return (tiles(l) + NW - 1) / NW; }
+  static constexpr int tpw_off(int l) {
+    int o = 0;
+    for (int i = 0; i < l; ++i) o += tpw(i);
+    return o;
+  }
+  static constexpr int ntpw() { return tpw_off(L); }
+  // Exchange tiles hold up to this many features (multiples of 32).
+  static constexpr int fa() {
+    int m = 0;
+    for (int i = 0; i < L; ++i) m = 32 * wib(i) > m ? 32 * wib(i) : m;
+    return m;
+  }
+  static constexpr int fz() {
+    int m = 0;
+    for (int i = 0; i < L; ++i) m = 32 * wob(i) > m ? 32 * wob(i) : m;
+    return m;
+  }
+  static constexpr int ksmax() {
+    int m = 0;
+    for (int i = 0; i <= L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
+    return m;
+  }
+  static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
+  static constexpr bool valid() {
+    for (int i = 1; i < L; ++i)
+      if (N::d[i] % 32 != 0) return false;  // hidden widths in whole 32-feature blocks
+    if (DX && N::d[0] % 32 != 0) return false;
+    return N::valid() && R >= 128 && lds_bytes() <= 163840;
+  }
+};
 
-int bwd_dispatch(int, const int*, const BwdParams&, hipStream_t) {
+// Swizzled slot of element (feature f, row r) in an exchange tile of R rows.
+template <int R>
+__device__ __forceinline__ int xslot(int f, int r) {
+  return f * R + (r ^ ((8 * (f & 15)) & (R - 1)));
+}
+
+// Stages the dgrad A fragments: fragment (mb, s) of layer l, lane (i, g) holds
+// W_l[outfeat(mb, i)][16s + 8g + j], j = 0..7 -- one 16-byte load per lane.
+template <class N, class Gm, int NT>
+__device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* lds) {
+#pragma unroll
+  for (int l = 0; l < N::L; ++l) {
+    if (!Gm::has_dgrad(l)) continue;
+    const int Nout = N::d[l + 1];
+    const int KS = Gm::dks(l);
+    const int items = Gm::dmb(l) * KS * 64;
+    const f16* __restrict__ w = p.w[l];
+    for (int item = threadIdx.x; item < items; item += NT) {
+      const int f = item >> 6, lane = item & 63;
+      const int mb = f / KS, s = f % KS;
+      const int i = lane & 31, g = lane >> 5;
+      const int row = outfeat(mb, i);
+      lds[(Gm::dfrag_off(l) + f) * 64 + lane] =
+          *reinterpret_cast<const f16x8*>(w + (int64_t)row * Nout + 16 * s + 8 * g);
+    }
+  }
+}
+
+// Writes this lane's 8 consecutive features (16s + 8g + j) of row r into an
+// exchange tile.
+template <int R>
+__device__ __forceinline__ void xwrite(f16* t, int s, int g, int r, f16x8 v) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t[xslot<R>(16 * s + 8 * g + j, r)] = v[j];
+}
+
+// 16-byte exchange-tile fragment: rows 16kk + 8g .. +7 of feature f.
+template <int R>
+__device__ __forceinline__ f16x8 xread(const f16* t, int f, int kk, int g) {
+  return *reinterpret_cast<const f16x8*>(t + xslot<R>(f, 16 * kk + 8 * g));
+}
+
+template <class N, int NW, bool DX>
+struct BwdWave {
+  using Gm = BwdGeom<N, NW, DX>;
+  static constexpr int L = N::L;
+  static constexpr int R = Gm::R;
+  static constexpr int KSM = Gm::ksmax();
+
+  const BwdParams& p;
+  const f16x8* wfr;  // staged dgrad fragments
+  f16* ta;           // exchange tile: a_l, [feature][row]
+  f16* tz;           // exchange tile: dz_l, [feature][row]
+  int lane, n, g, wid;
+  int64_t row0;    // first row of this wave's 32 in the current round
+  uint32_t nrows;  // rows of those 32 that exist (0..32)
+  f32x16 (&wacc)[Gm::ntpw()];
+
+  // Resource over this wave's rows of a row-major [M, width] tensor with
+  // `elem` bytes per element; loads past the valid rows read zeros and
+  // stores there are dropped.
+  __device__ __forceinline__ rsrc_t rows_rsrc(const void* base, int width, int elem) const {
+    return make_rsrc(static_cast<const char*>(base) + row0 * width * elem, nrows * width * elem);
+  }
+
+  // dL/dout rows as B operands (dz_{L-1}).  Row stride 0 broadcasts row 0.
+  __device__ __forceinline__ void load_dout(f16x8 (&dz)[KSM]) const {
+    constexpr int W = N::d[L];
+    const int64_t st = p.dout_stride;
+    const uint32_t bytes = nrows ? (uint32_t)(((int64_t)(nrows - 1) * st + W) * 2) : 0u;
+    const rsrc_t r = make_rsrc(p.dout + row0 * st, bytes);
+#pragma unroll
+    for (int s = 0; s < W / 16; ++s)
+      dz[s] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + 16 * s + 8 * g) * 2), 0, 0));
+  }
+
+  // Wgrad of layer l over the R rows in the exchange tiles, for this wave's
+  // tiles.  K-steps (16 rows) outermost keeps only one step's fragments live.
+  template <int l>
+  __device__ __forceinline__ void wgrad() {
+    constexpr int WOB = Gm::wob(l);
+    constexpr int T = Gm::tpw(l);
+#pragma unroll
+    for (int kk = 0; kk < R / 16; ++kk) {
+#pragma unroll
+      for (int k = 0; k < T; ++k) {
+        const int t = wid + k * NW;
+        if (t < Gm::tiles(l)) {
+          const int fi = 32 * (t / WOB) + (lane & 31), fo = 32 * (t % WOB) + (lane & 31);
+          wacc[Gm::tpw_off(l) + k] =
+              mfma32x32x16(xread<R>(ta, fi, kk, g), xread<R>(tz, fo, kk, g), wacc[Gm::tpw_off(l) + k]);
+        }
+      }
+    }
+  }
+
+  // One layer of the backward for this wave's 32 rows: publish a_l and dz_l
+  // to the exchange tiles, run dgrad into dz_{l-1} (or dx), then the wgrad
+  // of dW_l once every wave has published.
+  template <int l>
+  __device__ __forceinline__ void layer(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
+    constexpr int KSA = N::d[l] / 16;      // K-steps of a_l
+    constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
+    const int r = wid * 32 + n;            // row within the round
+#pragma unroll
+    for (int s = 0; s < KSZ; ++s) xwrite<R>(tz, s, g, r, dz[s]);
+    if constexpr (l == 0) {
+      const rsrc_t xr = rows_rsrc(p.x, N::d[0], 2);
+#pragma unroll
+      for (int s = 0; s < KSA; ++s)
+        xwrite<R>(ta, s, g, r,
+                  __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                xr, (int)((n * N::d[0] + 16 * s + 8 * g) * 2), 0, 0)));
+    }
+
+    if constexpr (l >= 1 || Gm::has_dgrad(l)) {
+      constexpr int MB = N::d[l] / 32;
+      const int fbase = (Gm::dfrag_off(l) * 64 + lane) * 16;
+      const char* wb = reinterpret_cast<const char*>(wfr);
+      const rsrc_t hr = rows_rsrc(l >= 1 ? static_cast<const void*>(p.stash[l >= 1 ? l - 1 : 0]) : p.x, N::d[l], 4);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        // h_l = stash[l-1] (fp32) at features 32mb + [0, 32): K-steps 2mb, 2mb+1.
+        float h[2][8];
+        if constexpr (l >= 1) {
+#pragma unroll
+          for (int hs = 0; hs < 2; ++hs) {
+            const int s = 2 * mb + hs;
+            const int off = (n * N::d[l] + 16 * s + 8 * g) * 4;
+            const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0));
+            const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, 0));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              h[hs][j] = lo[j];
+              h[hs][4 + j] = hi[j];
+            }
+            xwrite<R>(ta, s, g, r,
+                      pack8(h[hs][0], h[hs][1], h[hs][2], h[hs][3], h[hs][4], h[hs][5], h[hs][6], h[hs][7]));
+          }
+        }
+        if constexpr (Gm::has_dgrad(l)) {
+          const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSZ * 1024));
+          f32x16 acc = {};
+#pragma unroll
+          for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16(frag[s * 64], dz[s], acc);
+          // Registers 0..7: features 32mb + 8g + [0..7] (K-step 2mb of a_l);
+          // 8..15: 32mb + 16 + 8g + [0..7] (K-step 2mb + 1).
+          if constexpr (l >= 1) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-h[0][j] * kLog2e));
+              v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-h[1][j] * kLog2e));
+            }
+            dzn[2 * mb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+            dzn[2 * mb + 1] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+          } else {
+            const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2);
+            const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
+            buf_store16(pack8(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
+            buf_store16(pack8(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
+                        e * 2 + 32);
+          }
+        }
+      }
+    }
+    __syncthreads();  // every wave's rows are in the exchange tiles
+    wgrad<l>();
+    __syncthreads();  // the tiles are free for the next layer
+  }
+
+  template <int l>
+  __device__ __forceinline__ void layers_from(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
+    layer<l>(dz, dzn);
+    if constexpr (l > 0) layers_from<l - 1>(dzn, dz);
+  }
+
+  // Adds the owned tiles of every dW_l to global memory (fp32 atomics).
+  template <int l>
+  __device__ __forceinline__ void flush() {
+    constexpr int WOB = Gm::wob(l);
+    constexpr int K = N::d[l], NO = N::d[l + 1];
+#pragma unroll
+    for (int k = 0; k < Gm::tpw(l); ++k) {
+      const int t = wid + k * NW;
+      if (t < Gm::tiles(l)) {
+        const int fo = 32 * (t % WOB) + (lane & 31);
+        const f32x16 acc = wacc[Gm::tpw_off(l) + k];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          // C layout: lane (o, g) holds rows 8a + 4g + b of its column, register 4a + b.
+          const int fi = 32 * (t / WOB) + 8 * (e >> 2) + 4 * g + (e & 3);
+          if (fi < K && fo < NO) unsafeAtomicAdd(p.dw[l] + (int64_t)fi * NO + fo, acc[e]);
+        }
+      }
+    }
+    if constexpr (l + 1 < L) flush<l + 1>();
+  }
+};
+
+template <class N, int NW, bool DX>
+__global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
+  using Gm = BwdGeom<N, NW, DX>;
+  static_assert(Gm::valid(), "unsupported backward shape");
+  constexpr int R = Gm::R;
+  constexpr int KSM = Gm::ksmax();
+  __shared__ f16x8 wfr[Gm::ndfrag() * 64];
+  __shared__ f16 ta[Gm::fa() * R];
+  __shared__ f16 tz[Gm::fz() * R];
+  stage_dgrad_weights<N, Gm, NW * 64>(p, wfr);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  f32x16 wacc[Gm::ntpw()];
+#pragma unroll
+  for (int k = 0; k < Gm::ntpw(); ++k) wacc[k] = (f32x16){};
+  BwdWave<N, NW, DX> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, 0, wacc};
+
+  const int64_t nrounds = (p.M + R - 1) / R;
+  // Every wave of a workgroup runs the same rounds (the barriers need all of them).
+  for (int64_t rd = blockIdx.x; rd < nrounds; rd += gridDim.x) {
+    wv.row0 = rd * R + wid * 32;
+    const int64_t left = p.M - wv.row0;
+    wv.nrows = (uint32_t)(left < 32 ? (left > 0 ? left : 0) : 32);
+    f16x8 dz[KSM], dzn[KSM];
+    wv.load_dout(dz);
+    wv.template layers_from<N::L - 1>(dz, dzn);
+  }
+  wv.template flush<0>();
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+
+typedef Net<128, 128, 128, 128> BNet3L128;
+typedef Net<32, 64, 64, 16> BNetNarrow;
+
+template <class N>
+static bool bdims_match(int L, const int* dims) {
+  if (L != N::L) return false;
+  for (int i = 0; i <= L; ++i)
+    if (dims[i] != N::d[i]) return false;
+  return true;
+}
+
+template <class N, int NW, bool DX>
+static int launch_bwd(const BwdParams& p, hipStream_t st) {
+  constexpr int kMaxDev = 64;
+  static int occ_cache[kMaxDev];  // 0 = unknown; benign race (idempotent value)
+  int cus = 0;
+  int rc = current_device_cus(&cus);
+  if (rc != MLPMK_OK) return rc;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  const void* kern = reinterpret_cast<const void*>(&bwd_kernel<N, NW, DX>);
+  int occ = (dev >= 0 && dev < kMaxDev) ? occ_cache[dev] : 0;
+  if (occ <= 0) {
+    rc = kernel_occupancy(kern, NW * 64, &occ);
+    if (rc != MLPMK_OK) return rc;
+    if (dev >= 0 && dev < kMaxDev) occ_cache[dev] = occ;
+  }
+  const int64_t nrounds = (p.M + 32 * NW - 1) / (32 * NW);
+  const int64_t cap = (int64_t)cus * occ;
+  const int grid = (int)(nrounds < cap ? nrounds : cap);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL((bwd_kernel<N, NW, DX>), dim3(grid), dim3(NW * 64), 0, st, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bwd kernel launch");
+  return MLPMK_OK;
+}
+
+template <class N, int NW>
+static int launch_bwd_any(const BwdParams& p, hipStream_t st) {
+  return p.dx ? launch_bwd<N, NW, true>(p, st) : launch_bwd<N, NW, false>(p, st);
+}
+
+bool bwd_supported_dims(int L, const int* dims) {
+  return bdims_match<BNet3L128>(L, dims) || bdims_match<BNetNarrow>(L, dims);
+}
+
+int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st) {
+  if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<BNet3L128, 4>(p, st);
+  if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<BNetNarrow, 4>(p, st);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
 }
 

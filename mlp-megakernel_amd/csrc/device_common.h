@@ -93,6 +93,16 @@ __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, f
   return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// An opaque copy of a wave-uniform offset.  Weight fragments never change
+// after staging, so without this the compiler would hoist every fragment read
+// out of a persistent row loop (and spill); routing the LDS address through
+// a volatile asm statement pins each block's reads inside the loop while
+// leaving the scheduler free to interleave everything else.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("; opaque %0" : "+v"(v));
+  return v;
+}
+
 // Compile-time description of a network: widths d[0] (input) .. d[L] (output).
 template <int... Ds>
 struct Net {

@@ -158,16 +158,6 @@ __device__ __forceinline__ void load_rows(i32x4 (&xa)[KS][NB], rsrc_t xr, int n,
 __device__ __forceinline__ f16x8 as_f16x8(f16x8 v) { return v; }
 __device__ __forceinline__ f16x8 as_f16x8(i32x4 v) { return __builtin_bit_cast(f16x8, v); }
 
-// An opaque copy of a wave-uniform offset.  Weight fragments never change
-// after staging, so without this the compiler would hoist every fragment read
-// out of the persistent row loop (and spill); routing the LDS address through
-// a volatile asm statement pins each block's reads inside the loop while
-// leaving the scheduler free to interleave everything else.
-__device__ __forceinline__ int opaque(int v) {
-  asm volatile("; opaque %0" : "+v"(v));
-  return v;
-}
-
 // MFMA chain of output block mb of layer l: acc[nb] = W_l[:, block mb]^T . in.
 template <int KS, int NB, class T, int KIN>
 __device__ __forceinline__ void mma_block(f32x16 (&acc)[NB], const f16x8* __restrict__ frag,

@@ -1,0 +1,133 @@
+"""Backward megakernel parity on the GPU: HIP path (through the C ABI) vs the
+CPU oracle's closed-form backward on the same seeded inputs.
+
+The GPU forward writes the fp32 activation stash; the oracle backward is fed
+the oracle's own hidden activations (fp32, computed from fp16-rounded layer
+inputs exactly as the megakernel does), so the check covers the stash too.
+
+Tolerances: fp32 weight gradients within rtol 2e-2.
+A pure relative test fails on entries that are near zero by cancellation, so
+each entry must satisfy |got - ref| <= 2e-2 * |ref| + 2e-3 * max|ref| (the
+atol scaled by the gradient's own magnitude), and the relative Frobenius
+error must stay below 1e-2.  fp16 dx within atol = rtol = 1e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mlp_oracle as orc
+from mlpmk import ops
+
+pytestmark = pytest.mark.gpu
+
+D3 = (128, 128, 128, 128)
+NARROW = (32, 64, 64, 16)
+
+
+def check_dw(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max()
+    bound = 2e-2 * np.abs(ref) + 2e-3 * scale
+    worst = np.max(np.abs(got - ref) - bound)
+    frob = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert worst <= 0 and frob < 1e-2, f"{what}: worst excess {worst:.3g} (scale {scale:.3g}), rel frob {frob:.3g}"
+    return frob
+
+
+def run_train(dims, m, seed, *, dout_mode="ones", with_dx=True, x_dist="normal"):
+    x, ws = orc.make_inputs(dims, m, seed=seed, x_dist=x_dist)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    out, hs = ops.fwd(xd, wd, stash=True)
+    rng = np.random.default_rng(seed + 17)
+    if dout_mode == "ones":
+        dout_np = np.ones((m, dims[-1]), np.float16)
+        dout = torch.ones((1, dims[-1]), dtype=torch.float16, device="cuda").expand(m, dims[-1])
+    elif dout_mode == "row":
+        row = rng.standard_normal(dims[-1]).astype(np.float16)
+        dout_np = np.broadcast_to(row, (m, dims[-1]))
+        dout = torch.from_numpy(row).cuda().reshape(1, -1).expand(m, dims[-1])
+    else:
+        dout_np = rng.standard_normal((m, dims[-1])).astype(np.float16)
+        dout = torch.from_numpy(dout_np).cuda()
+    dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(len(dims) - 1)]
+    dx = torch.empty_like(xd) if with_dx else None
+    ops.bwd(xd, wd, hs, dout, dws, dx)
+    torch.cuda.synchronize()
+    _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    rdws, rdx = orc.backward(x, ws, ref_h, dout_np.astype(np.float32), need_dx=with_dx)
+    return out, hs, dws, dx, rdws, rdx
+
+
+@pytest.mark.parametrize("m", [64, 256, 4096, 16384])
+def test_3l128_weight_and_data_gradients(m):
+    _, _, dws, dx, rdws, rdx = run_train(D3, m, seed=m)
+    for i in range(3):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")
+    ok, err, excess = orc.allclose_report(dx.float().cpu().numpy(), rdx, 1e-2, 1e-2)
+    assert ok, f"dx M={m}: max err {err:.3g}, excess {excess:.3g}"
+
+
+@pytest.mark.parametrize("m", [1, 31, 33, 129, 1000, 4097])
+def test_3l128_ragged_rows_without_dx(m):
+    # Rows past M must contribute nothing (their loads read zeros).
+    _, _, dws, dx, rdws, _ = run_train(D3, m, seed=3 * m + 1, dout_mode="full", with_dx=False)
+    assert dx is None
+    for i in range(3):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")
+
+
+@pytest.mark.parametrize("mode", ["row", "full"])
+def test_3l128_dout_layouts(mode):
+    # Broadcast rows (stride 0, the expanded grad of loss = out.sum()) and a
+    # dense dout give the same results as the oracle.
+    _, _, dws, dx, rdws, rdx = run_train(D3, 3000, seed=11, dout_mode=mode)
+    for i in range(3):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} {mode}")
+    ok, err, _ = orc.allclose_report(dx.float().cpu().numpy(), rdx, 1e-2, 1e-2)
+    assert ok, err
+
+
+def test_3l128_training_config_m131072():
+    # Training config at its largest M: the full gradients against the oracle.
+    _, _, dws, _, rdws, _ = run_train(D3, 131072, seed=5, with_dx=False)
+    for i in range(3):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M=131072")
+
+
+def test_weight_gradients_accumulate():
+    # dw is accumulated into (+=): a second call on the same buffers doubles it.
+    x, ws = orc.make_inputs(D3, 2048, seed=9)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dout = torch.ones((1, 128), dtype=torch.float16, device="cuda").expand(2048, 128)
+    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+    ops.bwd(xd, wd, hs, dout, dws)
+    once = [d.clone() for d in dws]
+    ops.bwd(xd, wd, hs, dout, dws)
+    for a, b in zip(once, dws):
+        torch.testing.assert_close(b, 2 * a, rtol=1e-5, atol=1e-5 * float(a.abs().max()))
+
+
+@pytest.mark.parametrize("m", [64, 1000, 65536])
+def test_narrow_gradients(m):
+    _, _, dws, dx, rdws, rdx = run_train(NARROW, m, seed=m + 2, x_dist="uniform", dout_mode="full")
+    for i in range(3):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"narrow dW{i + 1} M={m}")
+    ok, err, _ = orc.allclose_report(dx.float().cpu().numpy(), rdx, 1e-2, 1e-2)
+    assert ok, err
+
+
+def test_zero_dout_gives_zero_gradients():
+    x, ws = orc.make_inputs(D3, 512, seed=1)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dout = torch.zeros((512, 128), dtype=torch.float16, device="cuda")
+    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+    dx = torch.full_like(xd, 7.0)
+    ops.bwd(xd, wd, hs, dout, dws, dx)
+    assert all(float(d.abs().max()) == 0.0 for d in dws)
+    assert float(dx.abs().max()) == 0.0
