@@ -1,0 +1,134 @@
+"""``torch.autograd.Function`` wrappers of the megakernels.
+
+Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
+(/root/reference/README.md:18,24-34,58-70; /root/reference/mlp_fused.md:52-61,
+80-112,159-172,461-486 -- ``fused_mlp.py`` itself is not in the snapshot):
+
+* forward: one forward-megakernel launch that also writes the fp32 activation
+  stash (``mlpmk_fwd`` with ``stash``); with weight norm, one weight-norm launch
+  for all layers first (``mlpmk_wn_fwd``).
+* backward: one backward-megakernel launch (``mlpmk_bwd``) producing every fp32
+  weight gradient (and ``dx`` when ``x`` needs it); with weight norm, one more
+  launch turning all ``dW`` into ``dv, dg`` (``mlpmk_wn_bwd``).
+* AMP: ``custom_fwd(device_type="cuda", cast_inputs=torch.float16)`` and
+  ``custom_bwd`` as mlp_fused.md:168-172 describes.
+
+Every launch goes through ``libmlpmk.so``; there is no PyTorch fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+def _as_row_broadcast(dout):
+    """``dout`` with unit column stride, keeping a broadcast row (stride 0)
+    as a broadcast: ``loss = out.sum()`` hands back a fully expanded scalar
+    (strides (0, 0)); that becomes one materialised row expanded over M."""
+    if dout.dim() == 2 and dout.stride(1) == 1:
+        return dout
+    m, n = dout.shape
+    if dout.stride(0) == 0:
+        return dout[:1].contiguous().expand(m, n)
+    return dout.contiguous()
+
+
+class FusedMLPFunction(torch.autograd.Function):
+    """``out = softplus(... softplus(x @ W1) ...) @ WL`` with the fused backward.
+
+    Inputs: ``x`` [M, D] fp16 and L weights [in, out] fp16 (cast to fp16 under
+    autocast).  Returns fp16 ``out`` [M, OUT].
+    """
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float16)
+    def forward(ctx, x, *weights):
+        x = x.contiguous()
+        weights = [w.contiguous() for w in weights]
+        if any(ctx.needs_input_grad):
+            out, hs = ops.fwd(x, weights, stash=True)
+            ctx.save_for_backward(x, *weights, *hs)
+            ctx.n_layers = len(weights)
+        else:
+            out = ops.fwd(x, weights)
+        return out
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dout):
+        L = ctx.n_layers
+        saved = ctx.saved_tensors
+        x, weights, hs = saved[0], list(saved[1 : 1 + L]), list(saved[1 + L :])
+        dout = _as_row_broadcast(dout.to(torch.float16))
+        dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
+        dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        ops.bwd(x, weights, hs, dout, dws, dx)
+        return (dx, *[d if need else None for d, need in zip(dws, ctx.needs_input_grad[1:])])
+
+
+class FusedMLPWNFunction(torch.autograd.Function):
+    """Weight-normalised MLP: ``W_l[:, j] = g_l[j] v_l[:, j] / ||v_l[:, j]||``
+    for every layer from the contiguous blocks ``v_all`` / ``g_all``
+    (mlp_fused.md:478-480), then the fused MLP.
+
+    Launches: forward = weight norm (all layers) + forward megakernel;
+    backward = backward megakernel + weight-norm backward (all layers).
+    """
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float16)
+    def forward(ctx, x, v_all, g_all, dims):
+        x = x.contiguous()
+        dims = tuple(int(d) for d in dims)
+        L = len(dims) - 1
+        dev = x.device
+        nw = sum(dims[i] * dims[i + 1] for i in range(L))
+        w_all = torch.empty(nw, dtype=torch.float16, device=dev)
+        inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=dev)
+        ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
+        weights = _split(w_all, dims)
+        if any(ctx.needs_input_grad):
+            out, hs = ops.fwd(x, weights, stash=True)
+            ctx.save_for_backward(x, v_all, g_all, w_all, inv_all, *hs)
+            ctx.dims = dims
+        else:
+            out = ops.fwd(x, weights)
+        return out
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dout):
+        dims = ctx.dims
+        x, v_all, g_all, w_all, inv_all, *hs = ctx.saved_tensors
+        weights = _split(w_all, dims)
+        dout = _as_row_broadcast(dout.to(torch.float16))
+        dw_all = torch.zeros(w_all.numel(), dtype=torch.float32, device=x.device)
+        dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        ops.bwd(x, weights, hs, dout, _split(dw_all, dims), dx)
+        dv = dg = None
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            dv = torch.empty_like(v_all)
+            dg = torch.empty_like(g_all)
+            ops.wn_bwd(dims, dw_all, v_all.contiguous(), g_all.contiguous(), inv_all, dv, dg)
+        return dx, dv, dg, None
+
+
+def _split(flat, dims):
+    """Views of the per-layer [in, out] blocks of a flat parameter block."""
+    out, off = [], 0
+    for i in range(len(dims) - 1):
+        n = dims[i] * dims[i + 1]
+        out.append(flat[off : off + n].view(dims[i], dims[i + 1]))
+        off += n
+    return out
+
+
+def fused_mlp(x, *weights):
+    """Functional form of :class:`FusedMLPFunction`."""
+    return FusedMLPFunction.apply(x, *weights)
+
+
+def fused_mlp_wn(x, v_all, g_all, dims):
+    """Functional form of :class:`FusedMLPWNFunction`."""
+    return FusedMLPWNFunction.apply(x, v_all, g_all, tuple(dims))

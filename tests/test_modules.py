@@ -1,0 +1,70 @@
+"""Host-side plumbing of the drop-in modules (no GPU needed): parameter
+layout and initialisation, state_dict round trip, weight-norm views, the
+broadcast handling of ``loss = out.sum()`` gradients, and that the product
+path refuses CPU tensors instead of computing anything on the CPU."""
+import math
+
+import pytest
+import torch
+
+import fused_mlp
+import fused_mlp5
+import kernel
+from mlpmk.autograd import _as_row_broadcast, _split
+
+
+def test_parameter_layout_and_init():
+    torch.manual_seed(0)
+    m = fused_mlp.FusedMLPSoftplus(D=32, H=64, out_features=16)
+    assert m.dims == (32, 64, 64, 16)
+    shapes = [tuple(p.shape) for p in m.parameters()]
+    assert shapes == [(32, 64), (64, 64), (64, 16)]  # [in, out], as kernel.py:105,109,113 index W
+    big = fused_mlp.FusedMLPSoftplus()
+    for p, fan_in in zip(big.weights, (128, 128, 128)):
+        assert abs(float(p.std()) - 1 / math.sqrt(fan_in)) < 0.01
+    assert fused_mlp5.FusedMLP5Softplus().dims == (128,) * 6
+
+
+def test_state_dict_round_trip():
+    a = fused_mlp.FusedMLPSoftplusWN()
+    b = fused_mlp.FusedMLPSoftplusWN()
+    b.load_state_dict(a.state_dict())
+    assert set(a.state_dict()) == {"v_all", "g_all"}
+    assert torch.equal(a.v_all, b.v_all) and torch.equal(a.g_all, b.g_all)
+
+
+def test_weight_norm_blocks_are_contiguous_views():
+    m = fused_mlp.FusedMLPSoftplusWN(D=32, H=64, out_features=16)
+    assert m.v_all.numel() == 32 * 64 + 64 * 64 + 64 * 16
+    assert m.g_all.numel() == 64 + 64 + 16
+    assert torch.all(m.g_all == 1)
+    v1 = m.v(1)
+    assert v1.shape == (64, 64) and v1.data_ptr() == m.v_all.data_ptr() + 32 * 64 * 4
+    assert m.g(2).shape == (16,) and m.g(2).data_ptr() == m.g_all.data_ptr() + 128 * 4
+    flat = torch.arange(10.0)
+    parts = _split(flat, (1, 2, 4))
+    assert [tuple(p.shape) for p in parts] == [(1, 2), (2, 4)] and parts[1][1, 3] == 9
+
+
+def test_sum_gradient_becomes_one_broadcast_row():
+    g = torch.ones((), dtype=torch.float16).expand(5, 7)  # what out.sum() hands back
+    assert g.stride() == (0, 0)
+    r = _as_row_broadcast(g)
+    assert r.shape == (5, 7) and r.stride() == (0, 1) and torch.all(r == 1)
+    row = torch.randn(1, 7).half().expand(5, 7)
+    assert _as_row_broadcast(row).stride() == (0, 1)
+    dense = torch.randn(7, 5).half().t()
+    assert _as_row_broadcast(dense).is_contiguous()
+
+
+def test_product_path_refuses_cpu_tensors():
+    m = fused_mlp.FusedMLPSoftplus().half()
+    with pytest.raises(ValueError, match="GPU"):
+        m(torch.randn(4, 128).half())
+    x = torch.randn(4, 128).half()
+    ws = [torch.randn(128, 128).half() for _ in range(3)]
+    with pytest.raises(ValueError, match="GPU"):
+        kernel._fused_mlp_fwd(x, *ws)
+    # The eager reference model of kernel.py stays available and runs anywhere.
+    ref = kernel.Model()(x.float(), *[w.float() for w in ws])
+    assert ref.shape == (4, 128)
