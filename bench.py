@@ -176,6 +176,37 @@ def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
     return {"value": rows / el, "unit": "rows/s", "threads": torch.get_num_threads(), "sample": f"{reps} x {chunk} rows fp32"}
 
 
+TRAIN_BYTES_PER_ROW = 3072  # x 256 + out 256 + stash 1024 written; g 256 + stash 1024 + x 256 read
+TRAIN_FLOP_PER_ROW = 262144  # fwd 98,304 + dgrad 2 x 32,768 + wgrad 3 x 32,768 (no dx)
+
+
+def train_step_bench(torch, m, steps=50, warmup=10):
+    """One training step of BASELINE config 5 through the drop-in module:
+    weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
+    megakernel + weight-norm backward, x without grad.  Timed with HIP events
+    around `steps` back-to-back autograd steps (Python dispatch included)."""
+    import fused_mlp
+
+    torch.manual_seed(0)
+    model = fused_mlp.FusedMLPSoftplusWN().cuda()
+    x = torch.randn(m, 128, device="cuda").half()
+
+    def step(_):
+        model.v_all.grad = None
+        model.g_all.grad = None
+        model(x).sum().backward()
+
+    ramp_clock(torch, step, seconds=0.2)
+    ms = time_launches(torch, step, steps, warmup)
+    return {
+        "ms_per_step": round(ms, 5),
+        "rows_per_s": m / (ms * 1e-3),
+        "achieved_gbs": round(TRAIN_BYTES_PER_ROW * m / (ms * 1e-3) / 1e9, 1),
+        "tflops": round(TRAIN_FLOP_PER_ROW * m / (ms * 1e-3) / 1e12, 2),
+        "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd",
+    }
+
+
 def load_traffic(workload):
     """HBM bytes per launch of the workload's kernel, from the calibrated
     rocprofv3 FETCH_SIZE + WRITE_SIZE runs recorded in profiles/traffic.json
@@ -197,6 +228,8 @@ def main():
     ap.add_argument("--config", choices=sorted(CONFIG_DIMS), default="3l128")
     ap.add_argument("--m", type=int, default=None)
     ap.add_argument("--sweep", action="store_true", help="add the M=64..4096 latency sweep")
+    ap.add_argument("--train", action="store_true",
+                    help="add the training step (3L + weight norm, loss = out.sum()) at M = 4096, 16384, 131072")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     args = ap.parse_args()
@@ -301,6 +334,9 @@ def main():
             gr = time_graph(torch, lambda i: ops.fwd_into(xx, ww, oo))
             sweep[str(ms_m)] = {"event_ms": round(ev, 5), "graph_ms": round(gr, 5)}
         result["latency_sweep"] = sweep
+
+    if args.train:
+        result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(orc, dims, uniform, budget_s=args.cpu_budget)

@@ -57,11 +57,17 @@ struct BwdGeom {
     return o;
   }
   static constexpr int ndfrag() { return dfrag_off(L); }
-  // wgrad: 32x32 tiles of dW_l, dealt round-robin to the waves.
+  // wgrad: 32x32 tiles of dW_l.  When 2x2 blocks of tiles divide evenly
+  // among the waves, each wave owns whole blocks (2 A + 2 B fragment reads
+  // feed 4 MFMAs); otherwise single tiles are dealt round-robin.
   static constexpr int wib(int l) { return (N::d[l] + 31) / 32; }
   static constexpr int wob(int l) { return (N::d[l + 1] + 31) / 32; }
   static constexpr int tiles(int l) { return wib(l) * wob(l); }
-  static constexpr int tpw(int l) { return (tiles(l) + NW - 1) / NW; }
+  static constexpr int quads(int l) { return (wib(l) / 2) * (wob(l) / 2); }
+  static constexpr bool quad(int l) {
+    return wib(l) % 2 == 0 && wob(l) % 2 == 0 && quads(l) % NW == 0;
+  }
+  static constexpr int tpw(int l) { return quad(l) ? 4 * (quads(l) / NW) : (tiles(l) + NW - 1) / NW; }
   static constexpr int tpw_off(int l) {
     int o = 0;
     for (int i = 0; i < l; ++i) o += tpw(i);
@@ -84,6 +90,11 @@ struct BwdGeom {
     for (int i = 0; i <= L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
     return m;
   }
+  static constexpr int kshid() {  // K-steps of the widest hidden activation
+    int m = 1;
+    for (int i = 1; i < L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
+    return m;
+  }
   static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
   static constexpr bool valid() {
     for (int i = 1; i < L; ++i)
@@ -92,12 +103,6 @@ struct BwdGeom {
     return N::valid() && R >= 128 && lds_bytes() <= 163840;
   }
 };
-
-// Swizzled slot of element (feature f, row r) in an exchange tile of R rows.
-template <int R>
-__device__ __forceinline__ int xslot(int f, int r) {
-  return f * R + (r ^ ((8 * (f & 15)) & (R - 1)));
-}
 
 // Stages the dgrad A fragments: fragment (mb, s) of layer l, lane (i, g) holds
 // W_l[outfeat(mb, i)][16s + 8g + j], j = 0..7 -- one 16-byte load per lane.
@@ -121,26 +126,15 @@ __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* l
   }
 }
 
-// Writes this lane's 8 consecutive features (16s + 8g + j) of row r into an
-// exchange tile.
-template <int R>
-__device__ __forceinline__ void xwrite(f16* t, int s, int g, int r, f16x8 v) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) t[xslot<R>(16 * s + 8 * g + j, r)] = v[j];
-}
-
-// 16-byte exchange-tile fragment: rows 16kk + 8g .. +7 of feature f.
-template <int R>
-__device__ __forceinline__ f16x8 xread(const f16* t, int f, int kk, int g) {
-  return *reinterpret_cast<const f16x8*>(t + xslot<R>(f, 16 * kk + 8 * g));
-}
-
 template <class N, int NW, bool DX>
 struct BwdWave {
   using Gm = BwdGeom<N, NW, DX>;
   static constexpr int L = N::L;
   static constexpr int R = Gm::R;
   static constexpr int KSM = Gm::ksmax();
+  static constexpr int KSH = Gm::kshid();
+  static constexpr int KS0 = N::d[0] / 16;
+  static constexpr int KSL = N::d[L] / 16;
 
   const BwdParams& p;
   const f16x8* wfr;  // staged dgrad fragments
@@ -148,146 +142,218 @@ struct BwdWave {
   f16* tz;           // exchange tile: dz_l, [feature][row]
   int lane, n, g, wid;
   int64_t row0;    // first row of this wave's 32 in the current round
-  uint32_t nrows;  // rows of those 32 that exist (0..32)
+  int64_t rstep;   // rows between a workgroup's consecutive rounds
+  int wo[8];       // exchange-tile write slots of this lane's row, feature 8g + j
+  int rd;          // exchange-tile read column of fragment row 0 (XOR 16kk for step kk)
   f32x16 (&wacc)[Gm::ntpw()];
 
-  // Resource over this wave's rows of a row-major [M, width] tensor with
-  // `elem` bytes per element; loads past the valid rows read zeros and
-  // stores there are dropped.
-  __device__ __forceinline__ rsrc_t rows_rsrc(const void* base, int width, int elem) const {
-    return make_rsrc(static_cast<const char*>(base) + row0 * width * elem, nrows * width * elem);
+  // Prefetched rows (issued one phase ahead of their use).
+  f16x8 gbuf[KSL];     // dL/dout of the round = dz_{L-1}
+  float hbuf[KSH][8];  // h_l of the next phase, fp32
+  f16x8 xbuf[KS0];     // x rows
+
+  __device__ __forceinline__ void init_slots() {
+    const int r = wid * 32 + n;  // row within the round
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wo[j] = (8 * g + j) * R + (r ^ ((64 * g + 8 * j) & (R - 1)));
+    rd = (8 * g) ^ ((8 * (lane & 15)) & (R - 1));
   }
 
-  // dL/dout rows as B operands (dz_{L-1}).  Row stride 0 broadcasts row 0.
-  __device__ __forceinline__ void load_dout(f16x8 (&dz)[KSM]) const {
-    constexpr int W = N::d[L];
+  __device__ __forceinline__ uint32_t nrows_at(int64_t r0) const {
+    const int64_t left = p.M - r0;
+    return (uint32_t)(left < 32 ? (left > 0 ? left : 0) : 32);
+  }
+  // Resource over this wave's 32 rows from r0 of a row-major [M, width] tensor;
+  // loads past the valid rows read zeros and stores there are dropped.
+  __device__ __forceinline__ rsrc_t rows_rsrc(const void* base, int width, int elem, int64_t r0) const {
+    return make_rsrc(static_cast<const char*>(base) + r0 * width * elem, nrows_at(r0) * width * elem);
+  }
+
+  // dL/dout rows from r0 as B operands.  Row stride 0 broadcasts row 0.
+  __device__ __forceinline__ void load_dout(int64_t r0) {
     const int64_t st = p.dout_stride;
-    const uint32_t bytes = nrows ? (uint32_t)(((int64_t)(nrows - 1) * st + W) * 2) : 0u;
-    const rsrc_t r = make_rsrc(p.dout + row0 * st, bytes);
+    const uint32_t nr = nrows_at(r0);
+    const uint32_t bytes = nr ? (uint32_t)(((int64_t)(nr - 1) * st + N::d[L]) * 2) : 0u;
+    const rsrc_t r = make_rsrc(p.dout + r0 * st, bytes);
 #pragma unroll
-    for (int s = 0; s < W / 16; ++s)
-      dz[s] = __builtin_bit_cast(
+    for (int s = 0; s < KSL; ++s)
+      gbuf[s] = __builtin_bit_cast(
           f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + 16 * s + 8 * g) * 2), 0, 0));
+  }
+  // h_l (l >= 1, stash[l-1], fp32) rows from r0: 8 consecutive features per K-step.
+  template <int l>
+  __device__ __forceinline__ void load_h(int64_t r0) {
+    const rsrc_t hr = rows_rsrc(p.stash[l - 1], N::d[l], 4, r0);
+#pragma unroll
+    for (int s = 0; s < N::d[l] / 16; ++s) {
+      const int off = (n * N::d[l] + 16 * s + 8 * g) * 4;
+      const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0));
+      const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, 0));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hbuf[s][j] = lo[j];
+        hbuf[s][4 + j] = hi[j];
+      }
+    }
+  }
+  __device__ __forceinline__ void load_x(int64_t r0) {
+    const rsrc_t xr = rows_rsrc(p.x, N::d[0], 2, r0);
+#pragma unroll
+    for (int s = 0; s < KS0; ++s)
+      xbuf[s] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)((n * N::d[0] + 16 * s + 8 * g) * 2), 0, 0));
+  }
+
+  // This lane's 8 features 16s + 8g + [0..7] of its row into an exchange tile.
+  __device__ __forceinline__ void xwrite(f16* t, int s, f16x8 v) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[wo[j] + 16 * s * R] = v[j];
+  }
+  // 16-byte fragment: rows 16kk + 8g .. +7 of feature fb + (lane & 31), fb % 32 == 0.
+  __device__ __forceinline__ f16x8 xread(const f16* t, int fb, int kk) const {
+    return *reinterpret_cast<const f16x8*>(t + (fb + (lane & 31)) * R + (rd ^ (16 * kk)));
   }
 
   // Wgrad of layer l over the R rows in the exchange tiles, for this wave's
   // tiles.  K-steps (16 rows) outermost keeps only one step's fragments live.
   template <int l>
   __device__ __forceinline__ void wgrad() {
-    constexpr int WOB = Gm::wob(l);
-    constexpr int T = Gm::tpw(l);
+    constexpr int OFF = Gm::tpw_off(l);
 #pragma unroll
     for (int kk = 0; kk < R / 16; ++kk) {
+      if constexpr (Gm::quad(l)) {
+        constexpr int QO = Gm::wob(l) / 2;
 #pragma unroll
-      for (int k = 0; k < T; ++k) {
-        const int t = wid + k * NW;
-        if (t < Gm::tiles(l)) {
-          const int fi = 32 * (t / WOB) + (lane & 31), fo = 32 * (t % WOB) + (lane & 31);
-          wacc[Gm::tpw_off(l) + k] =
-              mfma32x32x16(xread<R>(ta, fi, kk, g), xread<R>(tz, fo, kk, g), wacc[Gm::tpw_off(l) + k]);
+        for (int k = 0; k < Gm::quads(l) / NW; ++k) {
+          const int q = wid + k * NW;
+          const int fi = 64 * (q / QO), fo = 64 * (q % QO);
+          const f16x8 a0 = xread(ta, fi, kk), a1 = xread(ta, fi + 32, kk);
+          const f16x8 b0 = xread(tz, fo, kk), b1 = xread(tz, fo + 32, kk);
+          wacc[OFF + 4 * k + 0] = mfma32x32x16(a0, b0, wacc[OFF + 4 * k + 0]);
+          wacc[OFF + 4 * k + 1] = mfma32x32x16(a0, b1, wacc[OFF + 4 * k + 1]);
+          wacc[OFF + 4 * k + 2] = mfma32x32x16(a1, b0, wacc[OFF + 4 * k + 2]);
+          wacc[OFF + 4 * k + 3] = mfma32x32x16(a1, b1, wacc[OFF + 4 * k + 3]);
+        }
+      } else {
+        constexpr int WOB = Gm::wob(l);
+#pragma unroll
+        for (int k = 0; k < Gm::tpw(l); ++k) {
+          const int t = wid + k * NW;
+          if (Gm::tiles(l) % NW == 0 || t < Gm::tiles(l))
+            wacc[OFF + k] = mfma32x32x16(xread(ta, 32 * (t / WOB), kk), xread(tz, 32 * (t % WOB), kk), wacc[OFF + k]);
         }
       }
     }
   }
 
-  // One layer of the backward for this wave's 32 rows: publish a_l and dz_l
-  // to the exchange tiles, run dgrad into dz_{l-1} (or dx), then the wgrad
-  // of dW_l once every wave has published.
+  // One layer of the backward for this wave's 32 rows.  On entry dz holds
+  // dz_l and hbuf (l >= 1) or xbuf (l = 0) holds a_l.  Publishes a_l and dz_l
+  // to the exchange tiles, runs dgrad into dzn = dz_{l-1} (or dx), and after
+  // the barrier issues the next phase's loads before the wgrad of dW_l so
+  // that their latency hides behind its MFMAs.
   template <int l>
-  __device__ __forceinline__ void layer(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
+  __device__ __forceinline__ void phase(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
     constexpr int KSA = N::d[l] / 16;      // K-steps of a_l
     constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
-    const int r = wid * 32 + n;            // row within the round
 #pragma unroll
-    for (int s = 0; s < KSZ; ++s) xwrite<R>(tz, s, g, r, dz[s]);
-    if constexpr (l == 0) {
-      const rsrc_t xr = rows_rsrc(p.x, N::d[0], 2);
+    for (int s = 0; s < KSZ; ++s) xwrite(tz, s, dz[s]);
 #pragma unroll
-      for (int s = 0; s < KSA; ++s)
-        xwrite<R>(ta, s, g, r,
-                  __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                                xr, (int)((n * N::d[0] + 16 * s + 8 * g) * 2), 0, 0)));
+    for (int s = 0; s < KSA; ++s) {
+      if constexpr (l >= 1)
+        xwrite(ta, s, pack8(hbuf[s][0], hbuf[s][1], hbuf[s][2], hbuf[s][3], hbuf[s][4], hbuf[s][5], hbuf[s][6], hbuf[s][7]));
+      else
+        xwrite(ta, s, xbuf[s]);
     }
-
-    if constexpr (l >= 1 || Gm::has_dgrad(l)) {
+    if constexpr (Gm::has_dgrad(l)) {
       constexpr int MB = N::d[l] / 32;
       const int fbase = (Gm::dfrag_off(l) * 64 + lane) * 16;
       const char* wb = reinterpret_cast<const char*>(wfr);
-      const rsrc_t hr = rows_rsrc(l >= 1 ? static_cast<const void*>(p.stash[l >= 1 ? l - 1 : 0]) : p.x, N::d[l], 4);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        // h_l = stash[l-1] (fp32) at features 32mb + [0, 32): K-steps 2mb, 2mb+1.
-        float h[2][8];
+        const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSZ * 1024));
+        f32x16 acc = {};
+#pragma unroll
+        for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16(frag[s * 64], dz[s], acc);
+        // Registers 0..7: features 32mb + 8g + [0..7] (K-step 2mb of a_l);
+        // 8..15: 32mb + 16 + 8g + [0..7] (K-step 2mb + 1).
         if constexpr (l >= 1) {
+          float v[16];
 #pragma unroll
-          for (int hs = 0; hs < 2; ++hs) {
-            const int s = 2 * mb + hs;
-            const int off = (n * N::d[l] + 16 * s + 8 * g) * 4;
-            const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0));
-            const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, 0));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              h[hs][j] = lo[j];
-              h[hs][4 + j] = hi[j];
-            }
-            xwrite<R>(ta, s, g, r,
-                      pack8(h[hs][0], h[hs][1], h[hs][2], h[hs][3], h[hs][4], h[hs][5], h[hs][6], h[hs][7]));
+          for (int j = 0; j < 8; ++j) {
+            v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[2 * mb][j] * kLog2e));
+            v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[2 * mb + 1][j] * kLog2e));
           }
-        }
-        if constexpr (Gm::has_dgrad(l)) {
-          const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSZ * 1024));
-          f32x16 acc = {};
-#pragma unroll
-          for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16(frag[s * 64], dz[s], acc);
-          // Registers 0..7: features 32mb + 8g + [0..7] (K-step 2mb of a_l);
-          // 8..15: 32mb + 16 + 8g + [0..7] (K-step 2mb + 1).
-          if constexpr (l >= 1) {
-            float v[16];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-h[0][j] * kLog2e));
-              v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-h[1][j] * kLog2e));
-            }
-            dzn[2 * mb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-            dzn[2 * mb + 1] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
-          } else {
-            const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2);
-            const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
-            buf_store16(pack8(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
-            buf_store16(pack8(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
-                        e * 2 + 32);
-          }
+          dzn[2 * mb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+          dzn[2 * mb + 1] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+        } else {
+          const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2, row0);
+          const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
+          buf_store16(pack8(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
+          buf_store16(pack8(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
+                      e * 2 + 32);
         }
       }
     }
     __syncthreads();  // every wave's rows are in the exchange tiles
+    if constexpr (l >= 2) {
+      load_h<l - 1>(row0);
+    } else if constexpr (l == 1) {
+      load_x(row0);
+    } else {  // the next round of this workgroup (empty resources past the end)
+      load_dout(row0 + rstep);
+      if constexpr (L >= 2) load_h<L - 1>(row0 + rstep);
+    }
     wgrad<l>();
     __syncthreads();  // the tiles are free for the next layer
   }
 
   template <int l>
-  __device__ __forceinline__ void layers_from(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
-    layer<l>(dz, dzn);
-    if constexpr (l > 0) layers_from<l - 1>(dzn, dz);
+  __device__ __forceinline__ void phases_from(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
+    phase<l>(dz, dzn);
+    if constexpr (l > 0) phases_from<l - 1>(dzn, dz);
+  }
+
+  __device__ __forceinline__ void round() {
+    f16x8 dz[KSM], dzn[KSM];
+#pragma unroll
+    for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
+    phases_from<L - 1>(dz, dzn);
+  }
+
+  // Adds one accumulated 32x32 tile (ti, to) of dW_l to global memory.
+  template <int l>
+  __device__ __forceinline__ void flush_tile(const f32x16& acc, int ti, int to) const {
+    constexpr int K = N::d[l], NO = N::d[l + 1];
+    const int fo = 32 * to + (lane & 31);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      // C layout: lane (o, g) holds rows 8a + 4g + b of its column, register 4a + b.
+      const int fi = 32 * ti + 8 * (e >> 2) + 4 * g + (e & 3);
+      if (fi < K && fo < NO) unsafeAtomicAdd(p.dw[l] + (int64_t)fi * NO + fo, acc[e]);
+    }
   }
 
   // Adds the owned tiles of every dW_l to global memory (fp32 atomics).
   template <int l>
   __device__ __forceinline__ void flush() {
-    constexpr int WOB = Gm::wob(l);
-    constexpr int K = N::d[l], NO = N::d[l + 1];
+    constexpr int OFF = Gm::tpw_off(l);
+    if constexpr (Gm::quad(l)) {
+      constexpr int QO = Gm::wob(l) / 2;
 #pragma unroll
-    for (int k = 0; k < Gm::tpw(l); ++k) {
-      const int t = wid + k * NW;
-      if (t < Gm::tiles(l)) {
-        const int fo = 32 * (t % WOB) + (lane & 31);
-        const f32x16 acc = wacc[Gm::tpw_off(l) + k];
+      for (int k = 0; k < Gm::quads(l) / NW; ++k) {
+        const int q = wid + k * NW;
+        const int ti = 2 * (q / QO), to = 2 * (q % QO);
+        flush_tile<l>(wacc[OFF + 4 * k + 0], ti, to);
+        flush_tile<l>(wacc[OFF + 4 * k + 1], ti, to + 1);
+        flush_tile<l>(wacc[OFF + 4 * k + 2], ti + 1, to);
+        flush_tile<l>(wacc[OFF + 4 * k + 3], ti + 1, to + 1);
+      }
+    } else {
+      constexpr int WOB = Gm::wob(l);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          // C layout: lane (o, g) holds rows 8a + 4g + b of its column, register 4a + b.
-          const int fi = 32 * (t / WOB) + 8 * (e >> 2) + 4 * g + (e & 3);
-          if (fi < K && fo < NO) unsafeAtomicAdd(p.dw[l] + (int64_t)fi * NO + fo, acc[e]);
-        }
+      for (int k = 0; k < Gm::tpw(l); ++k) {
+        const int t = wid + k * NW;
+        if (t < Gm::tiles(l)) flush_tile<l>(wacc[OFF + k], t / WOB, t % WOB);
       }
     }
     if constexpr (l + 1 < L) flush<l + 1>();
@@ -299,7 +365,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   using Gm = BwdGeom<N, NW, DX>;
   static_assert(Gm::valid(), "unsupported backward shape");
   constexpr int R = Gm::R;
-  constexpr int KSM = Gm::ksmax();
   __shared__ f16x8 wfr[Gm::ndfrag() * 64];
   __shared__ f16 ta[Gm::fa() * R];
   __shared__ f16 tz[Gm::fz() * R];
@@ -311,17 +376,17 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   f32x16 wacc[Gm::ntpw()];
 #pragma unroll
   for (int k = 0; k < Gm::ntpw(); ++k) wacc[k] = (f32x16){};
-  BwdWave<N, NW, DX> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, 0, wacc};
+  BwdWave<N, NW, DX> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, {}, 0, wacc};
+  wv.init_slots();
 
-  const int64_t nrounds = (p.M + R - 1) / R;
   // Every wave of a workgroup runs the same rounds (the barriers need all of them).
-  for (int64_t rd = blockIdx.x; rd < nrounds; rd += gridDim.x) {
-    wv.row0 = rd * R + wid * 32;
-    const int64_t left = p.M - wv.row0;
-    wv.nrows = (uint32_t)(left < 32 ? (left > 0 ? left : 0) : 32);
-    f16x8 dz[KSM], dzn[KSM];
-    wv.load_dout(dz);
-    wv.template layers_from<N::L - 1>(dz, dzn);
+  const int64_t nrounds = (p.M + R - 1) / R;
+  wv.row0 = (int64_t)blockIdx.x * R + wid * 32;
+  wv.load_dout(wv.row0);
+  if constexpr (N::L >= 2) wv.template load_h<N::L - 1>(wv.row0);
+  for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
+    wv.round();
+    wv.row0 += wv.rstep;
   }
   wv.template flush<0>();
 }

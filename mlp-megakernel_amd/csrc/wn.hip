@@ -4,10 +4,10 @@
 // Replaces `_wn_fwd_kernel` and `_wn_bwd_from_dw_T_kernel` of the reference's
 // training path (/root/reference/mlp_fused.md:466-486; the code itself is not
 // in the snapshot).  Parameters are contiguous blocks v_all / g_all, layer
-// after layer (mlp_fused.md:478-480).  Each thread owns one output column j of
-// one layer and walks its `in` rows; adjacent threads take adjacent columns, so
-// every row access of a wave is one contiguous segment of the [in, out]
-// row-major matrix (the column-wise read of fp32 dW needs no transposed copy).
+// after layer (mlp_fused.md:478-480).  Norms are per output column of the
+// [in, out] matrices; adjacent threads take adjacent columns, so every row
+// access of a wave is one contiguous segment of the row-major matrix (the
+// column-wise read of fp32 dW needs no transposed copy).
 #include "device_common.h"
 #include "host_common.h"
 
@@ -16,12 +16,16 @@ namespace mlpmk {
 struct WnLayout {
   int L;
   int in[kMaxLayers], out[kMaxLayers];
-  int64_t v_off[kMaxLayers];  // element offset of layer l in v / w / dw
-  int g_off[kMaxLayers];      // element offset of layer l in g / inv_norm
+  int64_t v_off[kMaxLayers];    // element offset of layer l in v / w / dw
+  int g_off[kMaxLayers];        // element offset of layer l in g / inv_norm
   int blk_off[kMaxLayers + 1];  // first workgroup of layer l
 };
 
-constexpr int kWnThreads = 64;
+// A workgroup owns 32 consecutive output columns of one layer; its 8 row
+// groups of 32 threads walk rows rg, rg + 8, ...  Each wave therefore reads
+// two rows x 32 columns per instruction (contiguous 64/128-byte segments), and
+// the per-column sums are reduced across the row groups in LDS.
+constexpr int kWnCols = 32, kWnRowGroups = 8, kWnThreads = kWnCols * kWnRowGroups;
 
 template <class P>
 __device__ __forceinline__ float ldp(const P* p, int64_t i) {
@@ -36,25 +40,42 @@ __device__ __forceinline__ int wn_layer_of(const WnLayout& lay, int blk) {
   return l;
 }
 
+// Sum over the row groups of a per-thread column partial; every thread of the
+// column gets the total.
+__device__ __forceinline__ float wn_colsum(float part, float (&red)[kWnRowGroups][kWnCols], int c, int rg) {
+  red[rg][c] = part;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kWnRowGroups; ++i) t += red[i][c];
+  return t;
+}
+
 template <class P>
 __global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const P* __restrict__ v,
                                                             const P* __restrict__ g, f16* __restrict__ w,
                                                             float* __restrict__ inv_norm) {
+  __shared__ float red[kWnRowGroups][kWnCols];
   const int l = wn_layer_of(lay, blockIdx.x);
-  const int j = (blockIdx.x - lay.blk_off[l]) * kWnThreads + threadIdx.x;
+  const int c = threadIdx.x % kWnCols, rg = threadIdx.x / kWnCols;
+  const int j = (blockIdx.x - lay.blk_off[l]) * kWnCols + c;
   const int K = lay.in[l], N = lay.out[l];
-  if (j >= N) return;
-  const P* vl = v + lay.v_off[l] + j;
+  const bool col = j < N;  // out widths are multiples of 16: a block may be half used
+  const int64_t base = lay.v_off[l] + j;
   float ss = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const float t = ldp(vl, (int64_t)k * N);
-    ss = fmaf(t, t, ss);
-  }
-  const float inv = 1.0f / sqrtf(ss);
+  if (col)
+    for (int k = rg; k < K; k += kWnRowGroups) {
+      const float t = ldp(v, base + (int64_t)k * N);
+      ss = fmaf(t, t, ss);
+    }
+  const float inv = 1.0f / sqrtf(wn_colsum(ss, red, c, rg));
+  if (!col) return;  // after the only barrier
   const float scale = ldp(g + lay.g_off[l], j) * inv;
-  f16* wl = w + lay.v_off[l] + j;
-  for (int k = 0; k < K; ++k) wl[(int64_t)k * N] = (f16)(ldp(vl, (int64_t)k * N) * scale);
-  inv_norm[lay.g_off[l] + j] = inv;
+  for (int k = rg; k < K; k += kWnRowGroups) {
+    const int64_t e = base + (int64_t)k * N;
+    w[e] = (f16)(ldp(v, e) * scale);
+  }
+  if (rg == 0) inv_norm[lay.g_off[l] + j] = inv;
 }
 
 template <class P>
@@ -62,21 +83,29 @@ __global__ __launch_bounds__(kWnThreads) void wn_bwd_kernel(WnLayout lay, const 
                                                             const P* __restrict__ v, const P* __restrict__ g,
                                                             const float* __restrict__ inv_norm,
                                                             P* __restrict__ dv, P* __restrict__ dg) {
+  __shared__ float red[kWnRowGroups][kWnCols];
   const int l = wn_layer_of(lay, blockIdx.x);
-  const int j = (blockIdx.x - lay.blk_off[l]) * kWnThreads + threadIdx.x;
+  const int c = threadIdx.x % kWnCols, rg = threadIdx.x / kWnCols;
+  const int j = (blockIdx.x - lay.blk_off[l]) * kWnCols + c;
   const int K = lay.in[l], N = lay.out[l];
-  if (j >= N) return;
+  const bool col = j < N;
   const int64_t base = lay.v_off[l] + j;
-  const float inv = inv_norm[lay.g_off[l] + j];
   float dot = 0.0f;  // <dW_j, v_j>
-  for (int k = 0; k < K; ++k) dot = fmaf(dw[base + (int64_t)k * N], ldp(v, base + (int64_t)k * N), dot);
+  if (col)
+    for (int k = rg; k < K; k += kWnRowGroups) {
+      const int64_t e = base + (int64_t)k * N;
+      dot = fmaf(dw[e], ldp(v, e), dot);
+    }
+  dot = wn_colsum(dot, red, c, rg);
+  if (!col) return;  // after the only barrier
+  const float inv = inv_norm[lay.g_off[l] + j];
   const float dgj = dot * inv;  // <dW_j, u_j>, u = v * inv
   const float gs = ldp(g + lay.g_off[l], j) * inv;
-  for (int k = 0; k < K; ++k) {
+  for (int k = rg; k < K; k += kWnRowGroups) {
     const int64_t e = base + (int64_t)k * N;
     dv[e] = (P)(gs * (dw[e] - dgj * ldp(v, e) * inv));
   }
-  dg[lay.g_off[l] + j] = (P)dgj;
+  if (rg == 0) dg[lay.g_off[l] + j] = (P)dgj;
 }
 
 static int wn_layout(int L, const int* dims, WnLayout* lay) {
@@ -92,7 +121,7 @@ static int wn_layout(int L, const int* dims, WnLayout* lay) {
     lay->blk_off[l] = bo;
     vo += (int64_t)dims[l] * dims[l + 1];
     go += dims[l + 1];
-    bo += (dims[l + 1] + kWnThreads - 1) / kWnThreads;
+    bo += (dims[l + 1] + kWnCols - 1) / kWnCols;
   }
   lay->blk_off[L] = bo;
   return MLPMK_OK;
