@@ -32,9 +32,10 @@ Pinning (what checks this restatement, in tests/test_oracle.py):
   forward   -> torch CPU float64 matmul+softplus (library), closed forms
                (zero W1 gives h1 = ln 2; identity weights give softplus(softplus(x)));
                linearity in the last layer; the committed golden fixtures.
-  backward  -> torch.autograd in float64 (library), torch.autograd.gradcheck
-               (finite differences) on tiny shapes; planted transposition and
-               dropped-derivative bugs must fail.
+  backward  -> torch.autograd in float64 (library), central finite
+               differences on tiny shapes; planted bugs must fail (dropped
+               activation derivative, derivative from the wrong argument,
+               W instead of W^T in the data gradient).
   wn_*      -> torch._weight_norm (library) and its autograd; invariants
                ||W[:, j]|| = |g_j|, <dv[:, j], v[:, j]> = 0.
 No function of this module is "parity unpinned".

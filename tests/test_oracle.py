@@ -205,6 +205,22 @@ def test_planted_backward_bugs_are_caught(monkeypatch):
     assert not close(orc.backward(x, ws, hs, dout, dtype=np.float64)[0])
 
 
+def test_planted_transposed_weight_in_data_gradient_is_caught():
+    # Square layers so that a data gradient through W instead of W^T still runs.
+    dims = (6, 6, 6, 6)
+    x, ws = orc.make_inputs(dims, 30, seed=5)
+    dout = np.random.default_rng(2).standard_normal((30, 6))
+    _, hs = orc.forward(x, ws, dtype=np.float64, return_hidden=True)
+    tdws, tdx = torch_grads(x, ws, dout)
+    good, gdx = orc.backward(x, ws, hs, dout, dtype=np.float64)
+    assert all(np.allclose(a, b, rtol=1e-6, atol=1e-9) for a, b in zip(good, tdws))
+    # dz_{l-1} = (dz_l W_l) * sigma instead of (dz_l W_l^T) * sigma: feed W^T
+    bad_ws = [w.T.copy() for w in ws]
+    bad, bdx = orc.backward(x, bad_ws, hs, dout, dtype=np.float64)
+    assert not np.allclose(bad[0], tdws[0], rtol=1e-3, atol=1e-6)
+    assert not np.allclose(bdx, tdx, rtol=1e-3, atol=1e-6)
+
+
 # --------------------------------------------------------------- weight norm --
 def test_wn_forward_matches_torch_weight_norm_and_invariants():
     vs, gs = orc.make_wn_params((128, 128, 128, 128))
