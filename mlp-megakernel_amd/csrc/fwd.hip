@@ -158,19 +158,58 @@ __device__ __forceinline__ void load_rows(i32x4 (&xa)[KS][NB], rsrc_t xr, int n,
 __device__ __forceinline__ f16x8 as_f16x8(f16x8 v) { return v; }
 __device__ __forceinline__ f16x8 as_f16x8(i32x4 v) { return __builtin_bit_cast(f16x8, v); }
 
-// MFMA chain of output block mb of layer l: acc[nb] = W_l[:, block mb]^T . in.
-template <int KS, int NB, class T, int KIN>
-__device__ __forceinline__ void mma_block(f32x16 (&acc)[NB], const f16x8* __restrict__ frag,
-                                          const T (&in)[KIN][NB]) {
-  f16x8 a[KS];
+// Steps of one row block: step t is output block mb(t) (32 features) of
+// layer layer(t), layers in order.
+template <class N>
+struct Steps {
+  static constexpr int count() {
+    int s = 0;
+    for (int l = 0; l < N::L; ++l) s += N::mbs(l);
+    return s;
+  }
+  static constexpr int layer(int t) {
+    int l = 0;
+    while (t >= N::mbs(l)) t -= N::mbs(l++);
+    return l;
+  }
+  static constexpr int mb(int t) {
+    int l = 0;
+    while (t >= N::mbs(l)) t -= N::mbs(l++);
+    return t;
+  }
+  static constexpr int frag(int t) { return N::frag_off(layer(t)) + mb(t) * N::ks(layer(t)); }
+};
+
+// Weight fragments (A operands) of one step's MFMA chain.
+template <int KSM>
+struct Frags {
+  f16x8 a[KSM];
+};
+
+// Reads step t's fragments from LDS.  The address goes through opaque():
+// weights never change after staging, and without it the compiler would
+// hoist every fragment read out of the persistent row loop (and spill).
+template <class N, int t, int KSM>
+__device__ __forceinline__ void load_frags(Frags<KSM>& f, const char* lds_b, int lane_off) {
+  constexpr int KS = N::ks(Steps<N>::layer(t));
+  const f16x8* src = reinterpret_cast<const f16x8*>(lds_b + opaque(lane_off + Steps<N>::frag(t) * 1024));
 #pragma unroll
-  for (int s = 0; s < KS; ++s) a[s] = frag[s * 64];
+  for (int s = 0; s < KS; ++s) f.a[s] = src[s * 64];
+}
+
+// MFMA chain of one output block over input K-steps [S0, S1):
+// acc[nb] (+)= W_l[K-steps, block]^T . in.  S0 == 0 starts from zero.
+template <int S0, int S1, int NB, int KSM, class T, int KIN>
+__device__ __forceinline__ void chain(f32x16 (&acc)[NB], const Frags<KSM>& f, const T (&in)[KIN][NB]) {
+  static_assert(KIN >= S1, "input K-steps");
+  if constexpr (S0 == 0) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x16){};
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x16){};
+  }
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = S0; s < S1; ++s)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16(a[s], as_f16x8(in[s][nb]), acc[nb]);
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16(f.a[s], as_f16x8(in[s][nb]), acc[nb]);
 }
 
 // Activation and hand-off of output block mb: hidden layers apply softplus
@@ -250,58 +289,87 @@ __device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane
   __builtin_amdgcn_wave_barrier();
 }
 
-// One layer l over NB batch blocks, software-pipelined by output block: the
-// MFMA chain of block mb+1 is issued before the epilogue of block mb, so one
-// wave keeps the matrix core busy while its VALU runs the activation.  `in`
-// holds the B operands of the layer's input K-steps; `nxt` receives the next
-// layer's.
-template <class N, int l, int NB, bool STASH, bool STAGE, int KIN, int KSM, class T>
-__device__ __forceinline__ void run_layer(const BlockIO& io, const f16x8* __restrict__ lds,
-                                          const T (&in)[KIN][NB], f16x8 (&nxt)[KSM][NB], int lane) {
-  static_assert(KIN >= N::ks(l), "input K-steps");
-  constexpr int KS = N::ks(l);
-  constexpr int MB = N::mbs(l);
-  const int fbase = (N::frag_off(l) * 64 + lane) * 16;  // byte offset of this lane's fragments
-  const char* lds_b = reinterpret_cast<const char*>(lds);
-  f32x16 acc[2][NB];
-  mma_block<KS, NB>(acc[0], reinterpret_cast<const f16x8*>(lds_b + opaque(fbase)), in);
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    if (mb + 1 < MB)
-      mma_block<KS, NB>(acc[(mb + 1) & 1],
-                        reinterpret_cast<const f16x8*>(lds_b + opaque(fbase + (mb + 1) * KS * 1024)), in);
-    epilogue<N, l, NB, STASH, STAGE, KSM>(io, acc[mb & 1], mb, nxt, lane);
-    if constexpr (l == N::L - 1 && STAGE) {
-      if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
-    }
+// Register state of a wave while it runs one row block.
+template <class N, int NB, int KSM>
+struct Chain {
+  static constexpr int KS0 = N::ks(0);
+  i32x4 xa[KS0][NB];             // x rows of the block (refilled with the next block's)
+  f16x8 b0[KSM][NB], b1[KSM][NB];  // hidden activations, ping-pong between layers
+  f32x16 acc[2][NB];             // accumulators of the current and the next step
+  Frags<KSM> fr[2];              // fragments of the next two steps
+
+  // Layer l reads x (l = 0), b0 (odd l) or b1 (even l >= 2) and writes b0
+  // (even l) or b1 (odd l).
+  template <int l>
+  __device__ __forceinline__ auto& in() {
+    if constexpr (l == 0) return xa;
+    else if constexpr (l % 2 == 1) return b0;
+    else return b1;
   }
+  template <int l>
+  __device__ __forceinline__ auto& out() {
+    if constexpr (l % 2 == 0) return b0;
+    else return b1;
+  }
+};
+
+// Step t of a row block.  Issue order: fragments of step t+2 (their LDS
+// latency hides behind two steps), the MFMA chain of step t+1 when it belongs
+// to the same layer (so it runs on the matrix core while this step's
+// activation runs on the VALU), the epilogue of step t, and -- at a layer
+// boundary -- the first chain of the next layer, which needs all of this
+// layer's outputs.  With an even step count the last two steps prefetch the
+// next row block's first two fragment sets (weights are the same for every
+// block).
+template <class N, int t, int NB, bool STASH, bool STAGE, int KSM>
+__device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chain<N, NB, KSM>& c,
+                                     const char* lds_b, int lane_off, int64_t next, int lane) {
+  using S = Steps<N>;
+  constexpr int T = S::count();
+  constexpr int l = S::layer(t), mb = S::mb(t);
+  constexpr bool same = t + 1 < T && S::layer(t + 1) == l;
+  constexpr int ROWS = 32 * NB;
+  if constexpr (t + 2 < T)
+    load_frags<N, t + 2, KSM>(c.fr[t & 1], lds_b, lane_off);
+  else if constexpr (T % 2 == 0)
+    load_frags<N, t + 2 - T, KSM>(c.fr[t & 1], lds_b, lane_off);
+  if constexpr (same) chain<0, N::ks(l), NB>(c.acc[(t + 1) & 1], c.fr[(t + 1) & 1], c.template in<l>());
+  // Last block of a layer: the next layer's first chain can already run over
+  // the K-steps the earlier blocks produced (2 per block); only the last two
+  // wait for this step's epilogue.
+  constexpr int EARLY = (t + 1 < T && !same) ? 2 * mb : 0;
+  if constexpr (EARLY > 0)
+    chain<0, EARLY, NB>(c.acc[(t + 1) & 1], c.fr[(t + 1) & 1], c.template in<(l + 1) % N::L>());
+  if constexpr (l == 0 && (same ? t + 1 == N::mbs(0) - 1 : t == 0)) {
+    // Every MFMA that reads x has been issued: refill xa with the next block's
+    // rows (past the end the resource is empty and the refill reads zeros).
+    MLPMK_SCHED_FENCE();
+    load_rows<N::ks(0), NB>(c.xa, block_io<N, false, ROWS>(p, next * ROWS).x, lane & 31, lane >> 5);
+  }
+  epilogue<N, l, NB, STASH, STAGE, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), lane);
+  if constexpr (l == N::L - 1 && STAGE) {
+    if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
+  }
+  if constexpr (t + 1 < T && !same)
+    chain<EARLY, N::ks(l + 1), NB>(c.acc[(t + 1) & 1], c.fr[(t + 1) & 1], c.template in<l + 1>());
+  if constexpr (t + 1 < T) step<N, t + 1, NB, STASH, STAGE, KSM>(p, io, c, lds_b, lane_off, next, lane);
 }
 
-// Layers l .. L-1, ping-ponging between two register buffers.
-template <class N, int l, int NB, bool STASH, bool STAGE, int KSM>
-__device__ __forceinline__ void run_chain(const BlockIO& io, const f16x8* __restrict__ lds,
-                                          f16x8 (&cur)[KSM][NB], f16x8 (&oth)[KSM][NB], int lane) {
-  run_layer<N, l, NB, STASH, STAGE, KSM, KSM>(io, lds, cur, oth, lane);
-  if constexpr (l + 1 < N::L) run_chain<N, l + 1, NB, STASH, STAGE, KSM>(io, lds, oth, cur, lane);
-}
-
-// One row block: layer 0 from the x rows in `xa`, then the refill of `xa` with
-// the rows of block `next` (its latency hides behind layers 1..L-1), then the
-// rest of the chain and the stores.
+// One row block: the whole layer chain, stores, and the x refill for block
+// `next`.  On entry c.xa holds the block's x rows and c.fr[0], c.fr[1] the
+// first two steps' fragments.
 template <class N, int NB, bool STASH, bool STAGE, int KSM>
-__device__ __forceinline__ void fwd_block(const FwdParams& p, const f16x8* __restrict__ lds,
-                                          i32x4* stage, int64_t b, int64_t next,
-                                          i32x4 (&xa)[N::ks(0)][NB], f16x8 (&b0)[KSM][NB],
-                                          f16x8 (&b1)[KSM][NB], int lane) {
-  constexpr int KS0 = N::ks(0);
+__device__ __forceinline__ void fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
+                                          int lane_off, i32x4* stage, int64_t b, int64_t next, int lane) {
   constexpr int ROWS = 32 * NB;
   BlockIO io = block_io<N, STASH, ROWS>(p, b * ROWS);
   io.stage = stage;
-  run_layer<N, 0, NB, STASH, STAGE, KS0, KSM>(io, lds, xa, b0, lane);
-  MLPMK_SCHED_FENCE();  // the refill must not be hoisted above layer 0
-  // Past the end the resource is empty: the refill then reads zeros.
-  load_rows<KS0, NB>(xa, block_io<N, false, ROWS>(p, next * ROWS).x, lane & 31, lane >> 5);
-  run_chain<N, 1, NB, STASH, STAGE, KSM>(io, lds, b0, b1, lane);
+  if constexpr (Steps<N>::count() % 2 != 0) {  // no wrap-around prefetch: load here
+    load_frags<N, 0, KSM>(c.fr[0], lds_b, lane_off);
+    if constexpr (Steps<N>::count() > 1) load_frags<N, 1, KSM>(c.fr[1], lds_b, lane_off);
+  }
+  chain<0, N::ks(0), NB>(c.acc[0], c.fr[0], c.xa);
+  step<N, 0, NB, STASH, STAGE, KSM>(p, io, c, lds_b, lane_off, next, lane);
 }
 
 // Persistent forward.  Workgroup b owns row blocks b, b + G, b + 2G, ...
@@ -309,15 +377,9 @@ __device__ __forceinline__ void fwd_block(const FwdParams& p, const f16x8* __res
 // from a counter in LDS.  Claiming (rather than a fixed wave-to-block map)
 // matters because the SIMD arbiter favours the older of two waves: with a
 // static split one wave of each pair finishes early and the other runs the
-// tail alone.  The x rows of a wave's next D claimed blocks are in flight in
-// a ring of D register buffers: once layer 0 has consumed a buffer, the
-// wave's next claim is requested into it.
-//
-// The first D blocks are peeled off the loop so that the loop header is
-// entered from two paths with the same outstanding memory operations (ring
-// refills, then stores).  vmcnt counts loads and stores in issue order; with
-// an unpeeled loop the prologue path (loads only) forces the waits for a
-// refilled buffer to also wait for the preceding stores.
+// tail alone.  Each wave keeps the x rows of its next claimed block in flight
+// while it computes the current one.  D is the number of such blocks in
+// flight; one is enough (deeper rings measured no faster).
 template <class N, int NB, bool STASH, int NW, int D>
 __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   static_assert(N::valid(), "unsupported widths");
@@ -363,30 +425,26 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   };
 
   // Past the end a block's resource is empty: its prefetch reads zeros.
-  i32x4 xa[D][KS0][NB];
-  int64_t q[D];
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    q[d] = claim();
-    load_rows<KS0, NB>(xa[d], block_io<N, false, ROWS>(p, q[d] * ROWS).x, lane & 31, lane >> 5);
+  static_assert(D == 1, "one block of x rows in flight per wave");
+  Chain<N, NB, KSM> c;
+  const char* lds_b = reinterpret_cast<const char*>(lds);
+  const int lane_off = lane * 16;  // this lane's 16 bytes within a 1 KiB fragment
+  int64_t b = claim();
+  if (b >= nblk) return;  // no barrier follows
+  load_rows<KS0, NB>(c.xa, block_io<N, false, ROWS>(p, b * ROWS).x, lane & 31, lane >> 5);
+  if constexpr (Steps<N>::count() % 2 == 0) {
+    load_frags<N, 0, KSM>(c.fr[0], lds_b, lane_off);
+    load_frags<N, 1, KSM>(c.fr[1], lds_b, lane_off);
   }
-  f16x8 b0[KSM][NB], b1[KSM][NB];
+  // The first block is peeled so that the loop header is entered from two
+  // paths with the same outstanding memory operations (the x refill, then
+  // stores): vmcnt counts loads and stores in issue order.
+  int64_t next = claim();
+  fwd_block<N, NB, STASH, STAGE, KSM>(p, c, lds_b, lane_off, stage, b, next, lane);
   // Claims are increasing per wave, so once one is past the end all later are.
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    if (q[d] >= nblk) return;  // no barrier follows
-    const int64_t nxt = claim();
-    fwd_block<N, NB, STASH, STAGE, KSM>(p, lds, stage, q[d], nxt, xa[d], b0, b1, lane);
-    q[d] = nxt;
-  }
-  for (;;) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      if (q[d] >= nblk) return;
-      const int64_t nxt = claim();
-      fwd_block<N, NB, STASH, STAGE, KSM>(p, lds, stage, q[d], nxt, xa[d], b0, b1, lane);
-      q[d] = nxt;
-    }
+  for (b = next; b < nblk; b = next) {
+    next = claim();
+    fwd_block<N, NB, STASH, STAGE, KSM>(p, c, lds_b, lane_off, stage, b, next, lane);
   }
 }
 
