@@ -22,8 +22,10 @@ import torch.nn.functional as F
 import _mlpmk  # noqa: F401  (registers the package as ``mlpmk``)
 from mlpmk import ops as _ops
 
-# Waves per workgroup of the gfx950 forward kernel (mlp-megakernel_amd/csrc/fwd.hip).
-_WAVES_PER_WG = 8
+# Waves per workgroup of the gfx950 inference forward (mlp-megakernel_amd/csrc/fwd.hip):
+# 12 (3 per SIMD) for 128-wide layers, 16 for the narrow network.
+_WAVES_PER_WG_WIDE = 12
+_WAVES_PER_WG_NARROW = 16
 
 
 def __getattr__(name):
@@ -36,8 +38,7 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False):
     """gfx950 launch policy in the reference's tuple shape
     ``(BM, BN3, BK1, BK2, BK3, warps)`` (kernel.py:25-53).
 
-    BM = rows a wave computes per block (32 for 128-wide layers, 64 for the
-    narrow network, one or two 32-row MFMA batch blocks), BN3 = the whole
+    BM = rows a wave computes per block (32: one MFMA batch block), BN3 = the whole
     output width (one pass computes every output column), BK* = 16 (the K of
     v_mfma_f32_32x32x16_f16), warps = 64-lane waves per workgroup.  The
     persistent grid is min(CUs x occupancy, ceil(M / (BM * warps))) and the
@@ -47,8 +48,8 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False):
     """
     if fp32:
         raise TypeError("the fused forward takes fp16 inputs (main-branch surface is fp16 only)")
-    bm = 64 if max(K1, N1, N2, N3) <= 64 else 32
-    return bm, N3, 16, 16, 16, _WAVES_PER_WG
+    narrow = max(K1, N1, N2, N3) <= 64
+    return 32, N3, 16, 16, 16, _WAVES_PER_WG_NARROW if narrow else _WAVES_PER_WG_WIDE
 
 
 def _fused_mlp_fwd(x, w1, w2, w3):

@@ -37,10 +37,17 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
-// AUX is the buffer instruction's cache-policy field (bit 1 = "nt").  The
-// megakernels use the default policy: on MI355X the non-temporal bit speeds
-// up a plain grid-stride copy (6.2 vs 5.6 TB/s) but slows the forward
-// megakernel by about 5%.
+// AUX is the buffer instruction's cache-policy field (bit 1 = "nt").
+// Measured on MI355X with the forward's access pattern (each wave reads its
+// rows as 32-byte segments of 32 rows per load, writes whole 1 KiB runs per
+// store), 256 MiB in + 256 MiB out:
+//   default loads + default stores   5.2 TB/s
+//   default loads + nt stores        6.9 TB/s
+//   nt loads      + nt stores        4.6 TB/s
+// nt loads lose because a 128-byte line is consumed by four successive loads
+// and must stay in the vector cache between them; nt stores stream the
+// output past L2 without evicting the input lines still being read.
+constexpr int kStreamStore = 2;
 template <class T, int AUX = 0>
 __device__ __forceinline__ T buf_load16(rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, AUX));

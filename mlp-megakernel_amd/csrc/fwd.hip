@@ -48,30 +48,35 @@ __device__ __forceinline__ float wscale(int l) {
   return (l == 0 ? kLog2e : 1.0f) * (l == N::L - 1 ? kLn2 : 1.0f);
 }
 
-template <class N, int NT>
+// Lane `lane` of fragment (mb, s) of layer l.
+template <class N>
+__device__ __forceinline__ f16x8 weight_fragment(const FwdParams& p, int l, int f, int lane) {
+  const int Nout = N::d[l + 1], KS = N::ks(l);
+  const int mb = f / KS, s = f % KS;
+  const int i = lane & 31, g = lane >> 5;
+  const int of = outfeat(mb, i);
+  f16x8 v;
+  if (of < Nout) {
+    const f16* src = p.w[l] + (int64_t)(16 * s + 8 * g) * Nout + of;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (f16)((float)src[(int64_t)j * Nout] * wscale<N>(l));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (f16)0.0f;
+  }
+  return v;
+}
+
+// Stages every fragment from the RF-th on; fragment F lands at LDS slot F - RF.
+template <class N, int NT, int RF>
 __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
 #pragma unroll
   for (int l = 0; l < N::L; ++l) {
-    const int K = N::d[l], Nout = N::d[l + 1];
-    const int KS = N::ks(l);
-    const int items = N::mbs(l) * KS * 64;
-    const f16* __restrict__ w = p.w[l];
+    const int items = N::mbs(l) * N::ks(l) * 64;
     for (int item = threadIdx.x; item < items; item += NT) {
       const int f = item >> 6, lane = item & 63;
-      const int mb = f / KS, s = f % KS;
-      const int i = lane & 31, g = lane >> 5;
-      const int of = outfeat(mb, i);
-      f16x8 v;
-      if (of < Nout) {
-        const f16* src = w + (int64_t)(16 * s + 8 * g) * Nout + of;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (f16)((float)src[(int64_t)j * Nout] * wscale<N>(l));
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (f16)0.0f;
-      }
-      (void)K;
-      lds[(N::frag_off(l) + f) * 64 + lane] = v;
+      if (N::frag_off(l) + f < RF) continue;
+      lds[(N::frag_off(l) + f - RF) * 64 + lane] = weight_fragment<N>(p, l, f, lane);
     }
   }
 }
@@ -84,28 +89,32 @@ struct BlockIO {
   i32x4* stage;  // this wave's LDS staging tile for the output rows (STAGE only)
 };
 
-// Output staging: whether the last layer's rows go through an LDS tile per
-// wave so that they leave as whole 128-byte cache lines.  A lane of the MFMA
-// result layout holds one row, so direct stores write 32 bytes into each of
-// 32 rows per instruction and complete a row's lines piecemeal, which costs
-// HBM write efficiency once rows are wider than 64 bytes.  The tile holds two
-// 32-feature output blocks (128 bytes per row); it is flushed after every
-// second block.  Needs output rows of a multiple of 64 features and LDS room
-// next to the staged weights.
+// LDS plan of a workgroup (160 KiB on gfx950), in priority order:
+//  * all weight fragments except `reg_frags` leading ones, which each wave
+//    keeps in VGPRs instead (4 registers per fragment);
+//  * output staging: the last layer's rows go through an LDS tile per wave so
+//    that they leave as whole 128-byte cache lines.  A lane of the MFMA result
+//    layout holds one row, so direct stores write 32 bytes into each of 32 rows
+//    per instruction and complete a row's lines piecemeal, which costs HBM
+//    write efficiency once rows are wider than 64 bytes.  The tile holds two
+//    32-feature output blocks (128 bytes per row) and is flushed after every
+//    second block.  Needs output rows of a multiple of 64 features;
+//  * the 16-byte row-block claim counter.  Without it waves would split the
+//    workgroup's blocks statically, and the SIMD arbiter's preference for the
+//    older of two waves then lets one wave of each pair finish far ahead of
+//    the other (measured: 142 vs 211 us for the 5-layer network at 1M rows).
+//    When the weights alone fill the LDS, one fragment moves to VGPRs to make
+//    room for it.
 template <class N, int NB, int NW>
-struct OutStage {
+struct LdsPlan {
+  static constexpr int kLds = 163840;
   static constexpr int kRowChunks = 8;  // 16-byte chunks per staged row segment
   static constexpr int kTileChunks = 32 * NB * kRowChunks;
-  static constexpr bool enabled =
-      N::d[N::L] % 64 == 0 && N::nfrag() * 1024 + NW * kTileChunks * 16 + 16 <= 163840;
-  static constexpr int bytes = enabled ? NW * kTileChunks * 16 : 0;
-};
-
-// Whether the workgroup's waves claim row blocks from an LDS counter (needs
-// 16 bytes of LDS next to the weights and the staging tiles).
-template <class N, int NB, int NW>
-struct Claim {
-  static constexpr bool enabled = N::nfrag() * 1024 + OutStage<N, NB, NW>::bytes + 16 <= 163840;
+  static constexpr int wbytes = N::nfrag() * 1024;
+  static constexpr bool stage = N::d[N::L] % 64 == 0 && wbytes + NW * kTileChunks * 16 + 16 <= kLds;
+  static constexpr int stage_bytes = stage ? NW * kTileChunks * 16 : 0;
+  static constexpr int reg_frags = wbytes + stage_bytes + 16 <= kLds ? 0 : 1;
+  static constexpr bool claim = wbytes - reg_frags * 1024 + stage_bytes + 16 <= kLds;
 };
 
 // LDS chunk slot of (row, chunk): the chunk index is XORed with the row so that
@@ -186,15 +195,18 @@ struct Frags {
   f16x8 a[KSM];
 };
 
-// Reads step t's fragments from LDS.  The address goes through opaque():
-// weights never change after staging, and without it the compiler would
-// hoist every fragment read out of the persistent row loop (and spill).
-template <class N, int t, int KSM>
-__device__ __forceinline__ void load_frags(Frags<KSM>& f, const char* lds_b, int lane_off) {
+// Reads step t's fragments from LDS (fragments below RF come from the
+// wave's register copy `rf`).  The address goes through opaque(): weights
+// never change after staging, and without it the compiler would hoist every
+// fragment read out of the persistent row loop (and spill).
+template <class N, int t, int KSM, int RF>
+__device__ __forceinline__ void load_frags(Frags<KSM>& f, const char* lds_b, int lane_off, f16x8 rf) {
   constexpr int KS = N::ks(Steps<N>::layer(t));
-  const f16x8* src = reinterpret_cast<const f16x8*>(lds_b + opaque(lane_off + Steps<N>::frag(t) * 1024));
+  constexpr int F0 = Steps<N>::frag(t);
+  const char* src = lds_b + opaque(lane_off);
 #pragma unroll
-  for (int s = 0; s < KS; ++s) f.a[s] = src[s * 64];
+  for (int s = 0; s < KS; ++s)
+    f.a[s] = F0 + s < RF ? rf : *reinterpret_cast<const f16x8*>(src + (F0 + s - RF) * 1024);
 }
 
 // MFMA chain of one output block over input K-steps [S0, S1):
@@ -237,9 +249,9 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
           __builtin_bit_cast(i32x4, pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]));
     } else if constexpr (LAST) {
       const f32x16& v = acc[nb];  // ln 2 is folded into the staged W_L
-      if (lo_ok) buf_store16(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
+      if (lo_ok) buf_store16<kStreamStore>(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
       if (hi_ok)
-        buf_store16(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
+        buf_store16<kStreamStore>(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
     } else {
       float v[16];
 #pragma unroll
@@ -250,12 +262,12 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
 #pragma unroll
         for (int e = 0; e < 16; ++e) h[e] = v[e] * kLn2;
         if (lo_ok) {
-          buf_store16((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
-          buf_store16((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
+          buf_store16<kStreamStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
+          buf_store16<kStreamStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
         }
         if (hi_ok) {
-          buf_store16((f32x4){h[8], h[9], h[10], h[11]}, sr, elem * 4 + 64);
-          buf_store16((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
+          buf_store16<kStreamStore>((f32x4){h[8], h[9], h[10], h[11]}, sr, elem * 4 + 64);
+          buf_store16<kStreamStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
         }
       }
       if (2 * mb < KSM) nxt[2 * mb][nb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
@@ -271,7 +283,7 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
 template <class N, int NB>
 __device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane) {
   constexpr int Nout = N::d[N::L];
-  constexpr int TC = OutStage<N, NB, 1>::kTileChunks;
+  constexpr int TC = LdsPlan<N, NB, 1>::kTileChunks;
   // The tile was written by other lanes of this wave; LDS executes one wave's
   // operations in order, so only the compiler needs a fence here.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -282,7 +294,7 @@ __device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane
     const int q = 64 * i + lane;  // linear 16-byte chunk of the tile
     const int row = q >> 3, c = q & 7;
     const i32x4 v = io.stage[stage_slot(row, c)];
-    __builtin_amdgcn_raw_buffer_store_b128(v, io.out, row * Nout * 2 + seg * 128 + c * 16, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, io.out, row * Nout * 2 + seg * 128 + c * 16, 0, kStreamStore);
   }
   // The next writes into the tile must stay behind these reads.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -296,7 +308,8 @@ struct Chain {
   i32x4 xa[KS0][NB];             // x rows of the block (refilled with the next block's)
   f16x8 b0[KSM][NB], b1[KSM][NB];  // hidden activations, ping-pong between layers
   f32x16 acc[2][NB];             // accumulators of the current and the next step
-  Frags<KSM> fr[2];              // fragments of the next two steps
+  Frags<KSM> fr;                 // fragments of the next step
+  f16x8 rf;                      // register-resident fragment (LdsPlan::reg_frags)
 
   // Layer l reads x (l = 0), b0 (odd l) or b1 (even l >= 2) and writes b0
   // (even l) or b1 (odd l).
@@ -313,15 +326,13 @@ struct Chain {
   }
 };
 
-// Step t of a row block.  Issue order: fragments of step t+2 (their LDS
-// latency hides behind two steps), the MFMA chain of step t+1 when it belongs
-// to the same layer (so it runs on the matrix core while this step's
-// activation runs on the VALU), the epilogue of step t, and -- at a layer
-// boundary -- the first chain of the next layer, which needs all of this
-// layer's outputs.  With an even step count the last two steps prefetch the
-// next row block's first two fragment sets (weights are the same for every
-// block).
-template <class N, int t, int NB, bool STASH, bool STAGE, int KSM>
+// Step t of a row block.  Issue order: fragments of step t+1 and, when it
+// belongs to the same layer, its MFMA chain (which runs on the matrix core
+// while this step's activation runs on the VALU), then the epilogue of step
+// t, and -- at a layer boundary -- the first chain of the next layer, which
+// needs all of this layer's outputs.  Fragments are single-buffered: the
+// chain waits for its LDS reads, which the other waves of the SIMD cover.
+template <class N, int t, int NB, bool STASH, bool STAGE, int KSM, int RF>
 __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chain<N, NB, KSM>& c,
                                      const char* lds_b, int lane_off, int64_t next, int lane) {
   using S = Steps<N>;
@@ -329,17 +340,14 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
   constexpr int l = S::layer(t), mb = S::mb(t);
   constexpr bool same = t + 1 < T && S::layer(t + 1) == l;
   constexpr int ROWS = 32 * NB;
-  if constexpr (t + 2 < T)
-    load_frags<N, t + 2, KSM>(c.fr[t & 1], lds_b, lane_off);
-  else if constexpr (T % 2 == 0)
-    load_frags<N, t + 2 - T, KSM>(c.fr[t & 1], lds_b, lane_off);
-  if constexpr (same) chain<0, N::ks(l), NB>(c.acc[(t + 1) & 1], c.fr[(t + 1) & 1], c.template in<l>());
+  if constexpr (t + 1 < T) load_frags<N, t + 1, KSM, RF>(c.fr, lds_b, lane_off, c.rf);
+  if constexpr (same) chain<0, N::ks(l), NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l>());
   // Last block of a layer: the next layer's first chain can already run over
   // the K-steps the earlier blocks produced (2 per block); only the last two
   // wait for this step's epilogue.
   constexpr int EARLY = (t + 1 < T && !same) ? 2 * mb : 0;
   if constexpr (EARLY > 0)
-    chain<0, EARLY, NB>(c.acc[(t + 1) & 1], c.fr[(t + 1) & 1], c.template in<(l + 1) % N::L>());
+    chain<0, EARLY, NB>(c.acc[(t + 1) & 1], c.fr, c.template in<(l + 1) % N::L>());
   if constexpr (l == 0 && (same ? t + 1 == N::mbs(0) - 1 : t == 0)) {
     // Every MFMA that reads x has been issued: refill xa with the next block's
     // rows (past the end the resource is empty and the refill reads zeros).
@@ -351,25 +359,21 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
     if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
   }
   if constexpr (t + 1 < T && !same)
-    chain<EARLY, N::ks(l + 1), NB>(c.acc[(t + 1) & 1], c.fr[(t + 1) & 1], c.template in<l + 1>());
-  if constexpr (t + 1 < T) step<N, t + 1, NB, STASH, STAGE, KSM>(p, io, c, lds_b, lane_off, next, lane);
+    chain<EARLY, N::ks(l + 1), NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l + 1>());
+  if constexpr (t + 1 < T) step<N, t + 1, NB, STASH, STAGE, KSM, RF>(p, io, c, lds_b, lane_off, next, lane);
 }
 
 // One row block: the whole layer chain, stores, and the x refill for block
-// `next`.  On entry c.xa holds the block's x rows and c.fr[0], c.fr[1] the
-// first two steps' fragments.
-template <class N, int NB, bool STASH, bool STAGE, int KSM>
+// `next`.  On entry c.xa holds the block's x rows.
+template <class N, int NB, bool STASH, bool STAGE, int KSM, int RF>
 __device__ __forceinline__ void fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
                                           int lane_off, i32x4* stage, int64_t b, int64_t next, int lane) {
   constexpr int ROWS = 32 * NB;
   BlockIO io = block_io<N, STASH, ROWS>(p, b * ROWS);
   io.stage = stage;
-  if constexpr (Steps<N>::count() % 2 != 0) {  // no wrap-around prefetch: load here
-    load_frags<N, 0, KSM>(c.fr[0], lds_b, lane_off);
-    if constexpr (Steps<N>::count() > 1) load_frags<N, 1, KSM>(c.fr[1], lds_b, lane_off);
-  }
-  chain<0, N::ks(0), NB>(c.acc[0], c.fr[0], c.xa);
-  step<N, 0, NB, STASH, STAGE, KSM>(p, io, c, lds_b, lane_off, next, lane);
+  load_frags<N, 0, KSM, RF>(c.fr, lds_b, lane_off, c.rf);
+  chain<0, N::ks(0), NB>(c.acc[0], c.fr, c.xa);
+  step<N, 0, NB, STASH, STAGE, KSM, RF>(p, io, c, lds_b, lane_off, next, lane);
 }
 
 // Persistent forward.  Workgroup b owns row blocks b, b + G, b + 2G, ...
@@ -384,19 +388,21 @@ template <class N, int NB, bool STASH, int NW, int D>
 __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   static_assert(N::valid(), "unsupported widths");
   static_assert(D >= 1 && D <= 4, "prefetch depth");
+  using Plan = LdsPlan<N, NB, NW>;
   constexpr int KSM = N::ksmax();
   constexpr int KS0 = N::ks(0);
   constexpr int ROWS = 32 * NB;
-  constexpr bool STAGE = OutStage<N, NB, NW>::enabled;
-  constexpr int TC = OutStage<N, NB, NW>::kTileChunks;
-  __shared__ f16x8 lds[N::nfrag() * 64];
+  constexpr bool STAGE = Plan::stage;
+  constexpr int TC = Plan::kTileChunks;
+  constexpr int RF = Plan::reg_frags;
+  constexpr bool CLAIM = Plan::claim;
+  __shared__ f16x8 lds[(N::nfrag() - RF) * 64];
   __shared__ i32x4 stage_tiles[STAGE ? NW * TC : 1];
-  constexpr bool CLAIM = Claim<N, NB, NW>::enabled;
   unsigned int* const claim_ctr = ClaimSlot<CLAIM>::get();
   if constexpr (CLAIM) {
     if (threadIdx.x == 0) *claim_ctr = 0;
   }
-  stage_weights<N, NW * 64>(p, lds);
+  stage_weights<N, NW * 64, RF>(p, lds);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -427,24 +433,21 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   // Past the end a block's resource is empty: its prefetch reads zeros.
   static_assert(D == 1, "one block of x rows in flight per wave");
   Chain<N, NB, KSM> c;
+  c.rf = RF ? weight_fragment<N>(p, 0, 0, lane) : f16x8{};
   const char* lds_b = reinterpret_cast<const char*>(lds);
   const int lane_off = lane * 16;  // this lane's 16 bytes within a 1 KiB fragment
   int64_t b = claim();
   if (b >= nblk) return;  // no barrier follows
   load_rows<KS0, NB>(c.xa, block_io<N, false, ROWS>(p, b * ROWS).x, lane & 31, lane >> 5);
-  if constexpr (Steps<N>::count() % 2 == 0) {
-    load_frags<N, 0, KSM>(c.fr[0], lds_b, lane_off);
-    load_frags<N, 1, KSM>(c.fr[1], lds_b, lane_off);
-  }
   // The first block is peeled so that the loop header is entered from two
   // paths with the same outstanding memory operations (the x refill, then
   // stores): vmcnt counts loads and stores in issue order.
   int64_t next = claim();
-  fwd_block<N, NB, STASH, STAGE, KSM>(p, c, lds_b, lane_off, stage, b, next, lane);
+  fwd_block<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
   // Claims are increasing per wave, so once one is past the end all later are.
   for (b = next; b < nblk; b = next) {
     next = claim();
-    fwd_block<N, NB, STASH, STAGE, KSM>(p, c, lds_b, lane_off, stage, b, next, lane);
+    fwd_block<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
   }
 }
 
@@ -498,9 +501,11 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
   return MLPMK_OK;
 }
 
-template <class N, int NB, int NW, int D>
+// NW waves per workgroup for inference, NWS with the fp32 stash (whose extra
+// address registers would spill at NW = 12 for the 3-layer network).
+template <class N, int NB, int NW, int NWS, int D>
 static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
-  return stash ? launch_fwd<N, NB, true, NW, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
+  return stash ? launch_fwd<N, NB, true, NWS, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
 }
 
 bool fwd_supported_dims(int L, const int* dims) {
@@ -509,9 +514,9 @@ bool fwd_supported_dims(int L, const int* dims) {
 }
 
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
-  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 8, 1>(p, stash, st);
-  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 8, 1>(p, stash, st);
-  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 8, 1>(p, stash, st);
+  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 8, 1>(p, stash, st);
+  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 12, 1>(p, stash, st);
+  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 1, 16, 16, 1>(p, stash, st);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
 }
 

@@ -126,8 +126,8 @@ def test_python_wrappers_validate_before_the_library():
 def test_drop_in_modules_import_without_gpu():
     import kernel
 
-    assert kernel._pick_config(4096, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 8)
-    assert kernel._pick_config(4096, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 8)
+    assert kernel._pick_config(4096, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 12)
+    assert kernel._pick_config(4096, 32, 64, 64, 16) == (32, 16, 16, 16, 16, 16)
     with pytest.raises(TypeError):
         kernel._pick_config(4096, 128, 128, 128, 128, fp32=True)
     assert callable(kernel._fused_mlp_fwd) and kernel.Model and kernel.ModelNew
