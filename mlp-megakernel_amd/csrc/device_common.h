@@ -82,15 +82,17 @@ __host__ __device__ constexpr int outfeat(int mb, int i) {
 // equals z to fp32 rounding (the 2^-|u| term is below 3e-9), which is the
 // reference's threshold branch (kernel.py:108).  One v_exp_f32 and one
 // v_log_f32 (hardware base-2 transcendentals), no range reduction needed.
-__device__ __forceinline__ float sp2(float u) {
-  float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(u));
-  float l = __builtin_amdgcn_logf(1.0f + e);
-  // med3 with a finite upper bound stays one v_med3_f32; an infinite bound is
-  // rewritten to max(), which IEEE mode precedes with a canonicalising v_max
-  // of the MFMA result (one extra VALU op per element).  The two differ only
-  // for u = +inf, where FLT_MAX still rounds to fp16 +inf.
-  return __builtin_amdgcn_fmed3f(u, 0.0f, 3.40282347e38f) + l;
+// sp2_tail is the bounded second term; the kernels add max(u, 0) themselves
+// (sp2_pack8 on packed fp16, the fp32 stash with sp2_relu).
+__device__ __forceinline__ float sp2_tail(float u) {
+  return __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(-__builtin_fabsf(u)));
 }
+
+// max(u, 0) as one v_med3_f32: an infinite upper bound is rewritten to max(),
+// which IEEE mode precedes with a canonicalising v_max of the MFMA result (one
+// extra VALU op per element).  The two differ only for u = +inf, where FLT_MAX
+// still rounds to fp16 +inf.
+__device__ __forceinline__ float sp2_relu(float u) { return __builtin_amdgcn_fmed3f(u, 0.0f, 3.40282347e38f); }
 
 __device__ __forceinline__ f16x2 cvt2(float a, float b) {
   return __builtin_convertvector((f32x2){a, b}, f16x2);  // v_cvt_pk_f16_f32 (RNE)
@@ -101,6 +103,23 @@ __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, f
   f16x2 p0 = cvt2(a0, a1), p1 = cvt2(a2, a3), p2 = cvt2(a4, a5), p3 = cvt2(a6, a7);
   f16x4 q0 = __builtin_shufflevector(p0, p1, 0, 1, 2, 3);
   f16x4 q1 = __builtin_shufflevector(p2, p3, 0, 1, 2, 3);
+  return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// sp2 of eight values as the next layer's fp16 operand, from u and its tail
+// l = sp2_tail(u): the max and the add run on packed halves (v_pk_max_f16,
+// v_pk_add_f16), so a pair of values costs 2 exp, 2 add, 2 log, 2 pack, 1 max
+// and 1 add -- one VALU operation less than max and add in fp32 followed by a
+// pack.  u and l are each rounded to fp16 before the fp16 add: at most ~1.5
+// fp16 ulp from the exact value instead of 0.5 ulp, far inside the 1e-2
+// tolerance of the outputs.
+__device__ __forceinline__ f16x8 sp2_pack8(const float* u, const float* l) {
+  f16x2 r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = __builtin_elementwise_max(cvt2(u[2 * i], u[2 * i + 1]), (f16x2){}) + cvt2(l[2 * i], l[2 * i + 1]);
+  f16x4 q0 = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3);
+  f16x4 q1 = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3);
   return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 

@@ -19,8 +19,8 @@
 //  * Activations run in base-2 units: W_1 is staged pre-scaled by log2(e) and
 //    W_L by ln(2), hidden layers chain with no scaling at all (ln2 and log2e
 //    cancel between W^T h' and the next exp2), so the epilogue is exp2, add,
-//    log2, max, add and a pack per element.  The stash stores natural-unit
-//    h = ln2 * h'.
+//    log2 per element in fp32, then pack, max and add on packed fp16 halves
+//    (see sp2_pack8).  The stash stores natural-unit h = ln2 * h' in fp32.
 //  * Each layer is software-pipelined by 32-feature output block: the MFMA
 //    chain of block mb+1 is issued ahead of block mb's activation, so the
 //    matrix core and the VALU work concurrently within one wave.
@@ -253,14 +253,18 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       if (hi_ok)
         buf_store16<kStreamStore>(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
     } else {
-      float v[16];
+      // log2 e is folded into the staged W_1, so acc is u in base-2 units.
+      float u[16], t[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = sp2(acc[nb][e]);  // log2 e is folded into the staged W_1
+      for (int e = 0; e < 16; ++e) {
+        u[e] = acc[nb][e];
+        t[e] = sp2_tail(u[e]);
+      }
       if constexpr (STASH) {
         const rsrc_t sr = io.stash[l];
         float h[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) h[e] = v[e] * kLn2;
+        for (int e = 0; e < 16; ++e) h[e] = (sp2_relu(u[e]) + t[e]) * kLn2;
         if (lo_ok) {
           buf_store16<kStreamStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
           buf_store16<kStreamStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
@@ -270,9 +274,8 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
           buf_store16<kStreamStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
         }
       }
-      if (2 * mb < KSM) nxt[2 * mb][nb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-      if (2 * mb + 1 < KSM)
-        nxt[2 * mb + 1][nb] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+      if (2 * mb < KSM) nxt[2 * mb][nb] = sp2_pack8(u, t);
+      if (2 * mb + 1 < KSM) nxt[2 * mb + 1][nb] = sp2_pack8(u + 8, t + 8);
     }
   }
 }
@@ -502,7 +505,7 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
 }
 
 // NW waves per workgroup for inference, NWS with the fp32 stash (whose extra
-// address registers would spill at NW = 12 for the 3-layer network).
+// registers would spill at NW = 12 for the 128-wide networks).
 template <class N, int NB, int NW, int NWS, int D>
 static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
   return stash ? launch_fwd<N, NB, true, NWS, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
@@ -515,7 +518,7 @@ bool fwd_supported_dims(int L, const int* dims) {
 
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
   if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 8, 1>(p, stash, st);
-  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 12, 1>(p, stash, st);
+  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 8, 1>(p, stash, st);
   if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 1, 16, 16, 1>(p, stash, st);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
 }
