@@ -12,6 +12,8 @@ oracle on the host cores, bounded sample).  ``--config`` / ``--m`` select
 other BASELINE configs, ``--sweep`` adds the latency sweep M = 64..4096.
 """
 import argparse
+import contextlib
+import gc
 import json
 import os
 import sys
@@ -55,22 +57,44 @@ def make_device_inputs(torch, dims, m, seed, uniform):
     return x, ws
 
 
-def ramp_clock(torch, fn, seconds=0.4):
-    """Untimed back-to-back launches for `seconds`: the GPU starts a process at
-    a low shader clock (about 1 GHz measured with s_memtime/s_memrealtime) and
-    needs a few hundred ms of load to reach its sustained clock."""
+@contextlib.contextmanager
+def gc_paused():
+    """Python's garbage collector off for the block (as timeit does), after
+    one collection up front: a generation-2 collection with torch loaded
+    stalls the launching thread for 25-40 ms, long enough for the GPU to
+    drain its queue in the middle of a timed region, and a collection between
+    the clock ramp and the timed launches idles the GPU long enough for its
+    clock to drop again."""
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
+
+
+def ramp_clock(torch, fn, seconds=0.1):
+    """Untimed back-to-back launches for about `seconds`, enqueued without
+    host synchronisation, so that the timed launches do not start from the
+    idle shader clock (~150 launches of the 3-layer forward to settle).  Kept
+    short: under seconds of continuous load the MI355X power management
+    lowers the clock (measured: the 3-layer forward drifts from ~127 to
+    ~140 us per launch over 0.5 s)."""
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    i = 0
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(20):
-            fn(i)
-            i += 1
-        torch.cuda.synchronize()
+    for i in range(10):
+        fn(i)
+    torch.cuda.synchronize()
+    per_launch = max((time.perf_counter() - t0) / 10, 1e-6)
+    for i in range(min(int(seconds / per_launch), 20000)):
+        fn(i)
+    torch.cuda.synchronize()
 
 
 def time_launches(torch, fn, steps, warmup):
     """Average ms per launch over `steps` back-to-back launches, bracketed by
-    HIP events on the launch stream (torch's current stream)."""
+    HIP events on the launch stream (torch's current stream).  Callers run it
+    inside gc_paused()."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -196,8 +220,9 @@ def train_step_bench(torch, m, steps=50, warmup=10):
         model.g_all.grad = None
         model(x).sum().backward()
 
-    ramp_clock(torch, step, seconds=0.2)
-    ms = time_launches(torch, step, steps, warmup)
+    with gc_paused():
+        ramp_clock(torch, step, seconds=0.2)
+        ms = time_launches(torch, step, steps, warmup)
     return {
         "ms_per_step": round(ms, 5),
         "rows_per_s": m / (ms * 1e-3),
@@ -277,8 +302,9 @@ def main():
     )
 
     # --- timed region -------------------------------------------------------
-    ramp_clock(torch, step)
-    ms = time_launches(torch, step, args.steps, args.warmup)
+    with gc_paused():
+        ramp_clock(torch, step)
+        ms = time_launches(torch, step, args.steps, args.warmup)
     nbytes, nflops = algorithmic(dims, m)
     achieved_gbs = nbytes / (ms * 1e-3) / 1e9
     tflops = nflops / (ms * 1e-3) / 1e12
@@ -298,7 +324,8 @@ def main():
     # achievable-HBM reference: the library's 16-byte copy over 512 MiB
     src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
-    cms = time_launches(torch, lambda i: ops.copy_bytes(src, dst), 20, 5)
+    with gc_paused():
+        cms = time_launches(torch, lambda i: ops.copy_bytes(src, dst), 20, 5)
     copy_gbs = 2 * src.numel() / (cms * 1e-3) / 1e9
     del src, dst
 
@@ -330,8 +357,9 @@ def main():
         for ms_m in (64, 128, 256, 512, 1024, 2048, 4096):
             xx, ww = make_device_inputs(torch, dims, ms_m, seed=0, uniform=uniform)
             oo = torch.empty((ms_m, dims[-1]), device="cuda", dtype=torch.float16)
-            ev = time_launches(torch, lambda i: ops.fwd_into(xx, ww, oo), 200, 20)
-            gr = time_graph(torch, lambda i: ops.fwd_into(xx, ww, oo))
+            with gc_paused():
+                ev = time_launches(torch, lambda i: ops.fwd_into(xx, ww, oo), 200, 20)
+                gr = time_graph(torch, lambda i: ops.fwd_into(xx, ww, oo))
             sweep[str(ms_m)] = {"event_ms": round(ev, 5), "graph_ms": round(gr, 5)}
         result["latency_sweep"] = sweep
 
