@@ -266,12 +266,12 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
 #pragma unroll
         for (int e = 0; e < 16; ++e) h[e] = (sp2_relu(u[e]) + t[e]) * kLn2;
         if (lo_ok) {
-          buf_store16<kStreamStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
-          buf_store16<kStreamStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
+          buf_store16<kStashStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
+          buf_store16<kStashStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
         }
         if (hi_ok) {
-          buf_store16<kStreamStore>((f32x4){h[8], h[9], h[10], h[11]}, sr, elem * 4 + 64);
-          buf_store16<kStreamStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
+          buf_store16<kStashStore>((f32x4){h[8], h[9], h[10], h[11]}, sr, elem * 4 + 64);
+          buf_store16<kStashStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
         }
       }
       if (2 * mb < KSM) nxt[2 * mb][nb] = sp2_pack8(u, t);

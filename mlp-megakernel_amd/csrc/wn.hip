@@ -51,6 +51,12 @@ __device__ __forceinline__ float wn_colsum(float part, float (&red)[kWnRowGroups
   return t;
 }
 
+// Rows per thread held in registers: every load of a column chunk is issued
+// before the first use, so a launch costs about two memory round trips (read
+// v, write w) instead of one per row; widths above kWnRowGroups * kWnRegRows
+// loop over chunks.
+constexpr int kWnRegRows = 16;
+
 template <class P>
 __global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const P* __restrict__ v,
                                                             const P* __restrict__ g, f16* __restrict__ w,
@@ -63,17 +69,32 @@ __global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const 
   const bool col = j < N;  // out widths are multiples of 16: a block may be half used
   const int64_t base = lay.v_off[l] + j;
   float ss = 0.0f;
-  if (col)
-    for (int k = rg; k < K; k += kWnRowGroups) {
-      const float t = ldp(v, base + (int64_t)k * N);
-      ss = fmaf(t, t, ss);
+  float t[kWnRegRows];
+  if (col) {
+    for (int k0 = 0; k0 < K; k0 += kWnRowGroups * kWnRegRows) {
+#pragma unroll
+      for (int i = 0; i < kWnRegRows; ++i) {
+        const int k = k0 + rg + i * kWnRowGroups;
+        t[i] = k < K ? ldp(v, base + (int64_t)k * N) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kWnRegRows; ++i) ss = fmaf(t[i], t[i], ss);
     }
+  }
   const float inv = 1.0f / sqrtf(wn_colsum(ss, red, c, rg));
   if (!col) return;  // after the only barrier
   const float scale = ldp(g + lay.g_off[l], j) * inv;
-  for (int k = rg; k < K; k += kWnRowGroups) {
-    const int64_t e = base + (int64_t)k * N;
-    w[e] = (f16)(ldp(v, e) * scale);
+  if (K <= kWnRowGroups * kWnRegRows) {  // the column chunk is still in registers
+#pragma unroll
+    for (int i = 0; i < kWnRegRows; ++i) {
+      const int k = rg + i * kWnRowGroups;
+      if (k < K) w[base + (int64_t)k * N] = (f16)(t[i] * scale);
+    }
+  } else {
+    for (int k = rg; k < K; k += kWnRowGroups) {
+      const int64_t e = base + (int64_t)k * N;
+      w[e] = (f16)(ldp(v, e) * scale);
+    }
   }
   if (rg == 0) inv_norm[lay.g_off[l] + j] = inv;
 }
@@ -91,19 +112,37 @@ __global__ __launch_bounds__(kWnThreads) void wn_bwd_kernel(WnLayout lay, const 
   const bool col = j < N;
   const int64_t base = lay.v_off[l] + j;
   float dot = 0.0f;  // <dW_j, v_j>
-  if (col)
-    for (int k = rg; k < K; k += kWnRowGroups) {
-      const int64_t e = base + (int64_t)k * N;
-      dot = fmaf(dw[e], ldp(v, e), dot);
+  float tw[kWnRegRows], tv[kWnRegRows];
+  if (col) {
+    for (int k0 = 0; k0 < K; k0 += kWnRowGroups * kWnRegRows) {
+#pragma unroll
+      for (int i = 0; i < kWnRegRows; ++i) {
+        const int k = k0 + rg + i * kWnRowGroups;
+        const int64_t e = base + (int64_t)k * N;
+        tw[i] = k < K ? dw[e] : 0.0f;
+        tv[i] = k < K ? ldp(v, e) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kWnRegRows; ++i) dot = fmaf(tw[i], tv[i], dot);
     }
+  }
   dot = wn_colsum(dot, red, c, rg);
   if (!col) return;  // after the only barrier
   const float inv = inv_norm[lay.g_off[l] + j];
   const float dgj = dot * inv;  // <dW_j, u_j>, u = v * inv
   const float gs = ldp(g + lay.g_off[l], j) * inv;
-  for (int k = rg; k < K; k += kWnRowGroups) {
-    const int64_t e = base + (int64_t)k * N;
-    dv[e] = (P)(gs * (dw[e] - dgj * ldp(v, e) * inv));
+  const float vs = dgj * inv;
+  if (K <= kWnRowGroups * kWnRegRows) {  // the column chunk is still in registers
+#pragma unroll
+    for (int i = 0; i < kWnRegRows; ++i) {
+      const int k = rg + i * kWnRowGroups;
+      if (k < K) dv[base + (int64_t)k * N] = (P)(gs * (tw[i] - vs * tv[i]));
+    }
+  } else {
+    for (int k = rg; k < K; k += kWnRowGroups) {
+      const int64_t e = base + (int64_t)k * N;
+      dv[e] = (P)(gs * (dw[e] - vs * ldp(v, e)));
+    }
   }
   if (rg == 0) dg[lay.g_off[l] + j] = (P)dgj;
 }
