@@ -78,7 +78,8 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
 
 /*
  * Backward megakernel (one launch): data gradients with MFMA, weight gradients
- * as split-K partials reduced in LDS and then added with global fp32 atomics.
+ * as split-K partials reduced in LDS and then added with global fp32 atomics
+ * by every workgroup.  mlpmk_bwd_ws below is the faster form.
  *
  * Replaces the fused backward of the reference's `FusedMLPSoftplus` autograd
  * function (/root/reference/mlp_fused.md:88-112, README.md:32) -- the file that
@@ -97,6 +98,32 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
 int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
               const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
               float* const* dw, int64_t M, void* stream);
+
+/*
+ * mlpmk_bwd with a caller-provided device workspace (same arguments and
+ * results; replaces the same reference interface).  Each workgroup of the
+ * backward megakernel stores its weight-gradient partial sums in the
+ * workspace with plain stores, and a second kernel on the same stream sums
+ * them into dw (+=, one thread per element, no atomics) instead of every
+ * workgroup adding its partials with fp32 atomics: device-wide fp32 atomics
+ * run at ~270 M elements/s, and that flush cost ~45-65 us at M = 131072
+ * (256 workgroups x 49152 dW elements).  Grids below 64 workgroups (small M)
+ * keep the atomic flush, which is then cheaper, and leave the workspace
+ * untouched.
+ *   workspace        device memory, 16-byte aligned, at least the size that
+ *                    mlpmk_bwd_workspace_size reports for the same
+ *                    (num_layers, dims, M, dx != NULL) on the current device;
+ *                    free again once both launches have run (stream order)
+ */
+int mlpmk_bwd_ws(int num_layers, const int* dims, const void* x, const void* const* w,
+                 const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+                 float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream);
+
+/*
+ * Bytes of workspace mlpmk_bwd_ws needs on the current device: one fp32 copy
+ * of all dW blocks per workgroup of the backward grid (0 when M == 0).
+ */
+int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int64_t M, int with_dx, int64_t* bytes);
 
 /*
  * Weight-norm forward for all layers in ONE launch:

@@ -16,6 +16,7 @@ bool fwd_supported_dims(int L, const int* dims);
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st);
 bool bwd_supported_dims(int L, const int* dims);
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st);
+int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes);
 int wn_fwd_dispatch(int L, const int* dims, int dtype, const void* v, const void* g, void* w_out,
                     float* inv_norm, hipStream_t st);
 int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const void* v, const void* g,
@@ -153,10 +154,9 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
   return fwd_dispatch(num_layers, dims, p, stash != nullptr, static_cast<hipStream_t>(stream));
 }
 
-int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
-              const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
-              float* const* dw, int64_t M, void* stream) {
-  g_last_error[0] = 0;
+static int bwd_common(int num_layers, const int* dims, const void* x, const void* const* w,
+                      const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+                      float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream) {
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
@@ -198,7 +198,45 @@ int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const*
   p.dout_stride = dout_row_stride;
   p.dx = static_cast<_Float16*>(dx);
   p.M = M;
+  if (workspace) {
+    if ((rc = check_ptr(workspace, "workspace"))) return rc;
+    int64_t need = 0;
+    if ((rc = bwd_workspace_bytes(num_layers, dims, M, dx != nullptr, &need))) return rc;
+    if (workspace_bytes < need)
+      return fail(MLPMK_ERR_INVALID_ARG, "workspace_bytes=%lld is below the %lld bytes needed",
+                  (long long)workspace_bytes, (long long)need);
+    p.part = static_cast<float*>(workspace);
+  }
   return bwd_dispatch(num_layers, dims, p, static_cast<hipStream_t>(stream));
+}
+
+int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
+              const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+              float* const* dw, int64_t M, void* stream) {
+  g_last_error[0] = 0;
+  return bwd_common(num_layers, dims, x, w, stash, dout, dout_row_stride, dx, dw, nullptr, 0, M, stream);
+}
+
+int mlpmk_bwd_ws(int num_layers, const int* dims, const void* x, const void* const* w,
+                 const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+                 float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream) {
+  g_last_error[0] = 0;
+  if (!workspace) return fail(MLPMK_ERR_INVALID_ARG, "workspace is NULL");
+  return bwd_common(num_layers, dims, x, w, stash, dout, dout_row_stride, dx, dw, workspace, workspace_bytes,
+                    M, stream);
+}
+
+int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int64_t M, int with_dx, int64_t* bytes) {
+  g_last_error[0] = 0;
+  if (!bytes) return fail(MLPMK_ERR_INVALID_ARG, "bytes is NULL");
+  *bytes = 0;
+  int rc = check_dims(num_layers, dims);
+  if (rc) return rc;
+  if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
+  if (!bwd_supported_dims(num_layers, dims))
+    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+  if (M == 0) return MLPMK_OK;
+  return bwd_workspace_bytes(num_layers, dims, M, with_dx != 0, bytes);
 }
 
 static int check_wn(int num_layers, const int* dims, int dtype) {

@@ -27,6 +27,11 @@ struct BwdParams {
   _Float16* dx;                        // nullable
   float* dw[kMaxLayersHost];           // fp32 [d[l], d[l+1]], accumulated with atomics
   int64_t M;
+  // Null: every workgroup adds its weight-gradient partial sums to dw with
+  // fp32 atomics.  Otherwise workgroup b stores them, laid out like the dW
+  // blocks back to back, at part + b * (sum_l d[l] * d[l+1]), and a second
+  // kernel sums the partials into dw.
+  float* part;
 };
 
 }  // namespace mlpmk

@@ -6,6 +6,8 @@ device.  Validation errors of the library surface as ``MlpmkError``.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -122,12 +124,25 @@ def fwd(x, weights, stash=False):
     return (out, hs) if stash else out
 
 
-def bwd(x, weights, stash, dout, dws, dx=None):
+def bwd_workspace_bytes(dims, M, with_dx):
+    """Bytes of workspace ``mlpmk_bwd_ws`` needs on the current device."""
+    lib = _lib.get()
+    pd, _k = _lib.int_array(dims)
+    out = ctypes.c_int64(0)
+    _check("mlpmk_bwd_workspace_size", lib.mlpmk_bwd_workspace_size(len(dims) - 1, pd, M, int(with_dx), ctypes.byref(out)))
+    return out.value
+
+
+def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     """Backward megakernel: accumulates fp32 weight gradients into ``dws``
     (callers zero them first) and writes ``dx`` if given.
 
     ``dout`` is [M, OUT] fp16 with unit column stride; a row stride of 0
     (``t.expand(M, OUT)`` of one row) is passed through as a broadcast.
+    With ``workspace`` (default) the weight-gradient partials of the
+    workgroups go through a workspace from torch's allocator and a second
+    kernel (``mlpmk_bwd_ws``); otherwise every workgroup adds its partials
+    with fp32 atomics (``mlpmk_bwd``).
     """
     dev = x.device
     _require(x, "x", torch.float16, dev)
@@ -160,11 +175,20 @@ def bwd(x, weights, stash, dout, dws, dx=None):
     ps, _k3 = _lib.ptr_array([s.data_ptr() for s in stash])
     pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
     with torch.cuda.device(dev):
-        rc = lib.mlpmk_bwd(
-            len(weights), pd, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
-            dx.data_ptr() if dx is not None else None, pg, M, _stream(dev),
-        )
-    _check("mlpmk_bwd", rc)
+        dxp = dx.data_ptr() if dx is not None else None
+        if workspace and M > 0:
+            nbytes = bwd_workspace_bytes(dims, M, dx is not None)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            rc = lib.mlpmk_bwd_ws(
+                len(weights), pd, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride, dxp, pg,
+                ws.data_ptr(), nbytes, M, _stream(dev),
+            )
+            _check("mlpmk_bwd_ws", rc)
+        else:
+            rc = lib.mlpmk_bwd(
+                len(weights), pd, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride, dxp, pg, M, _stream(dev),
+            )
+            _check("mlpmk_bwd", rc)
     return dws, dx
 
 

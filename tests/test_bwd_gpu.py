@@ -35,7 +35,7 @@ def check_dw(got, ref, what):
     return frob
 
 
-def run_train(dims, m, seed, *, dout_mode="ones", with_dx=True, x_dist="normal"):
+def run_train(dims, m, seed, *, dout_mode="ones", with_dx=True, x_dist="normal", workspace=True):
     x, ws = orc.make_inputs(dims, m, seed=seed, x_dist=x_dist)
     xd = torch.from_numpy(x).cuda()
     wd = [torch.from_numpy(w).cuda() for w in ws]
@@ -53,7 +53,7 @@ def run_train(dims, m, seed, *, dout_mode="ones", with_dx=True, x_dist="normal")
         dout = torch.from_numpy(dout_np).cuda()
     dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(len(dims) - 1)]
     dx = torch.empty_like(xd) if with_dx else None
-    ops.bwd(xd, wd, hs, dout, dws, dx)
+    ops.bwd(xd, wd, hs, dout, dws, dx, workspace=workspace)
     torch.cuda.synchronize()
     _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
     rdws, rdx = orc.backward(x, ws, ref_h, dout_np.astype(np.float32), need_dx=with_dx)
@@ -131,3 +131,54 @@ def test_zero_dout_gives_zero_gradients():
     ops.bwd(xd, wd, hs, dout, dws, dx)
     assert all(float(d.abs().max()) == 0.0 for d in dws)
     assert float(dx.abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dims,m", [(D3, 4096), (D3, 131072), (NARROW, 65536)])
+def test_atomic_flush_path_matches_oracle(dims, m):
+    # mlpmk_bwd (every workgroup adds its partials with fp32 atomics) next to
+    # the workspace path the other tests take.
+    _, _, dws, dx, rdws, rdx = run_train(dims, m, seed=21, workspace=False)
+    for i in range(len(dws)):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} (atomics)")
+    ok, err, _ = orc.allclose_report(dx.float().cpu().numpy(), rdx, 1e-2, 1e-2)
+    assert ok, f"dx (atomics): {err}"
+
+
+def test_workspace_and_atomic_paths_agree():
+    # Same inputs through both reductions: equal up to fp32 summation order.
+    x, ws = orc.make_inputs(D3, 65536, seed=5)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dout = torch.ones((1, 128), dtype=torch.float16, device="cuda").expand(65536, 128)
+    a = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+    b = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+    ops.bwd(xd, wd, hs, dout, a, workspace=True)
+    ops.bwd(xd, wd, hs, dout, b, workspace=False)
+    torch.cuda.synchronize()
+    for i in range(3):
+        scale = b[i].abs().max().item()
+        assert torch.allclose(a[i], b[i], rtol=1e-5, atol=1e-6 * scale), f"dW{i + 1}"
+
+
+def test_workspace_too_small_is_rejected():
+    import ctypes
+    from mlpmk import _lib
+    x, ws = orc.make_inputs(D3, 4096, seed=6)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dout = torch.ones((1, 128), dtype=torch.float16, device="cuda").expand(4096, 128)
+    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+    need = ops.bwd_workspace_bytes(list(D3), 4096, False)
+    assert need > 0 and need % (4 * 49152) == 0
+    buf = torch.empty(need, dtype=torch.uint8, device="cuda")
+    lib = _lib.get()
+    pd, _k1 = _lib.int_array(list(D3))
+    pw, _k2 = _lib.ptr_array([w.data_ptr() for w in wd])
+    ps, _k3 = _lib.ptr_array([h.data_ptr() for h in hs])
+    pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
+    rc = lib.mlpmk_bwd_ws(3, pd, xd.data_ptr(), pw, ps, dout.data_ptr(), 0, None, pg, buf.data_ptr(), need - 16,
+                          4096, torch.cuda.current_stream().cuda_stream)
+    assert rc == 1 and b"workspace_bytes" in lib.mlpmk_last_error()
+    assert all(d.abs().max().item() == 0 for d in dws)  # nothing launched
