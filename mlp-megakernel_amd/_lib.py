@@ -75,11 +75,22 @@ def get():
     return _lib
 
 
+_int_arrays = {}
+
+
 def int_array(vals):
-    arr = (c_int * len(vals))(*[int(v) for v in vals])
-    return ctypes.cast(arr, P_INT), arr
+    """A C int array of ``vals`` (cached per distinct tuple: the library only
+    reads it).  Returns ``(array, keepalive)``; ctypes passes an array where
+    the signature wants a pointer to its element type."""
+    key = tuple(int(v) for v in vals)
+    arr = _int_arrays.get(key)
+    if arr is None:
+        arr = (c_int * len(key))(*key)
+        _int_arrays[key] = arr
+    return arr, arr
 
 
 def ptr_array(ptrs):
-    arr = (c_void_p * len(ptrs))(*[c_void_p(int(p)) if p else None for p in ptrs])
-    return ctypes.cast(arr, P_VOIDP), arr
+    """A C array of device pointers (None for NULL); ``(array, keepalive)``."""
+    arr = (c_void_p * len(ptrs))(*ptrs)
+    return arr, arr
