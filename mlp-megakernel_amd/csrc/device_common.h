@@ -83,22 +83,20 @@ __host__ __device__ constexpr int outfeat(int mb, int i) {
   return 32 * mb + 16 * ((i >> 3) >> 1) + 8 * ((i >> 2) & 1) + 4 * ((i >> 3) & 1) + (i & 3);
 }
 
-// Softplus in base-2 units: sp2(u) = log2(1 + 2^u) = max(u, 0) + log2(1 + 2^-|u|).
-// For u = z*log2(e): softplus(z) = ln2 * sp2(u) for every z, and for z > 20 it
-// equals z to fp32 rounding (the 2^-|u| term is below 3e-9), which is the
-// reference's threshold branch (kernel.py:108).  One v_exp_f32 and one
-// v_log_f32 (hardware base-2 transcendentals), no range reduction needed.
-// sp2_tail is the bounded second term; the kernels add max(u, 0) themselves
-// (sp2_pack8 on packed fp16, the fp32 stash with sp2_relu).
-__device__ __forceinline__ float sp2_tail(float u) {
-  return __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(-__builtin_fabsf(u)));
+// Softplus in base-2 units: sp2(u) = log2(1 + 2^u).  For u = z*log2(e):
+// softplus(z) = ln2 * sp2(u) for every z.  Evaluated directly -- one v_exp_f32,
+// one add, one v_log_f32 (hardware base-2 transcendentals) -- it is within a
+// few fp32 ulp of the exact value wherever 2^u is finite: for u <= 0 the
+// rounding of 1 + 2^u costs at most 2^-24 absolute, for u > 0 at most 2^-24
+// relative, and for u >= 24 the result is u itself.  For u >= 128, 2^u
+// overflows and the result is +inf instead of u; callers detect that with
+// sp2_overflow and then substitute u, which is the reference's threshold
+// branch (kernel.py:108: z for z > 20, where the two agree to fp32 rounding).
+__device__ __forceinline__ float sp2(float u) {
+  return __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(u));
 }
-
-// max(u, 0) as one v_med3_f32: an infinite upper bound is rewritten to max(),
-// which IEEE mode precedes with a canonicalising v_max of the MFMA result (one
-// extra VALU op per element).  The two differ only for u = +inf, where FLT_MAX
-// still rounds to fp16 +inf.
-__device__ __forceinline__ float sp2_relu(float u) { return __builtin_amdgcn_fmed3f(u, 0.0f, 3.40282347e38f); }
+// Replaces an overflowed sp2 by u (u >= 128); every other value is kept as is.
+__device__ __forceinline__ float sp2_fix(float u, float s) { return u >= 128.0f ? u : s; }
 
 __device__ __forceinline__ f16x2 cvt2(float a, float b) {
   return __builtin_convertvector((f32x2){a, b}, f16x2);  // v_cvt_pk_f16_f32 (RNE)
@@ -112,21 +110,21 @@ __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, f
   return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// sp2 of eight values as the next layer's fp16 operand, from u and its tail
-// l = sp2_tail(u): the max and the add run on packed halves (v_pk_max_f16,
-// v_pk_add_f16), so a pair of values costs 2 exp, 2 add, 2 log, 2 pack, 1 max
-// and 1 add -- one VALU operation less than max and add in fp32 followed by a
-// pack.  u and l are each rounded to fp16 before the fp16 add: at most ~1.5
-// fp16 ulp from the exact value instead of 0.5 ulp, far inside the 1e-2
-// tolerance of the outputs.
-__device__ __forceinline__ f16x8 sp2_pack8(const float* u, const float* l) {
-  f16x2 r[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = __builtin_elementwise_max(cvt2(u[2 * i], u[2 * i + 1]), (f16x2){}) + cvt2(l[2 * i], l[2 * i + 1]);
-  f16x4 q0 = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3);
-  f16x4 q1 = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3);
-  return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+// Running maximum of packed sp2 values: four v_pk_maximum3_f16 per 16 values.
+// The maximum propagates NaN.
+__device__ __forceinline__ f16x2 sp2_track(f16x2 m, f16x8 lo, f16x8 hi) {
+  m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(lo.s01, lo.s23));
+  m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(lo.s45, lo.s67));
+  m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(hi.s01, hi.s23));
+  return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(hi.s45, hi.s67));
+}
+// True on every lane of the wave when some lane's tracked maximum is not below
+// 128.  A finite sp2 below 2^7 rounds to at most 128 in fp16, so this catches
+// every overflow (+inf) -- and every NaN, which the exact path reproduces
+// unchanged.
+__device__ __forceinline__ bool sp2_overflowed(f16x2 m) {
+  const f16 m1 = __builtin_elementwise_maximum(m.x, m.y);
+  return __builtin_amdgcn_ballot_w64(!(m1 < (f16)128.0f)) != 0;
 }
 
 // An opaque copy of a wave-uniform offset.  Weight fragments never change

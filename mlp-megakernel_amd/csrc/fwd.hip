@@ -19,8 +19,9 @@
 //  * Activations run in base-2 units: W_1 is staged pre-scaled by log2(e) and
 //    W_L by ln(2), hidden layers chain with no scaling at all (ln2 and log2e
 //    cancel between W^T h' and the next exp2), so the epilogue is exp2, add,
-//    log2 per element in fp32, then pack, max and add on packed fp16 halves
-//    (see sp2_pack8).  The stash stores natural-unit h = ln2 * h' in fp32.
+//    log2 per element in fp32 and one pack per pair (see sp2), after a
+//    wave-uniform overflow test per 16 values.  The stash stores natural-unit
+//    h = ln2 * h' in fp32.
 //  * Each layer is software-pipelined by 32-feature output block: the MFMA
 //    chain of block mb+1 is issued ahead of block mb's activation, so the
 //    matrix core and the VALU work concurrently within one wave.
@@ -195,52 +196,87 @@ struct Frags {
   f16x8 a[KSM];
 };
 
-// Reads step t's fragments from LDS (fragments below RF come from the
-// wave's register copy `rf`).  The address goes through opaque(): weights
-// never change after staging, and without it the compiler would hoist every
-// fragment read out of the persistent row loop (and spill).
-template <class N, int t, int KSM, int RF>
-__device__ __forceinline__ void load_frags(Frags<KSM>& f, const char* lds_b, int lane_off, f16x8 rf) {
-  constexpr int KS = N::ks(Steps<N>::layer(t));
-  constexpr int F0 = Steps<N>::frag(t);
-  const char* src = lds_b + opaque(lane_off);
+// This lane's LDS fragment slots, one base per 64 KiB window: ds_read's
+// immediate offset has 16 bits, so fragments past the first window would
+// otherwise each need their own address add.  The bases go through opaque():
+// weights never change after staging, and without it the compiler would
+// hoist every fragment read out of the persistent row loop (and spill).
+template <class N, int RF>
+struct FragBase {
+  static constexpr int kWindows = ((N::nfrag() - RF) * 1024 + 65535) / 65536;
+  const char* w[kWindows];
+  __device__ __forceinline__ FragBase(const char* lds_b, int lane_off) {
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
-    f.a[s] = F0 + s < RF ? rf : *reinterpret_cast<const f16x8*>(src + (F0 + s - RF) * 1024);
+    for (int i = 0; i < kWindows; ++i) w[i] = lds_b + opaque(lane_off + i * 65536);
+  }
+};
+
+// Fragment s of step t: from LDS, or the wave's register copy `rf` below RF.
+template <class N, int t, int RF>
+__device__ __forceinline__ f16x8 frag(int s, const FragBase<N, RF>& fb, f16x8 rf) {
+  constexpr int F0 = Steps<N>::frag(t);
+  if (F0 + s < RF) return rf;
+  const int off = (F0 + s - RF) * 1024;  // a constant after unrolling
+  return *reinterpret_cast<const f16x8*>(fb.w[off >> 16] + (off & 0xffff));
+}
+
+// Reads fragments [S0, KS) of step t.
+template <class N, int t, int KSM, int RF, int S0 = 0>
+__device__ __forceinline__ void load_frags(Frags<KSM>& f, const FragBase<N, RF>& fb, f16x8 rf) {
+  constexpr int KS = N::ks(Steps<N>::layer(t));
+#pragma unroll
+  for (int s = S0; s < KS; ++s) f.a[s] = frag<N, t, RF>(s, fb, rf);
 }
 
 // MFMA chain of one output block over input K-steps [S0, S1):
 // acc[nb] (+)= W_l[K-steps, block]^T . in.  S0 == 0 starts from zero.
-template <int S0, int S1, int NB, int KSM, class T, int KIN>
-__device__ __forceinline__ void chain(f32x16 (&acc)[NB], const Frags<KSM>& f, const T (&in)[KIN][NB]) {
+// As soon as the MFMAs of K-step s have been issued (they read their A
+// operand at issue), register f.a[s] is refilled with fragment s of step TN,
+// the chain after next: each LDS read then has a whole activation epilogue
+// to complete before its MFMA, and the fragments occupy no more registers
+// than one step's set.
+template <class N, int TN, int RF, int S0, int S1, int NB, int KSM, class T, int KIN>
+__device__ __forceinline__ void chain(f32x16 (&acc)[NB], Frags<KSM>& f, const T (&in)[KIN][NB],
+                                      const FragBase<N, RF>& fb, f16x8 rf) {
   static_assert(KIN >= S1, "input K-steps");
+  constexpr int KSN = N::ks(Steps<N>::layer(TN));
   if constexpr (S0 == 0) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x16){};
   }
 #pragma unroll
-  for (int s = S0; s < S1; ++s)
+  for (int s = S0; s < S1; ++s) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16(f.a[s], as_f16x8(in[s][nb]), acc[nb]);
+    if (s < KSN) f.a[s] = frag<N, TN, RF>(s, fb, rf);
+  }
 }
 
 // Activation and hand-off of output block mb: hidden layers apply softplus
 // (base-2 units), optionally store the fp32 stash, and pack the next layer's
-// B operands; the last layer stores fp16 rows of `out`.
-template <class N, int l, int NB, bool STASH, bool STAGE, int KSM>
+// B operands; the last layer stores fp16 rows of `out`.  The fast form
+// (EXACT false) evaluates sp2 directly and folds the packed values into the
+// running maximum `m`.  The exact form replaces overflowed values by u and
+// hands on sp2 / 2: in base-2 units a hidden activation is 1.44x its natural
+// value, so values above ~45,400 (natural) would not fit fp16, whereas the
+// reference's fp16 h (kernel.py:110) holds them up to 65,504.  Halving (and
+// doubling every later accumulator, kIn) keeps the whole range; both are
+// exact power-of-two scalings.
+template <class N, int l, int NB, bool STASH, bool STAGE, bool EXACT, int KSM>
 __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[NB], int mb,
-                                         f16x8 (&nxt)[KSM][NB], int lane) {
+                                         f16x8 (&nxt)[KSM][NB], f16x2& m, int lane) {
   constexpr int Nout = N::d[l + 1];
   constexpr bool LAST = (l == N::L - 1);
   const int n = lane & 31, g = lane >> 5;
   // Registers 0..7 -> features 32mb + 8g + [0..7]; 8..15 -> 32mb + 16 + 8g + [0..7].
   const bool lo_ok = (32 * mb + 16 <= Nout);  // folded after unrolling
   const bool hi_ok = (32 * mb + 32 <= Nout);
+  constexpr float kIn = (EXACT && l > 0) ? 2.0f : 1.0f;  // the exact form's halved inputs
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const uint32_t elem = (uint32_t)((nb * 32 + n) * Nout + 32 * mb + 8 * g);
     if constexpr (LAST && STAGE) {
-      const f32x16& v = acc[nb];  // ln 2 is folded into the staged W_L
+      const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
       const int row = nb * 32 + n;
       const int c = 4 * (mb & 1) + g;  // chunk within the staged 128-byte row segment
       io.stage[stage_slot(row, c)] =
@@ -248,23 +284,27 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       io.stage[stage_slot(row, c + 2)] =
           __builtin_bit_cast(i32x4, pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]));
     } else if constexpr (LAST) {
-      const f32x16& v = acc[nb];  // ln 2 is folded into the staged W_L
+      const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
       if (lo_ok) buf_store16<kStreamStore>(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
       if (hi_ok)
         buf_store16<kStreamStore>(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
     } else {
       // log2 e is folded into the staged W_1, so acc is u in base-2 units.
-      float u[16], t[16];
+      const f32x16 u = acc[nb] * kIn;
+      float s[16], q[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        u[e] = acc[nb][e];
-        t[e] = sp2_tail(u[e]);
+        s[e] = EXACT ? sp2_fix(u[e], sp2(u[e])) : sp2(u[e]);
+        q[e] = EXACT ? 0.5f * s[e] : s[e];
       }
+      const f16x8 lo = pack8(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
+      const f16x8 hi = pack8(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
+      if constexpr (!EXACT) m = sp2_track(m, lo, hi);
       if constexpr (STASH) {
         const rsrc_t sr = io.stash[l];
         float h[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) h[e] = (sp2_relu(u[e]) + t[e]) * kLn2;
+        for (int e = 0; e < 16; ++e) h[e] = s[e] * kLn2;
         if (lo_ok) {
           buf_store16<kStashStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, elem * 4);
           buf_store16<kStashStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, elem * 4 + 16);
@@ -274,8 +314,8 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
           buf_store16<kStashStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, elem * 4 + 80);
         }
       }
-      if (2 * mb < KSM) nxt[2 * mb][nb] = sp2_pack8(u, t);
-      if (2 * mb + 1 < KSM) nxt[2 * mb + 1][nb] = sp2_pack8(u + 8, t + 8);
+      if (2 * mb < KSM) nxt[2 * mb][nb] = lo;
+      if (2 * mb + 1 < KSM) nxt[2 * mb + 1][nb] = hi;
     }
   }
 }
@@ -311,7 +351,8 @@ struct Chain {
   i32x4 xa[KS0][NB];             // x rows of the block (refilled with the next block's)
   f16x8 b0[KSM][NB], b1[KSM][NB];  // hidden activations, ping-pong between layers
   f32x16 acc[2][NB];             // accumulators of the current and the next step
-  Frags<KSM> fr;                 // fragments of the next step
+  Frags<KSM> fr;                 // fragments of the next chain to issue
+  f16x2 ovf;                     // running maximum of the block's packed sp2 values
   f16x8 rf;                      // register-resident fragment (LdsPlan::reg_frags)
 
   // Layer l reads x (l = 0), b0 (odd l) or b1 (even l >= 2) and writes b0
@@ -329,54 +370,84 @@ struct Chain {
   }
 };
 
-// Step t of a row block.  Issue order: fragments of step t+1 and, when it
-// belongs to the same layer, its MFMA chain (which runs on the matrix core
-// while this step's activation runs on the VALU), then the epilogue of step
-// t, and -- at a layer boundary -- the first chain of the next layer, which
-// needs all of this layer's outputs.  Fragments are single-buffered: the
-// chain waits for its LDS reads, which the other waves of the SIMD cover.
-template <class N, int t, int NB, bool STASH, bool STAGE, int KSM, int RF>
+// Step t of a row block.  Issue order: when step t+1 belongs to the same
+// layer, its MFMA chain (which runs on the matrix core while this step's
+// activation runs on the VALU), then the epilogue of step t, and -- at a layer
+// boundary -- the first chain of the next layer, which needs all of this
+// layer's outputs.  c.fr holds step t+1's fragments on entry; the chain
+// replaces them with those of step t+2 (step 0 of the next row block after
+// the last chain of this one).
+template <class N, int t, int NB, bool STASH, bool STAGE, bool EXACT, int KSM, int RF>
 __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chain<N, NB, KSM>& c,
-                                     const char* lds_b, int lane_off, int64_t next, int lane) {
+                                     const FragBase<N, RF>& fb, int64_t next, int lane) {
   using S = Steps<N>;
   constexpr int T = S::count();
   constexpr int l = S::layer(t), mb = S::mb(t);
   constexpr bool same = t + 1 < T && S::layer(t + 1) == l;
   constexpr int ROWS = 32 * NB;
-  if constexpr (t + 1 < T) load_frags<N, t + 1, KSM, RF>(c.fr, lds_b, lane_off, c.rf);
-  if constexpr (same) chain<0, N::ks(l), NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l>());
+  constexpr int TN = (t + 2) % T;
+  constexpr int KS1 = t + 1 < T ? N::ks(S::layer(t + 1)) : 0;
+  if constexpr (same) {
+    chain<N, TN, RF, 0, KS1, NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l>(), fb, c.rf);
+    load_frags<N, TN, KSM, RF, KS1>(c.fr, fb, c.rf);
+  }
   // Last block of a layer: the next layer's first chain can already run over
   // the K-steps the earlier blocks produced (2 per block); only the last two
   // wait for this step's epilogue.
   constexpr int EARLY = (t + 1 < T && !same) ? 2 * mb : 0;
   if constexpr (EARLY > 0)
-    chain<0, EARLY, NB>(c.acc[(t + 1) & 1], c.fr, c.template in<(l + 1) % N::L>());
+    chain<N, TN, RF, 0, EARLY, NB>(c.acc[(t + 1) & 1], c.fr, c.template in<(l + 1) % N::L>(), fb, c.rf);
   if constexpr (l == 0 && (same ? t + 1 == N::mbs(0) - 1 : t == 0)) {
     // Every MFMA that reads x has been issued: refill xa with the next block's
     // rows (past the end the resource is empty and the refill reads zeros).
     MLPMK_SCHED_FENCE();
     load_rows<N::ks(0), NB>(c.xa, block_io<N, false, ROWS>(p, next * ROWS).x, lane & 31, lane >> 5);
   }
-  epilogue<N, l, NB, STASH, STAGE, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), lane);
+  epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.ovf, lane);
   if constexpr (l == N::L - 1 && STAGE) {
     if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
   }
-  if constexpr (t + 1 < T && !same)
-    chain<EARLY, N::ks(l + 1), NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l + 1>());
-  if constexpr (t + 1 < T) step<N, t + 1, NB, STASH, STAGE, KSM, RF>(p, io, c, lds_b, lane_off, next, lane);
+  if constexpr (t + 1 < T && !same) {
+    chain<N, TN, RF, EARLY, KS1, NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l + 1>(), fb, c.rf);
+    load_frags<N, TN, KSM, RF, KS1>(c.fr, fb, c.rf);
+  }
+  if constexpr (t + 1 < T) step<N, t + 1, NB, STASH, STAGE, EXACT, KSM, RF>(p, io, c, fb, next, lane);
 }
 
 // One row block: the whole layer chain, stores, and the x refill for block
-// `next`.  On entry c.xa holds the block's x rows.
-template <class N, int NB, bool STASH, bool STAGE, int KSM, int RF>
-__device__ __forceinline__ void fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
+// `next`.  On entry c.xa holds the block's x rows and c.fr the fragments of
+// step 0; on exit they hold the same for block `next`.  Returns (wave-
+// uniform) whether some sp2 of the fast form overflowed or was NaN.
+template <class N, int NB, bool STASH, bool STAGE, bool EXACT, int KSM, int RF>
+__device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
                                           int lane_off, i32x4* stage, int64_t b, int64_t next, int lane) {
   constexpr int ROWS = 32 * NB;
+  constexpr int T1 = 1 % Steps<N>::count();
   BlockIO io = block_io<N, STASH, ROWS>(p, b * ROWS);
   io.stage = stage;
-  load_frags<N, 0, KSM, RF>(c.fr, lds_b, lane_off, c.rf);
-  chain<0, N::ks(0), NB>(c.acc[0], c.fr, c.xa);
-  step<N, 0, NB, STASH, STAGE, KSM, RF>(p, io, c, lds_b, lane_off, next, lane);
+  const FragBase<N, RF> fb(lds_b, lane_off);
+  c.ovf = f16x2{};
+  chain<N, T1, RF, 0, N::ks(0), NB>(c.acc[0], c.fr, c.xa, fb, c.rf);
+  load_frags<N, T1, KSM, RF, N::ks(0)>(c.fr, fb, c.rf);
+  step<N, 0, NB, STASH, STAGE, EXACT, KSM, RF>(p, io, c, fb, next, lane);
+  return !EXACT && sp2_overflowed(c.ovf);
+}
+
+// Block b with the fast softplus form, then -- only if one of its wave's sp2
+// values overflowed (some u >= 128) -- again with the exact form, from a
+// fresh read of its x rows and step-0 fragments.  The second pass rewrites
+// every output (and stash) row of the block and leaves c as the first did.
+template <class N, int NB, bool STASH, bool STAGE, int KSM, int RF>
+__device__ __forceinline__ void fwd_block_checked(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
+                                                  int lane_off, i32x4* stage, int64_t b, int64_t next,
+                                                  int lane) {
+  constexpr int ROWS = 32 * NB;
+  if (__builtin_expect(fwd_block<N, NB, STASH, STAGE, false, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane),
+                       0)) {
+    load_rows<N::ks(0), NB>(c.xa, block_io<N, false, ROWS>(p, b * ROWS).x, lane & 31, lane >> 5);
+    load_frags<N, 0, KSM, RF>(c.fr, FragBase<N, RF>(lds_b, lane_off), c.rf);
+    fwd_block<N, NB, STASH, STAGE, true, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
+  }
 }
 
 // Persistent forward.  Workgroup b owns row blocks b, b + G, b + 2G, ...
@@ -442,15 +513,16 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   int64_t b = claim();
   if (b >= nblk) return;  // no barrier follows
   load_rows<KS0, NB>(c.xa, block_io<N, false, ROWS>(p, b * ROWS).x, lane & 31, lane >> 5);
+  load_frags<N, 0, KSM, RF>(c.fr, FragBase<N, RF>(lds_b, lane_off), c.rf);
   // The first block is peeled so that the loop header is entered from two
   // paths with the same outstanding memory operations (the x refill, then
   // stores): vmcnt counts loads and stores in issue order.
   int64_t next = claim();
-  fwd_block<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
+  fwd_block_checked<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
   // Claims are increasing per wave, so once one is past the end all later are.
   for (b = next; b < nblk; b = next) {
     next = claim();
-    fwd_block<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
+    fwd_block_checked<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
   }
 }
 

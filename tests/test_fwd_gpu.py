@@ -150,6 +150,78 @@ def test_threshold_edges_through_identity_weights():
     assert abs(out[0, 4] - np.log(3.0)) < 2e-3  # z = 0: softplus(softplus(0)) = log(1 + 2)
 
 
+@pytest.mark.parametrize("stash", [False, True])
+def test_large_preactivations_take_the_exact_path(stash):
+    # Past z = 88.7 the kernel's direct softplus form overflows (2^u in base-2
+    # units); such blocks are recomputed exactly and must give softplus(z) = z,
+    # the reference's z > 20 branch (kernel.py:108), up to the fp16 limit of
+    # the reference's hidden h (kernel.py:110).  Large rows sit among ordinary
+    # ones inside the same 32-row blocks, and only some blocks have any.
+    z = np.array([88.0, 88.8, 89.0, 100.0, 200.0, 1000.0, 3.0e4, 4.6e4, 5.0e4, 65504.0], dtype=np.float32)
+    m = 256
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((m, 128)) * 0.5).astype(np.float16)
+    rows = (3, 40, 41, 200)  # blocks 0, 1 and 6 of eight
+    for r in rows:
+        x[r, : z.size] = z.astype(np.float16)
+    eye = np.eye(128, dtype=np.float16)
+    xd, wd = _to_dev(x, [eye, eye, eye])
+    res = ops.fwd(xd, wd, stash=stash)
+    out = (res[0] if stash else res).float().cpu().numpy()
+    ref, ref_h = orc.forward(x, [eye, eye, eye], return_hidden=True)
+    _check(out, ref, "identity weights, large z")
+    for r in rows:
+        np.testing.assert_allclose(out[r, : z.size], z, rtol=2e-3)
+    if stash:
+        for i, h in enumerate(res[1]):
+            ok, err, _ = orc.allclose_report(h.cpu().numpy(), ref_h[i], 2e-3, 2e-3)
+            assert ok, f"stash h{i + 1}: max|err| {err}"
+
+
+@pytest.mark.parametrize("dims,stash", [((128, 128, 128, 128), False), ((128, 128, 128, 128), True),
+                                        ((128,) * 6, False), ((32, 64, 64, 16), False)])
+def test_scaled_inputs_overflow_many_blocks(dims, stash):
+    # x scaled so that ~30 % of pre-activations exceed z = 88.7 in every
+    # layer and every block takes the exact path; every 7th row keeps its
+    # ordinary scale and shares those blocks.
+    x, ws = orc.make_inputs(dims, 4096, seed=21)
+    x = (x.astype(np.float32) * 300.0).astype(np.float16)
+    small = np.zeros(len(x), dtype=bool)
+    small[::7] = True
+    x[small] = (x[small].astype(np.float32) / 300.0).astype(np.float16)
+    xd, wd = _to_dev(x, ws)
+    res = ops.fwd(xd, wd, stash=stash)
+    out = (res[0] if stash else res).float().cpu().numpy()
+    # Hidden activations reach ~1.5e3, where one fp16 ulp is 1.0: compare
+    # with the oracle that rounds them to fp16 like the reference kernel
+    # (kernel.py:110,117), with a bound scaled to the output range for the
+    # large rows and the usual one for the ordinary rows.
+    ref = orc.forward(x, ws, round_hidden=True)
+    assert np.isfinite(ref).all()
+    _check(out[small], ref[small], f"{dims} ordinary rows in exact-path blocks")
+    big_err = np.abs(out[~small] - ref[~small]).max()
+    assert big_err <= 2e-3 * np.abs(ref[~small]).max(), (big_err, np.abs(ref[~small]).max())
+    if stash:
+        assert torch.equal(res[0], ops.fwd(xd, wd))
+
+
+def test_inf_and_nan_inputs_propagate_like_the_oracle():
+    # inf * 0 inside the products gives NaN, as in the reference's fp32 dot;
+    # rows without non-finite inputs are unaffected.
+    x, ws = orc.make_inputs((128, 128, 128, 128), 128, seed=4)
+    x[5, 7] = np.inf
+    x[70, 0] = -np.inf
+    x[99, 3] = np.nan
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = orc.forward(x, ws)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    fin = np.isfinite(ref).all(axis=1)
+    assert fin.sum() == 125
+    _check(out[fin], ref[fin], "finite rows next to non-finite ones")
+
+
 def test_zero_first_layer_closed_form():
     x, ws = orc.make_inputs((128, 128, 128, 128), 512, seed=1)
     ws[0] = np.zeros_like(ws[0])
