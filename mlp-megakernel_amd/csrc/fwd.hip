@@ -576,11 +576,12 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
   return MLPMK_OK;
 }
 
-// NW waves per workgroup for inference, NWS with the fp32 stash (whose extra
-// registers would spill at NW = 12 for the 128-wide networks).
-template <class N, int NB, int NW, int NWS, int D>
+// NB row blocks per fragment read and NW waves per workgroup for inference,
+// NBS and NWS with the fp32 stash (whose extra registers would spill at
+// NW = 12 for the 128-wide networks, and at NB = 2 for the narrow one).
+template <class N, int NB, int NW, int NBS, int NWS, int D>
 static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
-  return stash ? launch_fwd<N, NB, true, NWS, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
+  return stash ? launch_fwd<N, NBS, true, NWS, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
 }
 
 bool fwd_supported_dims(int L, const int* dims) {
@@ -589,9 +590,9 @@ bool fwd_supported_dims(int L, const int* dims) {
 }
 
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
-  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 8, 1>(p, stash, st);
-  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 8, 1>(p, stash, st);
-  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 1, 16, 16, 1>(p, stash, st);
+  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 1, 8, 1>(p, stash, st);
+  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 1, 8, 1>(p, stash, st);
+  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 16, 1, 16, 1>(p, stash, st);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
 }
 
