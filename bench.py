@@ -212,7 +212,8 @@ def train_step_bench(torch, m, steps=50, warmup=10):
     """One training step of BASELINE config 5 through the drop-in module:
     weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
     megakernel + weight-norm backward, x without grad.  Timed with HIP events
-    around `steps` back-to-back autograd steps (Python dispatch included)."""
+    around `steps` back-to-back autograd steps (Python dispatch included), and
+    around `steps` replays of the whole step captured as one HIP graph."""
     import fused_mlp
 
     torch.manual_seed(0)
@@ -227,11 +228,30 @@ def train_step_bench(torch, m, steps=50, warmup=10):
     with gc_paused():
         ramp_clock(torch, step, seconds=0.2)
         ms = time_launches(torch, step, steps, warmup)
+
+    # The same step captured whole into one HIP graph (the library allocates
+    # nothing and records no memset); a replay costs launch latency plus the
+    # kernels, no Python or autograd dispatch.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            step(i)
+    torch.cuda.current_stream().wait_stream(side)
+    model.v_all.grad = None
+    model.g_all.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model(x).sum().backward()
+    with gc_paused():
+        gms = time_launches(torch, lambda i: graph.replay(), steps, warmup)
     return {
         "ms_per_step": round(ms, 5),
         "rows_per_s": m / (ms * 1e-3),
         "achieved_gbs": round(TRAIN_BYTES_PER_ROW * m / (ms * 1e-3) / 1e9, 1),
         "tflops": round(TRAIN_FLOP_PER_ROW * m / (ms * 1e-3) / 1e12, 2),
+        "graph_ms_per_step": round(gms, 5),
+        "graph_rows_per_s": m / (gms * 1e-3),
         "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd",
     }
 
