@@ -94,6 +94,9 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
  *   dx               NULL, or [M, dims[0]] fp16 (written)
  *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
  *                    caller zeroes them for a fresh gradient
+ * The 5-layer network is supported through mlpmk_bwd_ws only (it hands dz
+ * between two launches through the workspace); here it returns
+ * MLPMK_ERR_INVALID_ARG without touching the device.
  */
 int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
               const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
@@ -108,8 +111,13 @@ int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const*
  * workgroup adding its partials with fp32 atomics: device-wide fp32 atomics
  * run at ~270 M elements/s, and that flush cost ~45-65 us at M = 131072
  * (256 workgroups x 49152 dW elements).  Grids below 64 workgroups (small M)
- * keep the atomic flush, which is then cheaper, and leave the workspace
- * untouched.
+ * keep the atomic flush, which is then cheaper, and leave the partial-sum
+ * part of the workspace untouched.
+ * The 5-layer 128-wide backward runs as two launches: layers 4..2 (their
+ * dgrad weights and exchange tiles fill one workgroup's 160 KiB of LDS),
+ * whose fp16 gradient of h_1 goes through the first M * 256 bytes of the
+ * workspace (rounded up to 256) to layers 1..0.  Numerically the same as one
+ * launch: the in-register chain also hands dz on as fp16.
  *   workspace        device memory, 16-byte aligned, at least the size that
  *                    mlpmk_bwd_workspace_size reports for the same
  *                    (num_layers, dims, M, dx != NULL) on the current device;
@@ -121,7 +129,9 @@ int mlpmk_bwd_ws(int num_layers, const int* dims, const void* x, const void* con
 
 /*
  * Bytes of workspace mlpmk_bwd_ws needs on the current device: one fp32 copy
- * of all dW blocks per workgroup of the backward grid (0 when M == 0).
+ * of all dW blocks per workgroup of the backward grid, plus for the 5-layer
+ * network the dz block of the hand-over between its two launches (0 when
+ * M == 0).
  */
 int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int64_t M, int with_dx, int64_t* bytes);
 

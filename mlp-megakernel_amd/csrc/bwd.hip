@@ -31,6 +31,15 @@
 //    workgroup; at the end each wave adds them to the fp32 dW in global memory
 //    with hardware float atomics (one add per element per workgroup).
 //
+// Segment mode (SEG) runs the upper layers of a deeper network on their own:
+// layer 0 of the segment then takes its activation from the fp32 stash of
+// the layer below (p.h0) instead of x, and its data gradient leaves through
+// p.dx already multiplied by 1 - exp(-h) -- exactly the fp16 dz operand the
+// in-register chain would have handed to the next layer.  The 5-layer
+// backward is two launches this way (layers 4..2, then 1..0), because its
+// four dgrad weight blocks and the exchange tiles do not fit the 160 KiB LDS
+// of one workgroup together.
+//
 // The exchange tiles are XOR-swizzled, element (f, r) at f*R + (r ^ 8*(f & 15)):
 // the 2-byte writes of one half-wave (32 consecutive rows of one feature) hit
 // one 64-byte window, the two half-waves (features f and f+8) land 128 bytes
@@ -42,8 +51,9 @@
 
 namespace mlpmk {
 
-template <class N, int NW, bool DX>
+template <class N, int NW, bool DX, bool SEG = false>
 struct BwdGeom {
+  static_assert(!SEG || DX, "a segment always hands on the gradient below it");
   static constexpr int L = N::L;
   static constexpr int R = 32 * NW;  // rows per round
   static constexpr bool has_dgrad(int l) { return l >= 1 || DX; }
@@ -90,9 +100,9 @@ struct BwdGeom {
     for (int i = 0; i <= L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
     return m;
   }
-  static constexpr int kshid() {  // K-steps of the widest hidden activation
+  static constexpr int kshid() {  // K-steps of the widest activation read from a stash
     int m = 1;
-    for (int i = 1; i < L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
+    for (int i = SEG ? 0 : 1; i < L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
     return m;
   }
   static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
@@ -132,9 +142,9 @@ __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* l
   }
 }
 
-template <class N, int NW, bool DX>
+template <class N, int NW, bool DX, bool SEG>
 struct BwdWave {
-  using Gm = BwdGeom<N, NW, DX>;
+  using Gm = BwdGeom<N, NW, DX, SEG>;
   static constexpr int L = N::L;
   static constexpr int R = Gm::R;
   static constexpr int KSM = Gm::ksmax();
@@ -186,10 +196,11 @@ struct BwdWave {
       gbuf[s] = __builtin_bit_cast(
           f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + 16 * s + 8 * g) * 2), 0, 0));
   }
-  // h_l (l >= 1, stash[l-1], fp32) rows from r0: 8 consecutive features per K-step.
+  // a_l = h_l (stash[l-1], or p.h0 for layer 0 of a segment; fp32) rows from
+  // r0: 8 consecutive features per K-step.
   template <int l>
   __device__ __forceinline__ void load_h(int64_t r0) {
-    const rsrc_t hr = rows_rsrc(p.stash[l - 1], N::d[l], 4, r0);
+    const rsrc_t hr = rows_rsrc(l == 0 ? p.h0 : p.stash[l > 0 ? l - 1 : 0], N::d[l], 4, r0);
 #pragma unroll
     for (int s = 0; s < N::d[l] / 16; ++s) {
       const int off = (n * N::d[l] + 16 * s + 8 * g) * 4;
@@ -253,19 +264,21 @@ struct BwdWave {
   }
 
   // One layer of the backward for this wave's 32 rows.  On entry dz holds
-  // dz_l and hbuf (l >= 1) or xbuf (l = 0) holds a_l.  Publishes a_l and dz_l
-  // to the exchange tiles, runs dgrad into dzn = dz_{l-1} (or dx), and after
-  // the barrier issues the next phase's loads before the wgrad of dW_l so
-  // that their latency hides behind its MFMAs.
+  // dz_l and hbuf (l >= 1, or a segment) or xbuf (l = 0) holds a_l.
+  // Publishes a_l and dz_l to the exchange tiles, runs dgrad into
+  // dzn = dz_{l-1} (or dx), and after the barrier issues the next phase's
+  // loads before the wgrad of dW_l so that their latency hides behind its
+  // MFMAs.
   template <int l>
   __device__ __forceinline__ void phase(f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM]) {
     constexpr int KSA = N::d[l] / 16;      // K-steps of a_l
     constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
+    constexpr bool HA = l >= 1 || SEG;     // a_l came from a stash (fp32, in hbuf)
 #pragma unroll
     for (int s = 0; s < KSZ; ++s) xwrite(tz, s, dz[s]);
 #pragma unroll
     for (int s = 0; s < KSA; ++s) {
-      if constexpr (l >= 1)
+      if constexpr (HA)
         xwrite(ta, s, pack8(hbuf[s][0], hbuf[s][1], hbuf[s][2], hbuf[s][3], hbuf[s][4], hbuf[s][5], hbuf[s][6], hbuf[s][7]));
       else
         xwrite(ta, s, xbuf[s]);
@@ -282,15 +295,24 @@ struct BwdWave {
         for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16(frag[s * 64], dz[s], acc);
         // Registers 0..7: features 32mb + 8g + [0..7] (K-step 2mb of a_l);
         // 8..15: 32mb + 16 + 8g + [0..7] (K-step 2mb + 1).
-        if constexpr (l >= 1) {
+        if constexpr (HA) {
           float v[16];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[2 * mb][j] * kLog2e));
             v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[2 * mb + 1][j] * kLog2e));
           }
-          dzn[2 * mb] = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-          dzn[2 * mb + 1] = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+          const f16x8 lo = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+          const f16x8 hi = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+          if constexpr (l >= 1) {
+            dzn[2 * mb] = lo;
+            dzn[2 * mb + 1] = hi;
+          } else {  // segment: dz of the layer below leaves through p.dx
+            const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2, row0);
+            const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
+            buf_store16(lo, dr, e * 2);
+            buf_store16(hi, dr, e * 2 + 32);
+          }
         } else {
           const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2, row0);
           const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
@@ -301,7 +323,7 @@ struct BwdWave {
       }
     }
     __syncthreads();  // every wave's rows are in the exchange tiles
-    if constexpr (l >= 2) {
+    if constexpr (l >= 2 || (l == 1 && SEG)) {
       load_h<l - 1>(row0);
     } else if constexpr (l == 1) {
       load_x(row0);
@@ -373,9 +395,9 @@ struct BwdWave {
   }
 };
 
-template <class N, int NW, bool DX>
+template <class N, int NW, bool DX, bool SEG>
 __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
-  using Gm = BwdGeom<N, NW, DX>;
+  using Gm = BwdGeom<N, NW, DX, SEG>;
   static_assert(Gm::valid(), "unsupported backward shape");
   constexpr int R = Gm::R;
   __shared__ f16x8 wfr[Gm::ndfrag() * 64];
@@ -389,7 +411,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   f32x16 wacc[Gm::ntpw()];
 #pragma unroll
   for (int k = 0; k < Gm::ntpw(); ++k) wacc[k] = (f32x16){};
-  BwdWave<N, NW, DX> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, {}, 0, wacc};
+  BwdWave<N, NW, DX, SEG> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, {}, 0, wacc};
   wv.init_slots();
 
   // Every wave of a workgroup runs the same rounds (the barriers need all of them).
@@ -452,6 +474,8 @@ __global__ __launch_bounds__(kCombineCols* kCombineGroups) void bwd_combine_kern
 // ---------------------------------------------------------------------------
 
 typedef Net<128, 128, 128, 128> BNet3L128;
+typedef Net<128, 128, 128, 128, 128, 128> BNet5L128;
+typedef Net<128, 128, 128> BNet2L128;  // layers 1..0 of the 5-layer network
 typedef Net<32, 64, 64, 16> BNetNarrow;
 
 template <class N>
@@ -464,7 +488,7 @@ static bool bdims_match(int L, const int* dims) {
 
 // Grid of the persistent backward: one workgroup per round of 32*NW rows, at
 // most CUs x occupancy.
-template <class N, int NW, bool DX>
+template <class N, int NW, bool DX, bool SEG>
 static int bwd_grid(int64_t M, int* grid) {
   constexpr int kMaxDev = 64;
   static int occ_cache[kMaxDev];  // 0 = unknown; benign race (idempotent value)
@@ -474,7 +498,7 @@ static int bwd_grid(int64_t M, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  const void* kern = reinterpret_cast<const void*>(&bwd_kernel<N, NW, DX>);
+  const void* kern = reinterpret_cast<const void*>(&bwd_kernel<N, NW, DX, SEG>);
   int occ = (dev >= 0 && dev < kMaxDev) ? occ_cache[dev] : 0;
   if (occ <= 0) {
     rc = kernel_occupancy(kern, NW * 64, &occ);
@@ -492,15 +516,15 @@ static int bwd_grid(int64_t M, int* grid) {
 // atomics, 29.8 us with the workspace), so the workspace goes unused.
 constexpr int kPartialMinGrid = 64;
 
-template <class N, int NW, bool DX>
+template <class N, int NW, bool DX, bool SEG = false>
 static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
   int grid = 0;
-  int rc = bwd_grid<N, NW, DX>(p_in.M, &grid);
+  int rc = bwd_grid<N, NW, DX, SEG>(p_in.M, &grid);
   if (rc != MLPMK_OK) return rc;
   BwdParams p = p_in;
   if (grid < kPartialMinGrid) p.part = nullptr;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((bwd_kernel<N, NW, DX>), dim3(grid), dim3(NW * 64), 0, st, p);
+  hipLaunchKernelGGL((bwd_kernel<N, NW, DX, SEG>), dim3(grid), dim3(NW * 64), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bwd kernel launch");
   if (p.part) {
@@ -508,7 +532,7 @@ static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
     lay.L = N::L;
     lay.nelem = N::weight_elems();
     for (int l = 0; l < N::L; ++l) {
-      lay.off[l] = BwdGeom<N, NW, DX>::woff(l);
+      lay.off[l] = BwdGeom<N, NW, DX, SEG>::woff(l);
       lay.dw[l] = p.dw[l];
     }
     lay.off[N::L] = lay.nelem;
@@ -525,26 +549,88 @@ static int launch_bwd_any(const BwdParams& p, hipStream_t st) {
   return p.dx ? launch_bwd<N, NW, true>(p, st) : launch_bwd<N, NW, false>(p, st);
 }
 
-template <class N, int NW>
-static int bwd_workspace_any(int64_t M, bool dx, int64_t* bytes) {
+template <class N, int NW, bool DX, bool SEG = false>
+static int partial_bytes(int64_t M, int64_t* bytes) {
   int grid = 0;
-  const int rc = dx ? bwd_grid<N, NW, true>(M, &grid) : bwd_grid<N, NW, false>(M, &grid);
+  const int rc = bwd_grid<N, NW, DX, SEG>(M, &grid);
   if (rc == MLPMK_OK) *bytes = (int64_t)grid * N::weight_elems() * (int64_t)sizeof(float);
   return rc;
 }
 
+template <class N, int NW>
+static int bwd_workspace_any(int64_t M, bool dx, int64_t* bytes) {
+  return dx ? partial_bytes<N, NW, true>(M, bytes) : partial_bytes<N, NW, false>(M, bytes);
+}
+
+// The 5-layer backward: layers 4..2 as a segment (kernel A, 96 KiB of dgrad
+// fragments + 64 KiB of exchange tiles), whose fp16 dz_1 goes through the
+// workspace to layers 1..0 (kernel B, the 2-layer network with dz_1 as its
+// output gradient).  Workspace: dz_1 [M, 128] fp16, then the weight-gradient
+// partials of whichever launch needs more (the launches run in stream order,
+// so they share the block).
+static int64_t dz_bytes(int64_t M) { return (M * 128 * 2 + 255) / 256 * 256; }
+
+static int bwd5_workspace(int64_t M, bool dx, int64_t* bytes) {
+  int64_t a = 0, b = 0;
+  int rc = partial_bytes<BNet3L128, 4, true, true>(M, &a);
+  if (rc != MLPMK_OK) return rc;
+  rc = dx ? partial_bytes<BNet2L128, 4, true>(M, &b) : partial_bytes<BNet2L128, 4, false>(M, &b);
+  if (rc != MLPMK_OK) return rc;
+  *bytes = dz_bytes(M) + (a > b ? a : b);
+  return MLPMK_OK;
+}
+
+static int launch_bwd5(const BwdParams& p, hipStream_t st) {
+  if (!p.part)
+    return fail(MLPMK_ERR_INVALID_ARG,
+                "the 5-layer backward passes dz between two launches through the workspace: use mlpmk_bwd_ws");
+  char* const ws = reinterpret_cast<char*>(p.part);
+  _Float16* const dz1 = reinterpret_cast<_Float16*>(ws);
+  float* const part = reinterpret_cast<float*>(ws + dz_bytes(p.M));
+  BwdParams a = {};
+  for (int l = 0; l < 3; ++l) {
+    a.w[l] = p.w[2 + l];
+    a.dw[l] = p.dw[2 + l];
+  }
+  a.stash[0] = p.stash[2];  // h_3
+  a.stash[1] = p.stash[3];  // h_4
+  a.h0 = p.stash[1];        // h_2
+  a.dout = p.dout;
+  a.dout_stride = p.dout_stride;
+  a.dx = dz1;
+  a.M = p.M;
+  a.part = part;
+  int rc = launch_bwd<BNet3L128, 4, true, true>(a, st);
+  if (rc != MLPMK_OK) return rc;
+  BwdParams b = {};
+  b.x = p.x;
+  for (int l = 0; l < 2; ++l) {
+    b.w[l] = p.w[l];
+    b.dw[l] = p.dw[l];
+  }
+  b.stash[0] = p.stash[0];  // h_1
+  b.dout = dz1;
+  b.dout_stride = 128;
+  b.dx = p.dx;
+  b.M = p.M;
+  b.part = part;
+  return launch_bwd_any<BNet2L128, 4>(b, st);
+}
+
 int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
   if (bdims_match<BNet3L128>(L, dims)) return bwd_workspace_any<BNet3L128, 4>(M, dx, bytes);
+  if (bdims_match<BNet5L128>(L, dims)) return bwd5_workspace(M, dx, bytes);
   if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<BNetNarrow, 4>(M, dx, bytes);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
 }
 
 bool bwd_supported_dims(int L, const int* dims) {
-  return bdims_match<BNet3L128>(L, dims) || bdims_match<BNetNarrow>(L, dims);
+  return bdims_match<BNet3L128>(L, dims) || bdims_match<BNet5L128>(L, dims) || bdims_match<BNetNarrow>(L, dims);
 }
 
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st) {
   if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<BNet3L128, 4>(p, st);
+  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd5(p, st);
   if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<BNetNarrow, 4>(p, st);
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
 }

@@ -32,6 +32,9 @@ struct BwdParams {
   // blocks back to back, at part + b * (sum_l d[l] * d[l+1]), and a second
   // kernel sums the partials into dw.
   float* part;
+  // Segment mode only (the upper layers of a deeper network): the fp32
+  // activation feeding layer 0, h_{l0} of the full network, in place of x.
+  const float* h0;
 };
 
 }  // namespace mlpmk

@@ -101,6 +101,19 @@ def test_bwd_validation_codes():
         assert call() == UNSUPPORTED
 
 
+def test_5l_backward_is_supported_but_needs_a_workspace():
+    lib = _lib.get()
+    d = [128] * 6
+    pd, _k1 = _lib.int_array(d)
+    assert ops.bwd_supported(d)
+    pw, _k2 = _lib.ptr_array([A] * 5)
+    ps, _k3 = _lib.ptr_array([A] * 4)
+    pg, _k4 = _lib.ptr_array([A] * 5)
+    # Rejected before any device call: dz travels between two launches through the workspace.
+    assert lib.mlpmk_bwd(5, pd, A, pw, ps, A, 128, None, pg, 256, None) == INVALID
+    assert b"mlpmk_bwd_ws" in lib.mlpmk_last_error()
+
+
 def test_wn_and_copy_validation_codes():
     lib = _lib.get()
     pd, _k = _lib.int_array([128, 128, 128, 128])

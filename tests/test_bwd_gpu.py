@@ -21,6 +21,7 @@ from mlpmk import ops
 pytestmark = pytest.mark.gpu
 
 D3 = (128, 128, 128, 128)
+D5 = (128,) * 6
 NARROW = (32, 64, 64, 16)
 
 
@@ -67,6 +68,39 @@ def test_3l128_weight_and_data_gradients(m):
         check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")
     ok, err, excess = orc.allclose_report(dx.float().cpu().numpy(), rdx, 1e-2, 1e-2)
     assert ok, f"dx M={m}: max err {err:.3g}, excess {excess:.3g}"
+
+
+@pytest.mark.parametrize("m", [64, 4096, 16384, 65536])
+def test_5l128_weight_and_data_gradients(m):
+    # Two launches: layers 4..2 as a segment (its layer-0 activation is the
+    # stash h_2, its data gradient the fp16 dz_1 in the workspace), then
+    # layers 1..0 with dz_1 as their output gradient.
+    _, _, dws, dx, rdws, rdx = run_train(D5, m, seed=50 + m)
+    for i in range(5):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")
+    ok, err, excess = orc.allclose_report(dx.float().cpu().numpy(), rdx, 1e-2, 1e-2)
+    assert ok, f"dx M={m}: max err {err:.3g}, excess {excess:.3g}"
+
+
+@pytest.mark.parametrize("m", [1, 33, 1000, 4097])
+def test_5l128_ragged_rows_without_dx(m):
+    _, _, dws, dx, rdws, _ = run_train(D5, m, seed=7 * m + 2, dout_mode="full", with_dx=False)
+    assert dx is None
+    for i in range(5):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")
+
+
+def test_5l128_without_workspace_is_rejected():
+    x, ws = orc.make_inputs(D5, 256, seed=9)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dout = torch.ones((256, 128), dtype=torch.float16, device="cuda")
+    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(5)]
+    with pytest.raises(ops.MlpmkError, match="mlpmk_bwd_ws"):
+        ops.bwd(xd, wd, hs, dout, dws, workspace=False)
+    torch.cuda.synchronize()
+    assert all(float(d.abs().max()) == 0.0 for d in dws)
 
 
 @pytest.mark.parametrize("m", [1, 31, 33, 129, 1000, 4097])

@@ -199,17 +199,43 @@ def test_wn_module_matches_committed_golden_training_step():
     assert ok, f"dx: {err}"
 
 
-def test_five_layer_module_forward_and_unsupported_backward():
+def test_five_layer_module_forward_and_backward():
+    # The 5-layer backward runs as two launches (layers 4..2 as a segment
+    # handing fp16 dz_1 to layers 1..0 through the workspace).
     import fused_mlp5
 
     torch.manual_seed(4)
     model = fused_mlp5.FusedMLP5Softplus().cuda().half()
-    x = torch.randn(4096, 128, device="cuda").half()
+    x = torch.randn(4096, 128, device="cuda").half().requires_grad_(True)
     with torch.no_grad():
         out = model(x)
-    ref_out, _, _ = torch_ref(x, list(model.weights))
+    ref_out, ref_dx, ref_dws = torch_ref(x, list(model.weights))
     ok, err, _ = orc.allclose_report(out.float().cpu().numpy(), ref_out, 1e-2, 1e-2)
     assert ok, err
-    y = model(x)
-    with pytest.raises(ops.MlpmkError, match="UNSUPPORTED_SHAPE"):
-        y.sum().backward()
+    model(x).sum().backward()
+    for i, w in enumerate(model.weights):
+        check_grad(w.grad.float().cpu().numpy(), ref_dws[i], f"dW{i + 1}")
+    ok, err, _ = orc.allclose_report(x.grad.float().cpu().numpy(), ref_dx, 1e-2, 1e-2)
+    assert ok, f"dx: {err}"
+
+
+@pytest.mark.parametrize("m", [4096, 65536])
+def test_five_layer_wn_module(m):
+    import fused_mlp5
+
+    torch.manual_seed(6)
+    model = fused_mlp5.FusedMLP5SoftplusWN().cuda()
+    with torch.no_grad():
+        model.g_all.mul_(torch.rand_like(model.g_all) + 0.5)
+    x = torch.randn(m, 128, device="cuda").half()
+    out = model(x)
+    out.sum().backward()
+    ref_out, ref_dv, ref_dg = _torch_wn_ref(x, model.v_all, model.g_all, model.dims)
+    ok, err, _ = orc.allclose_report(out.detach().float().cpu().numpy(), ref_out, 1e-2, 1e-2)
+    assert ok, f"out: {err}"
+    nw = 0
+    for i in range(5):
+        k, n = model.dims[i], model.dims[i + 1]
+        check_grad(model.v_all.grad[nw:nw + k * n].cpu().numpy(), ref_dv[nw:nw + k * n], f"dv{i + 1}")
+        nw += k * n
+    check_grad(model.g_all.grad.cpu().numpy(), ref_dg, "dg")
