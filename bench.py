@@ -204,11 +204,9 @@ def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
     return {"value": rows / el, "unit": "rows/s", "threads": torch.get_num_threads(), "sample": f"{reps} x {chunk} rows fp32"}
 
 
-TRAIN_BYTES_PER_ROW = 3072  # x 256 + out 256 + stash 1024 written; g 256 + stash 1024 + x 256 read
-TRAIN_FLOP_PER_ROW = 262144  # fwd 98,304 + dgrad 2 x 32,768 + wgrad 3 x 32,768 (no dx)
 
 
-def train_step_bench(torch, m, steps=50, warmup=10):
+def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3):
     """One training step of BASELINE config 5 through the drop-in module:
     weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
     megakernel + weight-norm backward, x without grad.  Timed with HIP events
@@ -217,7 +215,7 @@ def train_step_bench(torch, m, steps=50, warmup=10):
     import fused_mlp
 
     torch.manual_seed(0)
-    model = fused_mlp.FusedMLPSoftplusWN().cuda()
+    model = fused_mlp.FusedMLPSoftplusWN(n_layers=n_layers).cuda()
     x = torch.randn(m, 128, device="cuda").half()
 
     def step(_):
@@ -245,14 +243,19 @@ def train_step_bench(torch, m, steps=50, warmup=10):
         model(x).sum().backward()
     with gc_paused():
         gms = time_launches(torch, lambda i: graph.replay(), steps, warmup)
+    # per row: x + out + stash written in the forward; dout, stash, x read
+    # back (no dx).  Flops: forward 2*sum(in*out), dgrad of layers 1.., wgrad.
+    nbytes = 256 + 256 + 512 * (n_layers - 1) + 256 + 512 * (n_layers - 1) + 256
+    flop = 32768 * (3 * n_layers - 1)
     return {
         "ms_per_step": round(ms, 5),
         "rows_per_s": m / (ms * 1e-3),
-        "achieved_gbs": round(TRAIN_BYTES_PER_ROW * m / (ms * 1e-3) / 1e9, 1),
-        "tflops": round(TRAIN_FLOP_PER_ROW * m / (ms * 1e-3) / 1e12, 2),
+        "achieved_gbs": round(nbytes * m / (ms * 1e-3) / 1e9, 1),
+        "tflops": round(flop * m / (ms * 1e-3) / 1e12, 2),
         "graph_ms_per_step": round(gms, 5),
         "graph_rows_per_s": m / (gms * 1e-3),
-        "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd",
+        "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd" if n_layers == 3 else
+                    "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..2, then 1..0) + wn_bwd",
     }
 
 
@@ -278,7 +281,8 @@ def main():
     ap.add_argument("--m", type=int, default=None)
     ap.add_argument("--sweep", action="store_true", help="add the M=64..4096 latency sweep")
     ap.add_argument("--train", action="store_true",
-                    help="add the training step (3L + weight norm, loss = out.sum()) at M = 4096, 16384, 131072")
+                    help="add the training step (3L + weight norm, loss = out.sum()) at M = 4096, 16384, 131072, "
+                         "and the 5-layer one at M = 65536, 131072")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     args = ap.parse_args()
@@ -396,6 +400,7 @@ def main():
 
     if args.train:
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
+        result["training_5l"] = {str(mt): train_step_bench(torch, mt, n_layers=5) for mt in (65536, 131072)}
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(orc, dims, uniform, budget_s=args.cpu_budget)
