@@ -159,8 +159,9 @@ struct BwdWave {
   int lane, n, g, wid;
   int64_t row0;    // first row of this wave's 32 in the current round
   int64_t rstep;   // rows between a workgroup's consecutive rounds
-  int wo[8];       // exchange-tile write slots of this lane's row, feature 8g + j
+  int wo[4];       // exchange-tile write slots: feature n of a block, rows 8a + 4g .. +3
   int rd;          // exchange-tile read column of fragment row 0 (XOR 16kk for step kk)
+  f16x8 eye[2];    // B operands of the exact transpose: column n <- K-step feature n - 16h
   f32x16 (&wacc)[Gm::ntpw()];
 
   // Prefetched rows (issued one phase ahead of their use).
@@ -169,10 +170,15 @@ struct BwdWave {
   f16x8 xbuf[KS0];     // x rows
 
   __device__ __forceinline__ void init_slots() {
-    const int r = wid * 32 + n;  // row within the round
+    // Element (f, r) of a tile sits at f*R + (r ^ 8*(f & 15)); for feature
+    // 32t + n of block t the XOR term is 8*(n & 15) whatever t is.
 #pragma unroll
-    for (int j = 0; j < 8; ++j) wo[j] = (8 * g + j) * R + (r ^ ((64 * g + 8 * j) & (R - 1)));
+    for (int a = 0; a < 4; ++a) wo[a] = n * R + ((wid * 32 + 8 * a + 4 * g) ^ ((8 * (n & 15)) & (R - 1)));
     rd = (8 * g) ^ ((8 * (lane & 15)) & (R - 1));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) eye[h][j] = (f16)(n == 8 * g + j + 16 * h ? 1.0f : 0.0f);
   }
 
   __device__ __forceinline__ uint32_t nrows_at(int64_t r0) const {
@@ -221,10 +227,27 @@ struct BwdWave {
           f16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)((n * N::d[0] + 16 * s + 8 * g) * 2), 0, 0));
   }
 
-  // This lane's 8 features 16s + 8g + [0..7] of its row into an exchange tile.
-  __device__ __forceinline__ void xwrite(f16* t, int s, f16x8 v) const {
+  // Writes the wave's 32 rows of KS K-steps of features (row-per-lane B
+  // operands v[s]: row n, features 16s + 8g + [0..7]) into an exchange tile
+  // laid out [feature][row].  The transpose runs on the matrix core: with v[s]
+  // as the A operand and eye[s & 1] as B, D[r][c] = v_row_r[32t + c] exactly
+  // (one product by 1.0 per output, fp32 accumulation), and the D layout gives
+  // each lane one feature and four consecutive rows per register group, so
+  // each 32-feature block leaves as four 8-byte writes per lane instead of 32
+  // two-byte ones.  (An inf in a K-step group turns that group's row into NaN
+  // through inf * 0; it only arises from an overflowed forward.)
+  template <int KS>
+  __device__ __forceinline__ void xwrite(f16* t, const f16x8 (&v)[KS]) const {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[wo[j] + 16 * s * R] = v[j];
+    for (int blk = 0; blk < (KS + 1) / 2; ++blk) {
+      f32x16 d = mfma32x32x16(v[2 * blk], eye[0], (f32x16){});
+      if (2 * blk + 1 < KS) d = mfma32x32x16(v[2 * blk + 1], eye[1], d);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f16x2 lo = cvt2(d[4 * a], d[4 * a + 1]), hi = cvt2(d[4 * a + 2], d[4 * a + 3]);
+        *reinterpret_cast<f16x4*>(t + wo[a] + 32 * blk * R) = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+      }
+    }
   }
   // 16-byte fragment: rows 16kk + 8g .. +7 of feature fb + (lane & 31), fb % 32 == 0.
   __device__ __forceinline__ f16x8 xread(const f16* t, int fb, int kk) const {
@@ -274,14 +297,20 @@ struct BwdWave {
     constexpr int KSA = N::d[l] / 16;      // K-steps of a_l
     constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
     constexpr bool HA = l >= 1 || SEG;     // a_l came from a stash (fp32, in hbuf)
+    {
+      f16x8 zs[KSZ];
 #pragma unroll
-    for (int s = 0; s < KSZ; ++s) xwrite(tz, s, dz[s]);
+      for (int s = 0; s < KSZ; ++s) zs[s] = dz[s];
+      xwrite(tz, zs);
+    }
+    if constexpr (HA) {
+      f16x8 as[KSA];
 #pragma unroll
-    for (int s = 0; s < KSA; ++s) {
-      if constexpr (HA)
-        xwrite(ta, s, pack8(hbuf[s][0], hbuf[s][1], hbuf[s][2], hbuf[s][3], hbuf[s][4], hbuf[s][5], hbuf[s][6], hbuf[s][7]));
-      else
-        xwrite(ta, s, xbuf[s]);
+      for (int s = 0; s < KSA; ++s)
+        as[s] = pack8(hbuf[s][0], hbuf[s][1], hbuf[s][2], hbuf[s][3], hbuf[s][4], hbuf[s][5], hbuf[s][6], hbuf[s][7]);
+      xwrite(ta, as);
+    } else {
+      xwrite(ta, xbuf);
     }
     if constexpr (Gm::has_dgrad(l)) {
       constexpr int MB = N::d[l] / 32;
@@ -411,7 +440,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   f32x16 wacc[Gm::ntpw()];
 #pragma unroll
   for (int k = 0; k < Gm::ntpw(); ++k) wacc[k] = (f32x16){};
-  BwdWave<N, NW, DX, SEG> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, {}, 0, wacc};
+  BwdWave<N, NW, DX, SEG> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, {}, 0, {}, wacc};
   wv.init_slots();
 
   // Every wave of a workgroup runs the same rounds (the barriers need all of them).
