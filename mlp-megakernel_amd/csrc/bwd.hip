@@ -151,17 +151,18 @@ struct BwdWave {
   static constexpr int KSH = Gm::kshid();
   static constexpr int KS0 = N::d[0] / 16;
   static constexpr int KSL = N::d[L] / 16;
+  static constexpr int FA = Gm::fa(), FZ = Gm::fz();  // features per exchange-tile row
 
   const BwdParams& p;
   const f16x8* wfr;  // staged dgrad fragments
-  f16* ta;           // exchange tile: a_l, [feature][row]
-  f16* tz;           // exchange tile: dz_l, [feature][row]
+  f16* ta;           // exchange tile: a_l, [row][feature] (FA features per row)
+  f16* tz;           // exchange tile: dz_l, [row][feature] (FZ features per row)
   int lane, n, g, wid;
   int64_t row0;    // first row of this wave's 32 in the current round
   int64_t rstep;   // rows between a workgroup's consecutive rounds
-  int wo[4];       // exchange-tile write slots: feature n of a block, rows 8a + 4g .. +3
-  int rd;          // exchange-tile read column of fragment row 0 (XOR 16kk for step kk)
-  f16x8 eye[2];    // B operands of the exact transpose: column n <- K-step feature n - 16h
+  int wsw;         // swizzle of this lane's row (the row it writes)
+  int rrow[2];     // rows (within a K-step of 16) of this lane's two transposed reads
+  int rcol;        // first of the 4 features the lane addresses in a read, less the block base
   f32x16 (&wacc)[Gm::ntpw()];
 
   // Prefetched rows (issued one phase ahead of their use).
@@ -169,19 +170,29 @@ struct BwdWave {
   float hbuf[KSH][8];  // h_l of the next phase, fp32
   f16x8 xbuf[KS0];     // x rows
 
-  __device__ __forceinline__ void init_slots() {
-    // Element (f, r) of a tile sits at f*R + (r ^ 8*(f & 15)); for feature
-    // 32t + n of block t the XOR term is 8*(n & 15) whatever t is.
-#pragma unroll
-    for (int a = 0; a < 4; ++a) wo[a] = n * R + ((wid * 32 + 8 * a + 4 * g) ^ ((8 * (n & 15)) & (R - 1)));
-    rd = (8 * g) ^ ((8 * (lane & 15)) & (R - 1));
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) eye[h][j] = (f16)(n == 8 * g + j + 16 * h ? 1.0f : 0.0f);
+  // Tile layout: element (r, f) of a tile with F features per row sits at
+  // r*F + (f ^ swz(r, F)).  The XOR moves whole 8-feature chunks, so every
+  // 16-byte write and every 8-byte transposed read stays contiguous; eight
+  // consecutive rows get eight distinct chunk slots (the writes of 8 lanes,
+  // one row each, hit distinct banks) and rows r .. r+3 of one read land in
+  // four distinct 16-feature windows.
+  static __device__ __forceinline__ int swz(int r, int F) {
+    return (16 * (r & 3) + 8 * ((r >> 2) & 1) + 64 * ((r >> 3) & 1)) & (F - 1);
   }
 
-  __device__ __forceinline__ uint32_t nrows_at(int64_t r0) const {
+  __device__ __forceinline__ void init_slots() {
+    wsw = wid * 32 + n;  // the row this lane writes (swizzle taken per tile width)
+    // ds_read_b64_tr_b16, per 16-lane group: result lane i, element j is
+    // element (i & 3) of the 8 bytes addressed by lane (i >> 2) + 4j.  Lane
+    // 4j + c of group q addresses row 8*(q >> 1) + j (+4 for the second read)
+    // and features 16*(q & 1) + 4c .. +3 of the fragment's 32, so result lane
+    // i gets feature 16*(q & 1) + i of rows 8*(q >> 1) + 0..3 (then 4..7):
+    // the 8 K-values of MFMA operand lane (m = lane & 31, g = lane >> 5).
+    const int q = lane >> 4, i = lane & 15;
+    rrow[0] = 8 * (q >> 1) + (i >> 2);
+    rrow[1] = rrow[0] + 4;
+    rcol = 16 * (q & 1) + 4 * (i & 3);
+  }  __device__ __forceinline__ uint32_t nrows_at(int64_t r0) const {
     const int64_t left = p.M - r0;
     return (uint32_t)(left < 32 ? (left > 0 ? left : 0) : 32);
   }
@@ -228,30 +239,28 @@ struct BwdWave {
   }
 
   // Writes the wave's 32 rows of KS K-steps of features (row-per-lane B
-  // operands v[s]: row n, features 16s + 8g + [0..7]) into an exchange tile
-  // laid out [feature][row].  The transpose runs on the matrix core: with v[s]
-  // as the A operand and eye[s & 1] as B, D[r][c] = v_row_r[32t + c] exactly
-  // (one product by 1.0 per output, fp32 accumulation), and the D layout gives
-  // each lane one feature and four consecutive rows per register group, so
-  // each 32-feature block leaves as four 8-byte writes per lane instead of 32
-  // two-byte ones.  (An inf in a K-step group turns that group's row into NaN
-  // through inf * 0; it only arises from an overflowed forward.)
-  template <int KS>
+  // operands v[s]: row n, features 16s + 8g + [0..7]) into an exchange tile:
+  // one 16-byte write per K-step, straight from the registers.
+  template <int F, int KS>
   __device__ __forceinline__ void xwrite(f16* t, const f16x8 (&v)[KS]) const {
+    const int r = wsw, sw = swz(r, F);
 #pragma unroll
-    for (int blk = 0; blk < (KS + 1) / 2; ++blk) {
-      f32x16 d = mfma32x32x16(v[2 * blk], eye[0], (f32x16){});
-      if (2 * blk + 1 < KS) d = mfma32x32x16(v[2 * blk + 1], eye[1], d);
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const f16x2 lo = cvt2(d[4 * a], d[4 * a + 1]), hi = cvt2(d[4 * a + 2], d[4 * a + 3]);
-        *reinterpret_cast<f16x4*>(t + wo[a] + 32 * blk * R) = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
-      }
-    }
+    for (int s = 0; s < KS; ++s) *reinterpret_cast<f16x8*>(t + r * F + ((16 * s + 8 * g) ^ sw)) = v[s];
   }
-  // 16-byte fragment: rows 16kk + 8g .. +7 of feature fb + (lane & 31), fb % 32 == 0.
+  // MFMA operand for features fb .. fb+31 (fb % 32 == 0) over rows
+  // 16kk .. 16kk+15 of the round: lane (m, g) gets rows 16kk + 8g + [0..7] of
+  // feature fb + m, through two transposing LDS reads.
+  template <int F>
   __device__ __forceinline__ f16x8 xread(const f16* t, int fb, int kk) const {
-    return *reinterpret_cast<const f16x8*>(t + (fb + (lane & 31)) * R + (rd ^ (16 * kk)));
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    s16x4 h[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int r = rrow[k];  // swz(16kk + r) == swz(r)
+      const f16* a = t + (16 * kk + r) * F + ((fb + rcol) ^ swz(r, F));
+      h[k] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)const_cast<f16*>(a));
+    }
+    return __builtin_bit_cast(f16x8, __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7));
   }
 
   // Wgrad of layer l over the R rows in the exchange tiles, for this wave's
@@ -267,8 +276,8 @@ struct BwdWave {
         for (int k = 0; k < Gm::quads(l) / NW; ++k) {
           const int q = wid + k * NW;
           const int fi = 64 * (q / QO), fo = 64 * (q % QO);
-          const f16x8 a0 = xread(ta, fi, kk), a1 = xread(ta, fi + 32, kk);
-          const f16x8 b0 = xread(tz, fo, kk), b1 = xread(tz, fo + 32, kk);
+          const f16x8 a0 = xread<FA>(ta, fi, kk), a1 = xread<FA>(ta, fi + 32, kk);
+          const f16x8 b0 = xread<FZ>(tz, fo, kk), b1 = xread<FZ>(tz, fo + 32, kk);
           wacc[OFF + 4 * k + 0] = mfma32x32x16(a0, b0, wacc[OFF + 4 * k + 0]);
           wacc[OFF + 4 * k + 1] = mfma32x32x16(a0, b1, wacc[OFF + 4 * k + 1]);
           wacc[OFF + 4 * k + 2] = mfma32x32x16(a1, b0, wacc[OFF + 4 * k + 2]);
@@ -280,7 +289,8 @@ struct BwdWave {
         for (int k = 0; k < Gm::tpw(l); ++k) {
           const int t = wid + k * NW;
           if (Gm::tiles(l) % NW == 0 || t < Gm::tiles(l))
-            wacc[OFF + k] = mfma32x32x16(xread(ta, 32 * (t / WOB), kk), xread(tz, 32 * (t % WOB), kk), wacc[OFF + k]);
+            wacc[OFF + k] =
+                mfma32x32x16(xread<FA>(ta, 32 * (t / WOB), kk), xread<FZ>(tz, 32 * (t % WOB), kk), wacc[OFF + k]);
         }
       }
     }
@@ -301,16 +311,16 @@ struct BwdWave {
       f16x8 zs[KSZ];
 #pragma unroll
       for (int s = 0; s < KSZ; ++s) zs[s] = dz[s];
-      xwrite(tz, zs);
+      xwrite<FZ>(tz, zs);
     }
     if constexpr (HA) {
       f16x8 as[KSA];
 #pragma unroll
       for (int s = 0; s < KSA; ++s)
         as[s] = pack8(hbuf[s][0], hbuf[s][1], hbuf[s][2], hbuf[s][3], hbuf[s][4], hbuf[s][5], hbuf[s][6], hbuf[s][7]);
-      xwrite(ta, as);
+      xwrite<FA>(ta, as);
     } else {
-      xwrite(ta, xbuf);
+      xwrite<FA>(ta, xbuf);
     }
     if constexpr (Gm::has_dgrad(l)) {
       constexpr int MB = N::d[l] / 32;
@@ -440,7 +450,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   f32x16 wacc[Gm::ntpw()];
 #pragma unroll
   for (int k = 0; k < Gm::ntpw(); ++k) wacc[k] = (f32x16){};
-  BwdWave<N, NW, DX, SEG> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, {}, 0, {}, wacc};
+  BwdWave<N, NW, DX, SEG> wv{p, wfr, ta, tz, lane, lane & 31, lane >> 5, wid, 0, (int64_t)gridDim.x * R, 0, {}, 0, wacc};
   wv.init_slots();
 
   // Every wave of a workgroup runs the same rounds (the barriers need all of them).
