@@ -106,6 +106,14 @@ struct BwdGeom {
     return m;
   }
   static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
+  // Per-layer prefetch: every stash layer (and x) gets its own register
+  // buffer, reloaded for the next round right after its last use, so each
+  // load has a whole round to arrive instead of one wgrad.  Measured at
+  // M = 131072: the two-layer kernel (lower half of the 5-layer backward)
+  // 37.5 -> 34.4 us; the 3-layer 128-wide kernel spills with it, and the
+  // narrow one gains nothing (20.6 vs 21.2 us), so they share one buffer
+  // loaded one phase ahead.
+  static constexpr bool pf() { return !SEG && L <= 2; }
   // Element offset of dW_l in the dW blocks laid out back to back.
   static constexpr int woff(int l) {
     int o = 0;
@@ -166,8 +174,9 @@ struct BwdWave {
   f32x16 (&wacc)[Gm::ntpw()];
 
   // Prefetched rows (issued one phase ahead of their use).
-  f16x8 gbuf[KSL];     // dL/dout of the round = dz_{L-1}
-  float hbuf[KSH][8];  // h_l of the next phase, fp32
+  static constexpr bool PF = Gm::pf();
+  f16x8 gbuf[KSL];                 // dL/dout of the round = dz_{L-1}
+  float hbuf[PF ? L : 1][KSH][8];  // h_l, fp32: buffer l (PF) or one shared buffer
   f16x8 xbuf[KS0];     // x rows
 
   // Tile layout: element (r, f) of a tile with F features per row sits at
@@ -217,6 +226,7 @@ struct BwdWave {
   // r0: 8 consecutive features per K-step.
   template <int l>
   __device__ __forceinline__ void load_h(int64_t r0) {
+    constexpr int B = PF ? l : 0;
     const rsrc_t hr = rows_rsrc(l == 0 ? p.h0 : p.stash[l > 0 ? l - 1 : 0], N::d[l], 4, r0);
 #pragma unroll
     for (int s = 0; s < N::d[l] / 16; ++s) {
@@ -225,8 +235,8 @@ struct BwdWave {
       const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, 0));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        hbuf[s][j] = lo[j];
-        hbuf[s][4 + j] = hi[j];
+        hbuf[B][s][j] = lo[j];
+        hbuf[B][s][4 + j] = hi[j];
       }
     }
   }
@@ -307,6 +317,7 @@ struct BwdWave {
     constexpr int KSA = N::d[l] / 16;      // K-steps of a_l
     constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
     constexpr bool HA = l >= 1 || SEG;     // a_l came from a stash (fp32, in hbuf)
+    constexpr int B = PF ? l : 0;          // its buffer
     {
       f16x8 zs[KSZ];
 #pragma unroll
@@ -317,7 +328,8 @@ struct BwdWave {
       f16x8 as[KSA];
 #pragma unroll
       for (int s = 0; s < KSA; ++s)
-        as[s] = pack8(hbuf[s][0], hbuf[s][1], hbuf[s][2], hbuf[s][3], hbuf[s][4], hbuf[s][5], hbuf[s][6], hbuf[s][7]);
+        as[s] = pack8(hbuf[B][s][0], hbuf[B][s][1], hbuf[B][s][2], hbuf[B][s][3], hbuf[B][s][4], hbuf[B][s][5],
+                      hbuf[B][s][6], hbuf[B][s][7]);
       xwrite<FA>(ta, as);
     } else {
       xwrite<FA>(ta, xbuf);
@@ -338,8 +350,8 @@ struct BwdWave {
           float v[16];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[2 * mb][j] * kLog2e));
-            v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[2 * mb + 1][j] * kLog2e));
+            v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[B][2 * mb][j] * kLog2e));
+            v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[B][2 * mb + 1][j] * kLog2e));
           }
           const f16x8 lo = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
           const f16x8 hi = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
@@ -362,7 +374,12 @@ struct BwdWave {
       }
     }
     __syncthreads();  // every wave's rows are in the exchange tiles
-    if constexpr (l >= 2 || (l == 1 && SEG)) {
+    if constexpr (PF) {  // this layer's buffer is free: the next round's rows
+      if constexpr (HA)
+        load_h<l>(row0 + rstep);
+      else
+        load_x(row0 + rstep);
+    } else if constexpr (l >= 2 || (l == 1 && SEG)) {
       load_h<l - 1>(row0);
     } else if constexpr (l == 1) {
       load_x(row0);
@@ -372,6 +389,16 @@ struct BwdWave {
     }
     wgrad<l>();
     __syncthreads();  // the tiles are free for the next layer
+  }
+
+  // First round with per-layer prefetch: every layer's rows.
+  template <int l>
+  __device__ __forceinline__ void prefetch_all(int64_t r0) {
+    if constexpr (l >= 1 || SEG)
+      load_h<l>(r0);
+    else
+      load_x(r0);
+    if constexpr (l > 0) prefetch_all<l - 1>(r0);
   }
 
   template <int l>
@@ -384,6 +411,7 @@ struct BwdWave {
     f16x8 dz[KSM], dzn[KSM];
 #pragma unroll
     for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
+    if constexpr (PF) load_dout(row0 + rstep);
     phases_from<L - 1>(dz, dzn);
   }
 
@@ -457,7 +485,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   const int64_t nrounds = (p.M + R - 1) / R;
   wv.row0 = (int64_t)blockIdx.x * R + wid * 32;
   wv.load_dout(wv.row0);
-  if constexpr (N::L >= 2) wv.template load_h<N::L - 1>(wv.row0);
+  if constexpr (BwdWave<N, NW, DX, SEG>::PF) {
+    wv.template prefetch_all<N::L - 1>(wv.row0);
+  } else if constexpr (N::L >= 2) {
+    wv.template load_h<N::L - 1>(wv.row0);
+  }
   for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
     wv.round();
     wv.row0 += wv.rstep;
