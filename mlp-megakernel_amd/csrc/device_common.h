@@ -110,13 +110,23 @@ __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, f
   return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Running maximum of packed sp2 values: four v_pk_maximum3_f16 per 16 values.
-// The maximum propagates NaN.
+// Running maximum of packed sp2 values; the maximum propagates NaN.
+// CHAIN: max(max(m, a), b) folds into one v_pk_maximum3_f16 per two packed
+// values (4 per call); the pairwise tree costs ~6 per call but leaves the
+// scheduler more freedom, which the stash kernels need to stay spill-free.
+template <bool CHAIN>
 __device__ __forceinline__ f16x2 sp2_track(f16x2 m, f16x8 lo, f16x8 hi) {
-  m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(lo.s01, lo.s23));
-  m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(lo.s45, lo.s67));
-  m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(hi.s01, hi.s23));
-  return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(hi.s45, hi.s67));
+  if constexpr (CHAIN) {
+    m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, lo.s01), lo.s23);
+    m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, lo.s45), lo.s67);
+    m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, hi.s01), hi.s23);
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, hi.s45), hi.s67);
+  } else {
+    m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(lo.s01, lo.s23));
+    m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(lo.s45, lo.s67));
+    m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(hi.s01, hi.s23));
+    return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(hi.s45, hi.s67));
+  }
 }
 // True on every lane of the wave when some lane's tracked maximum is not below
 // 128.  A finite sp2 below 2^7 rounds to at most 128 in fp16, so this catches

@@ -299,7 +299,7 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       }
       const f16x8 lo = pack8(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
       const f16x8 hi = pack8(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
-      if constexpr (!EXACT) m = sp2_track(m, lo, hi);
+      if constexpr (!EXACT) m = sp2_track<!STASH>(m, lo, hi);
       if constexpr (STASH) {
         const rsrc_t sr = io.stash[l];
         float h[16];
