@@ -11,8 +11,9 @@ Same public surface as /root/reference/kernel.py:
   * ``NUM_SMS`` (kernel.py:18) is read lazily on first access instead of at
     import, so importing this module needs no GPU.
 
-The launch goes to the hand-written gfx950 HIP megakernel in ``libmlpmk.so``
-(``mlp-megakernel_amd/csrc/fwd.hip``) through its C ABI.  There is no Triton
+The launch goes to the hand-written gfx950 HIP megakernels in ``libmlpmk.so``
+(``mlp-megakernel_amd/csrc/fwd.hip``, ``fwd_split.hip`` for small batches)
+through its C ABI.  There is no Triton
 and no fallback: without the library every call raises.
 """
 import torch
@@ -22,9 +23,10 @@ import torch.nn.functional as F
 import _mlpmk  # noqa: F401  (registers the package as ``mlpmk``)
 from mlpmk import ops as _ops
 
-# Waves per workgroup of the gfx950 inference forward (mlp-megakernel_amd/csrc/fwd.hip):
-# 12 (3 per SIMD) for 128-wide layers, 16 for the narrow network.
-_WAVES_PER_WG_WIDE = 12
+# gfx950 launch policy of the inference forward (mlp-megakernel_amd/csrc/fwd.hip
+# and fwd_split.hip), mirrored here for _pick_config.
+_MI355X_CUS = 256
+_WAVES_PER_WG_WIDE = 12  # one-block-per-wave kernel, 3 waves per SIMD
 _WAVES_PER_WG_NARROW = 16
 
 
@@ -34,22 +36,37 @@ def __getattr__(name):
     raise AttributeError(name)
 
 
-def _pick_config(M, K1, N1, N2, N3, fp32=False):
+def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
     """gfx950 launch policy in the reference's tuple shape
-    ``(BM, BN3, BK1, BK2, BK3, warps)`` (kernel.py:25-53).
+    ``(BM, BN3, BK1, BK2, BK3, warps)`` (kernel.py:25-53), as the library
+    applies it for the 3-layer network at this M.
 
-    BM = rows a wave computes per block (32: one MFMA batch block), BN3 = the whole
-    output width (one pass computes every output column), BK* = 16 (the K of
-    v_mfma_f32_32x32x16_f16), warps = 64-lane waves per workgroup.  The
-    persistent grid is min(CUs x occupancy, ceil(M / (BM * warps))) and the
-    waves of a workgroup claim its row blocks from an LDS counter.  ``fp32``
-    inputs are not supported by the main-branch surface either
-    (/root/reference/AGENTS.md:86-88).
+    BM = rows per block (32: one MFMA batch block; 64 for the narrow network's
+    one-block-per-wave kernel, which reads each weight fragment for two
+    blocks), BN3 = the whole output width (a workgroup computes every output
+    column), BK* = 16 (the K of v_mfma_f32_32x32x16_f16), warps = 64-lane waves
+    per workgroup:
+      * up to one 32-row block per CU (two for the narrow network): the
+        feature-split kernel, one wave per 32 output features (4 waves, 2 for
+        the narrow network) sharing each block;
+      * otherwise the persistent one-block-per-wave kernel with 4 waves per
+        workgroup up to 4 blocks per CU, 8 up to 8, then 12 (16 narrow).
+    ``num_cus`` defaults to ``NUM_SMS`` on a GPU and to MI355X's 256
+    otherwise.  ``fp32`` inputs are not supported by the main-branch surface
+    either (/root/reference/AGENTS.md:86-88).
     """
     if fp32:
         raise TypeError("the fused forward takes fp16 inputs (main-branch surface is fp16 only)")
+    if num_cus is None:
+        num_cus = NUM_SMS if torch.cuda.is_available() else _MI355X_CUS  # noqa: F821 (module __getattr__)
     narrow = max(K1, N1, N2, N3) <= 64
-    return 32, N3, 16, 16, 16, _WAVES_PER_WG_NARROW if narrow else _WAVES_PER_WG_WIDE
+    if -(-M // 32) <= (2 if narrow else 1) * num_cus:
+        return 32, N3, 16, 16, 16, 2 if narrow else 4
+    bm = 64 if narrow else 32
+    blocks = -(-M // bm)
+    warps = 4 if blocks <= 4 * num_cus else 8 if blocks <= 8 * num_cus else (
+        _WAVES_PER_WG_NARROW if narrow else _WAVES_PER_WG_WIDE)
+    return bm, N3, 16, 16, 16, warps
 
 
 def _fused_mlp_fwd(x, w1, w2, w3):

@@ -102,6 +102,18 @@ __device__ __forceinline__ f16x2 cvt2(float a, float b) {
   return __builtin_convertvector((f32x2){a, b}, f16x2);  // v_cvt_pk_f16_f32 (RNE)
 }
 
+// A staged weight: w * sc rounded to fp32, then to fp16 (RNE both times).  The
+// opaque step keeps the compiler from fusing the multiply and the conversion
+// into a single-rounding v_fma_mix in some staging paths and not in others:
+// the two roundings differ by one fp16 ulp for a few weights, and every
+// kernel (any launch shape, inference or training forward) must stage the
+// same bits.
+__device__ __forceinline__ f16 scaled_weight(f16 w, float sc) {
+  float t = (float)w * sc;
+  asm volatile("" : "+v"(t));
+  return (f16)t;
+}
+
 __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, float a4, float a5,
                                        float a6, float a7) {
   f16x2 p0 = cvt2(a0, a1), p1 = cvt2(a2, a3), p2 = cvt2(a4, a5), p3 = cvt2(a6, a7);

@@ -60,7 +60,7 @@ __device__ __forceinline__ f16x8 weight_fragment(const FwdParams& p, int l, int 
   if (of < Nout) {
     const f16* src = p.w[l] + (int64_t)(16 * s + 8 * g) * Nout + of;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (f16)((float)src[(int64_t)j * Nout] * wscale<N>(l));
+    for (int j = 0; j < 8; ++j) v[j] = scaled_weight(src[(int64_t)j * Nout], wscale<N>(l));
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = (f16)0.0f;
@@ -68,16 +68,110 @@ __device__ __forceinline__ f16x8 weight_fragment(const FwdParams& p, int l, int 
   return v;
 }
 
+// Staging tasks: task (l, kb, cb) covers the 8 x 8 tile of W_l at input rows
+// 8kb.. and output columns 8cb.. (columns padded to whole 32-feature blocks).
+template <class N>
+struct StageTasks {
+  static constexpr int cbs(int l) { return N::mbs(l) * 4; }
+  static constexpr int count(int l) { return (N::d[l] / 8) * cbs(l); }
+  static constexpr int first(int l) {
+    int o = 0;
+    for (int i = 0; i < l; ++i) o += count(i);
+    return o;
+  }
+  static constexpr int total() { return first(N::L); }
+};
+
+// Task t of layer l: eight 16-byte row loads of the tile (consecutive tasks
+// take consecutive column blocks, so a wave's loads cover whole W rows), an
+// 8 x 8 transpose in registers, and eight 16-byte LDS writes.  The tile's
+// rows are input features 16s + 8g + [0..7] (s = kb / 2, g = kb % 2) and its
+// 8 columns are outfeat(mb, i) for 8 lanes i of one fragment, so column q
+// becomes lane (i, g)'s whole 16 bytes of fragment (mb, s).
+template <class N, int l>
+__device__ __forceinline__ void stage_load(const FwdParams& p, f16x8 (&r)[8], int t) {
+  constexpr int Nout = N::d[l + 1], CB = StageTasks<N>::cbs(l);
+  const int kb = t / CB, cb = t % CB;
+  if (8 * cb < Nout) {
+    const f16* src = p.w[l] + (int64_t)(8 * kb) * Nout + 8 * cb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = *reinterpret_cast<const f16x8*>(src + (int64_t)j * Nout);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = f16x8{};
+  }
+}
+
+template <class N, int l, int RF>
+__device__ __forceinline__ void stage_store(f16x8* lds, const f16x8 (&r)[8], int t) {
+  constexpr int CB = StageTasks<N>::cbs(l), KS = N::ks(l);
+  const int kb = t / CB, cb = t % CB;
+  const float sc = wscale<N>(l);
+  const int s = kb >> 1, g = kb & 1;
+  const int c0 = 8 * cb, mb = c0 >> 5;
+  // outfeat(mb, i) = 32mb + 16 i4 + 8 i2 + 4 i3 + (i & 3) for i = 16 i4 + 8 i3 + 4 i2 + (i & 3).
+  const int ibase = 16 * ((c0 >> 4) & 1) + 4 * ((c0 >> 3) & 1);
+  const int f = N::frag_off(l) + mb * KS + s;
+  if (f < RF) return;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = ibase + 8 * (q >> 2) + (q & 3);
+    f16x8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = scaled_weight(r[j][q], sc);
+    lds[(f - RF) * 64 + 32 * g + i] = v;
+  }
+}
+
+// Task t (counted over all layers) -> its layer's stage_load / stage_store.
+template <class N, int l>
+__device__ __forceinline__ void stage_load_any(const FwdParams& p, f16x8 (&r)[8], int t) {
+  if constexpr (l < N::L) {
+    if (t < StageTasks<N>::first(l + 1)) stage_load<N, l>(p, r, t - StageTasks<N>::first(l));
+    else stage_load_any<N, l + 1>(p, r, t);
+  }
+}
+template <class N, int l, int RF>
+__device__ __forceinline__ void stage_store_any(f16x8* lds, const f16x8 (&r)[8], int t) {
+  if constexpr (l < N::L) {
+    if (t < StageTasks<N>::first(l + 1)) stage_store<N, l, RF>(lds, r, t - StageTasks<N>::first(l));
+    else stage_store_any<N, l + 1, RF>(lds, r, t);
+  }
+}
+
 // Stages every fragment from the RF-th on; fragment F lands at LDS slot F - RF.
+// When the 8 x 8 tasks give every thread of the workgroup at least one, they
+// replace the per-(fragment, lane) column gathers of weight_fragment() (same
+// values): 8x fewer load instructions, 3L-128 staging 6.0K -> 4.7K cycles,
+// 5L-128 11.0K -> 6.7K.  With fewer tasks than threads (the narrow network:
+// 128 tasks for 1024 threads) the gathers spread over all threads are faster
+// (2.0K vs 3.2K cycles).  A thread with several tasks issues all their loads
+// before its first LDS write, so the staging costs one memory round trip.
 template <class N, int NT, int RF>
 __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
+  constexpr int TOTAL = StageTasks<N>::total();
+  if constexpr (TOTAL >= NT) {
+    constexpr int TPT = (TOTAL + NT - 1) / NT;
+    f16x8 r[TPT][8];
 #pragma unroll
-  for (int l = 0; l < N::L; ++l) {
-    const int items = N::mbs(l) * N::ks(l) * 64;
-    for (int item = threadIdx.x; item < items; item += NT) {
-      const int f = item >> 6, lane = item & 63;
-      if (N::frag_off(l) + f < RF) continue;
-      lds[(N::frag_off(l) + f - RF) * 64 + lane] = weight_fragment<N>(p, l, f, lane);
+    for (int k = 0; k < TPT; ++k) {
+      const int t = threadIdx.x + k * NT;
+      if (TOTAL % NT == 0 || t < TOTAL) stage_load_any<N, 0>(p, r[k], t);
+    }
+#pragma unroll
+    for (int k = 0; k < TPT; ++k) {
+      const int t = threadIdx.x + k * NT;
+      if (TOTAL % NT == 0 || t < TOTAL) stage_store_any<N, 0, RF>(lds, r[k], t);
+    }
+  } else {
+#pragma unroll
+    for (int l = 0; l < N::L; ++l) {
+      const int items = N::mbs(l) * N::ks(l) * 64;
+      for (int item = threadIdx.x; item < items; item += NT) {
+        const int f = item >> 6, lane = item & 63;
+        if (N::frag_off(l) + f < RF) continue;
+        lds[(N::frag_off(l) + f - RF) * 64 + lane] = weight_fragment<N>(p, l, f, lane);
+      }
     }
   }
 }
@@ -579,9 +673,27 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
 // NB row blocks per fragment read and NW waves per workgroup for inference,
 // NBS and NWS with the fp32 stash (whose extra registers would spill at
 // NW = 12 for the 128-wide networks, and at NB = 2 for the narrow one).
+//
+// Small batches take narrower workgroups.  With NW waves per workgroup the
+// grid holds ceil(blocks / NW) workgroups, so with few blocks a 12-wave
+// workgroup packs three one-block waves onto each SIMD of a handful of CUs
+// (M = 4096: 11 CUs, each wave's block 14K cycles because three waves share
+// the SIMD) while the rest of the chip idles.  Up to 4 blocks per CU the
+// kernel runs 4-wave workgroups (one wave per SIMD), up to 8 blocks per CU
+// 8-wave workgroups; the persistent NW-wave kernel takes over beyond that.
 template <class N, int NB, int NW, int NBS, int NWS, int D>
 static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
-  return stash ? launch_fwd<N, NBS, true, NWS, D>(p, st) : launch_fwd<N, NB, false, NW, D>(p, st);
+  int cus = 0;
+  const int rc = current_device_cus(&cus);
+  if (rc != MLPMK_OK) return rc;
+  const int64_t nblk = (p.M + 32 * (stash ? NBS : NB) - 1) / (32 * (stash ? NBS : NB));
+  if (stash) {
+    if (NWS > 4 && nblk <= 4 * (int64_t)cus) return launch_fwd<N, NBS, true, 4, D>(p, st);
+    return launch_fwd<N, NBS, true, NWS, D>(p, st);
+  }
+  if (NW > 4 && nblk <= 4 * (int64_t)cus) return launch_fwd<N, NB, false, 4, D>(p, st);
+  if (NW > 8 && nblk <= 8 * (int64_t)cus) return launch_fwd<N, NB, false, 8, D>(p, st);
+  return launch_fwd<N, NB, false, NW, D>(p, st);
 }
 
 bool fwd_supported_dims(int L, const int* dims) {
@@ -589,7 +701,16 @@ bool fwd_supported_dims(int L, const int* dims) {
          dims_match<NetNarrow>(L, dims);
 }
 
+int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus);
+
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
+  int cus = 0;
+  const int rc = current_device_cus(&cus);
+  if (rc != MLPMK_OK) return rc;
+  // Small batches run the feature-split kernel (fwd_split.hip) when it has one
+  // for these widths and batch size.
+  const int rs = fwd_split_dispatch(L, dims, p, stash, st, cus);
+  if (rs != MLPMK_ERR_UNSUPPORTED_SHAPE) return rs;
   if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 1, 8, 1>(p, stash, st);
   if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 1, 8, 1>(p, stash, st);
   if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 16, 1, 16, 1>(p, stash, st);

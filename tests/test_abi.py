@@ -139,8 +139,19 @@ def test_python_wrappers_validate_before_the_library():
 def test_drop_in_modules_import_without_gpu():
     import kernel
 
-    assert kernel._pick_config(4096, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 12)
-    assert kernel._pick_config(4096, 32, 64, 64, 16) == (32, 16, 16, 16, 16, 16)
+    # MI355X (256 CUs): feature-split kernel up to one 32-row block per CU
+    # (two for the narrow network), then 4-, 8- and 12/16-wave workgroups.
+    cfg = kernel._pick_config
+    assert cfg(4096, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 4)
+    assert cfg(8192, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 4)
+    assert cfg(16384, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 4)
+    assert cfg(65536, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 8)
+    assert cfg(1048576, 128, 128, 128, 128) == (32, 128, 16, 16, 16, 12)
+    assert cfg(4096, 32, 64, 64, 16) == (32, 16, 16, 16, 16, 2)
+    assert cfg(16384, 32, 64, 64, 16) == (32, 16, 16, 16, 16, 2)
+    assert cfg(40000, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 4)
+    assert cfg(4194304, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 16)
+    assert cfg(4096, 128, 128, 128, 128, num_cus=8) == (32, 128, 16, 16, 16, 12)
     with pytest.raises(TypeError):
         kernel._pick_config(4096, 128, 128, 128, 128, fp32=True)
     assert callable(kernel._fused_mlp_fwd) and kernel.Model and kernel.ModelNew

@@ -84,6 +84,41 @@ def test_narrow_forward(m):
     _check(out, orc.forward(x, ws), f"narrow M={m}")
 
 
+@pytest.mark.parametrize(
+    "dims,m,uniform",
+    [
+        ((128, 128, 128, 128), 40000, False),  # 8-wave workgroups (1024 < blocks <= 2048)
+        ((128,) * 6, 20000, False),  # 4-wave workgroups (625 blocks)
+        ((32, 64, 64, 16), 100000, True),  # 8-wave workgroups, 64-row blocks
+    ],
+)
+def test_small_batch_launch_shapes(dims, m, uniform):
+    x, ws = orc.make_inputs(dims, m, seed=1, x_dist="uniform" if uniform else "normal")
+    xd, wd = _to_dev(x, ws)
+    out = ops.fwd(xd, wd).float().cpu().numpy()
+    _check(out, orc.forward(x, ws), f"{dims} M={m}")
+
+
+@pytest.mark.parametrize(
+    "dims,sizes,uniform",
+    [
+        ((128, 128, 128, 128), (4096, 16384, 65536, 1048576), False),
+        ((128,) * 6, (4096, 20000, 65536, 1048576), False),
+        ((32, 64, 64, 16), (4096, 40000, 131072, 4194304), True),
+    ],
+)
+def test_launch_shape_does_not_change_results(dims, sizes, uniform):
+    # The host picks the feature-split kernel (a block or two per CU), or 4-,
+    # 8- or NW-wave workgroups of the one-block-per-wave kernel, by batch size
+    # (the sizes here take each in turn); a row's result must not depend on
+    # which kernel computed it.
+    x, ws = _device_inputs(dims, max(sizes), seed=2, uniform=uniform)
+    outs = [ops.fwd(x[:m].contiguous(), ws) for m in sizes]
+    n = min(sizes)
+    for m, o in zip(sizes[1:], outs[1:]):
+        assert torch.equal(o[:n], outs[0]), f"{dims}: rows of M={m} differ from M={sizes[0]}"
+
+
 def _device_inputs(dims, m, seed, uniform=False):
     g = torch.Generator(device="cuda").manual_seed(seed)
     if uniform:
@@ -150,15 +185,16 @@ def test_threshold_edges_through_identity_weights():
     assert abs(out[0, 4] - np.log(3.0)) < 2e-3  # z = 0: softplus(softplus(0)) = log(1 + 2)
 
 
+# M = 256 runs the feature-split kernel, M = 16384 the one-block-per-wave one.
+@pytest.mark.parametrize("m", [256, 16384])
 @pytest.mark.parametrize("stash", [False, True])
-def test_large_preactivations_take_the_exact_path(stash):
+def test_large_preactivations_take_the_exact_path(stash, m):
     # Past z = 88.7 the kernel's direct softplus form overflows (2^u in base-2
     # units); such blocks are recomputed exactly and must give softplus(z) = z,
     # the reference's z > 20 branch (kernel.py:108), up to the fp16 limit of
     # the reference's hidden h (kernel.py:110).  Large rows sit among ordinary
     # ones inside the same 32-row blocks, and only some blocks have any.
     z = np.array([88.0, 88.8, 89.0, 100.0, 200.0, 1000.0, 3.0e4, 4.6e4, 5.0e4, 65504.0], dtype=np.float32)
-    m = 256
     rng = np.random.default_rng(11)
     x = (rng.standard_normal((m, 128)) * 0.5).astype(np.float16)
     rows = (3, 40, 41, 200)  # blocks 0, 1 and 6 of eight
@@ -178,13 +214,14 @@ def test_large_preactivations_take_the_exact_path(stash):
             assert ok, f"stash h{i + 1}: max|err| {err}"
 
 
+@pytest.mark.parametrize("m", [4096, 20000])
 @pytest.mark.parametrize("dims,stash", [((128, 128, 128, 128), False), ((128, 128, 128, 128), True),
                                         ((128,) * 6, False), ((32, 64, 64, 16), False)])
-def test_scaled_inputs_overflow_many_blocks(dims, stash):
+def test_scaled_inputs_overflow_many_blocks(dims, stash, m):
     # x scaled so that ~30 % of pre-activations exceed z = 88.7 in every
     # layer and every block takes the exact path; every 7th row keeps its
     # ordinary scale and shares those blocks.
-    x, ws = orc.make_inputs(dims, 4096, seed=21)
+    x, ws = orc.make_inputs(dims, m, seed=21)
     x = (x.astype(np.float32) * 300.0).astype(np.float16)
     small = np.zeros(len(x), dtype=bool)
     small[::7] = True
@@ -205,10 +242,11 @@ def test_scaled_inputs_overflow_many_blocks(dims, stash):
         assert torch.equal(res[0], ops.fwd(xd, wd))
 
 
-def test_inf_and_nan_inputs_propagate_like_the_oracle():
+@pytest.mark.parametrize("m", [128, 16384])
+def test_inf_and_nan_inputs_propagate_like_the_oracle(m):
     # inf * 0 inside the products gives NaN, as in the reference's fp32 dot;
     # rows without non-finite inputs are unaffected.
-    x, ws = orc.make_inputs((128, 128, 128, 128), 128, seed=4)
+    x, ws = orc.make_inputs((128, 128, 128, 128), m, seed=4)
     x[5, 7] = np.inf
     x[70, 0] = -np.inf
     x[99, 3] = np.nan
@@ -218,7 +256,7 @@ def test_inf_and_nan_inputs_propagate_like_the_oracle():
         ref = orc.forward(x, ws)
     assert np.array_equal(np.isnan(out), np.isnan(ref))
     fin = np.isfinite(ref).all(axis=1)
-    assert fin.sum() == 125
+    assert fin.sum() == m - 3
     _check(out[fin], ref[fin], "finite rows next to non-finite ones")
 
 
