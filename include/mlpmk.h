@@ -53,10 +53,19 @@ const char* mlpmk_status_string(int status);
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* mlpmk_last_error(void);
 
-/* 1 if a forward kernel exists for (num_layers, dims), else 0.  Host only. */
+/*
+ * 1 if a forward kernel exists for (num_layers, dims), else 0.  Host only.
+ * Supported: the compiled shapes 3 x 128-wide, 5 x 128-wide and 32-64-64-16,
+ * and any network of 2..5 layers whose input and hidden widths are multiples
+ * of 16 in [16, 128] and whose output width is in [1, 128] (runtime-width
+ * kernels, compiled at width 128 with the true widths as launch parameters;
+ * the reference's kernel takes tile-multiple K1, N1, N2 and masks N3,
+ * /root/reference/kernel.py:60-63,86-87).
+ */
 int mlpmk_fwd_supported(int num_layers, const int* dims);
 
-/* 1 if the backward kernel exists for (num_layers, dims), else 0.  Host only. */
+/* 1 if the backward kernel exists for (num_layers, dims), else 0.  Host only.
+ * The same shapes as mlpmk_fwd_supported. */
 int mlpmk_bwd_supported(int num_layers, const int* dims);
 
 /*
@@ -90,12 +99,13 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
  *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd
  *   dout             dL/dout, fp16, row l at dout + l * dout_row_stride
  *                    elements; dout_row_stride = 0 broadcasts one row
- *                    (the expanded ones of loss = out.sum())
+ *                    (the expanded ones of loss = out.sum()), otherwise a
+ *                    multiple of 8 (16-byte rows) not below the output width
  *   dx               NULL, or [M, dims[0]] fp16 (written)
  *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
  *                    caller zeroes them for a fresh gradient
- * The 5-layer network is supported through mlpmk_bwd_ws only (it hands dz
- * between two launches through the workspace); here it returns
+ * Networks of 4 and 5 layers are supported through mlpmk_bwd_ws only (they
+ * hand dz between two launches through the workspace); here they return
  * MLPMK_ERR_INVALID_ARG without touching the device.
  */
 int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
@@ -113,10 +123,10 @@ int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const*
  * (256 workgroups x 49152 dW elements).  Grids below 64 workgroups (small M)
  * keep the atomic flush, which is then cheaper, and leave the partial-sum
  * part of the workspace untouched.
- * The 5-layer 128-wide backward runs as two launches: layers 4..2 (their
- * dgrad weights and exchange tiles fill one workgroup's 160 KiB of LDS),
- * whose fp16 gradient of h_1 goes through the first M * 256 bytes of the
- * workspace (rounded up to 256) to layers 1..0.  Numerically the same as one
+ * Networks of 4 and 5 layers run as two launches: layers L-1..2 (for the
+ * 5-layer 128-wide network their dgrad weights and exchange tiles fill one
+ * workgroup's 160 KiB of LDS), whose fp16 gradient of h_1 goes through the
+ * first M * 256 bytes of the workspace (rounded up to 256) to layers 1..0.  Numerically the same as one
  * launch: the in-register chain also hands dz on as fp16.
  *   workspace        device memory, 16-byte aligned, at least the size that
  *                    mlpmk_bwd_workspace_size reports for the same

@@ -151,6 +151,7 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
   p.x = static_cast<const _Float16*>(x);
   p.out = static_cast<_Float16*>(out);
   p.M = M;
+  for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
   return fwd_dispatch(num_layers, dims, p, stash != nullptr, static_cast<hipStream_t>(stream));
 }
 
@@ -198,6 +199,7 @@ static int bwd_common(int num_layers, const int* dims, const void* x, const void
   p.dout_stride = dout_row_stride;
   p.dx = static_cast<_Float16*>(dx);
   p.M = M;
+  for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
   if (workspace) {
     if ((rc = check_ptr(workspace, "workspace"))) return rc;
     int64_t need = 0;
@@ -244,10 +246,7 @@ static int check_wn(int num_layers, const int* dims, int dtype) {
   if (rc) return rc;
   if (dtype != MLPMK_DTYPE_F32 && dtype != MLPMK_DTYPE_F16)
     return fail(MLPMK_ERR_INVALID_ARG, "param_dtype=%d (0 = fp32, 1 = fp16)", dtype);
-  for (int i = 0; i <= num_layers; ++i)
-    if (dims[i] % 16 != 0)
-      return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "dims[%d]=%d is not a multiple of 16", i, dims[i]);
-  return MLPMK_OK;
+  return MLPMK_OK;  // element-wise kernels: any positive widths
 }
 
 int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, const void* v, const void* g,

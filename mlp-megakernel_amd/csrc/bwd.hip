@@ -113,7 +113,7 @@ struct BwdGeom {
   // 37.5 -> 34.4 us; the 3-layer 128-wide kernel spills with it, and the
   // narrow one gains nothing (20.6 vs 21.2 us), so they share one buffer
   // loaded one phase ahead.
-  static constexpr bool pf() { return !SEG && L <= 2; }
+  static constexpr bool pf() { return !N::gen && !SEG && L <= 2; }
   // Element offset of dW_l in the dW blocks laid out back to back.
   static constexpr int woff(int l) {
     int o = 0;
@@ -130,12 +130,15 @@ struct BwdGeom {
 
 // Stages the dgrad A fragments: fragment (mb, s) of layer l, lane (i, g) holds
 // W_l[outfeat(mb, i)][16s + 8g + j], j = 0..7 -- one 16-byte load per lane.
+// For a runtime-width (Gen) network the true widths come from p.dims: W_l
+// rows are p.dims[l + 1] wide (any width for the last layer), read element by
+// element, and entries past the true widths stage as zeros.
 template <class N, class Gm, int NT>
 __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* lds) {
 #pragma unroll
   for (int l = 0; l < N::L; ++l) {
     if (!Gm::has_dgrad(l)) continue;
-    const int Nout = N::d[l + 1];
+    const int Nout = N::gen ? p.dims[l + 1] : N::d[l + 1];
     const int KS = Gm::dks(l);
     const int items = Gm::dmb(l) * KS * 64;
     const f16* __restrict__ w = p.w[l];
@@ -144,8 +147,17 @@ __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* l
       const int mb = f / KS, s = f % KS;
       const int i = lane & 31, g = lane >> 5;
       const int row = outfeat(mb, i);
-      lds[(Gm::dfrag_off(l) + f) * 64 + lane] =
-          *reinterpret_cast<const f16x8*>(w + (int64_t)row * Nout + 16 * s + 8 * g);
+      if constexpr (N::gen) {
+        f16x8 v;
+        const int k0 = 16 * s + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[j] = (row < p.dims[l] && k0 + j < Nout) ? w[(int64_t)row * Nout + k0 + j] : (f16)0.0f;
+        lds[(Gm::dfrag_off(l) + f) * 64 + lane] = v;
+      } else {
+        lds[(Gm::dfrag_off(l) + f) * 64 + lane] =
+            *reinterpret_cast<const f16x8*>(w + (int64_t)row * Nout + 16 * s + 8 * g);
+      }
     }
   }
 }
@@ -201,7 +213,9 @@ struct BwdWave {
     rrow[0] = 8 * (q >> 1) + (i >> 2);
     rrow[1] = rrow[0] + 4;
     rcol = 16 * (q & 1) + 4 * (i & 3);
-  }  __device__ __forceinline__ uint32_t nrows_at(int64_t r0) const {
+  }  // True width of activation / gradient level l (p.dims for Gen networks).
+  __device__ __forceinline__ int dw_(int l) const { return N::gen ? p.dims[l] : N::d[l]; }
+  __device__ __forceinline__ uint32_t nrows_at(int64_t r0) const {
     const int64_t left = p.M - r0;
     return (uint32_t)(left < 32 ? (left > 0 ? left : 0) : 32);
   }
@@ -214,9 +228,32 @@ struct BwdWave {
   // dL/dout rows from r0 as B operands.  Row stride 0 broadcasts row 0.
   __device__ __forceinline__ void load_dout(int64_t r0) {
     const int64_t st = p.dout_stride;
+    const int OW = dw_(L);
     const uint32_t nr = nrows_at(r0);
-    const uint32_t bytes = nr ? (uint32_t)(((int64_t)(nr - 1) * st + N::d[L]) * 2) : 0u;
+    const uint32_t bytes = nr ? (uint32_t)(((int64_t)(nr - 1) * st + OW) * 2) : 0u;
     const rsrc_t r = make_rsrc(p.dout + r0 * st, bytes);
+    if constexpr (N::gen) {
+      // Runtime output width OW: whole 8-feature pieces below OW in one
+      // 16-byte load, the piece that straddles OW element by element (the
+      // resource ends at the row's OW-th element, and a broadcast row may be
+      // exactly OW long), pieces past OW zero.
+#pragma unroll
+      for (int s = 0; s < KSL; ++s) {
+        const int c = 16 * s + 8 * g;
+        if (c + 8 <= OW) {
+          gbuf[s] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + c) * 2), 0, 0));
+        } else {
+          gbuf[s] = f16x8{};
+          if (c < OW) {
+#pragma unroll
+            for (int j = 0; j < 7; ++j)
+              if (c + j < OW)
+                gbuf[s][j] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(r, (int)((n * st + c + j) * 2), 0, 0));
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < KSL; ++s)
       gbuf[s] = __builtin_bit_cast(
@@ -227,10 +264,16 @@ struct BwdWave {
   template <int l>
   __device__ __forceinline__ void load_h(int64_t r0) {
     constexpr int B = PF ? l : 0;
-    const rsrc_t hr = rows_rsrc(l == 0 ? p.h0 : p.stash[l > 0 ? l - 1 : 0], N::d[l], 4, r0);
+    const int HW = dw_(l);  // a multiple of 16 for Gen networks: K-steps past it are zero
+    const rsrc_t hr = rows_rsrc(l == 0 ? p.h0 : p.stash[l > 0 ? l - 1 : 0], HW, 4, r0);
 #pragma unroll
     for (int s = 0; s < N::d[l] / 16; ++s) {
-      const int off = (n * N::d[l] + 16 * s + 8 * g) * 4;
+      if (N::gen && 16 * s >= HW) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hbuf[B][s][j] = 0.0f;
+        continue;
+      }
+      const int off = (n * HW + 16 * s + 8 * g) * 4;
       const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0));
       const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, 0));
 #pragma unroll
@@ -241,11 +284,14 @@ struct BwdWave {
     }
   }
   __device__ __forceinline__ void load_x(int64_t r0) {
-    const rsrc_t xr = rows_rsrc(p.x, N::d[0], 2, r0);
+    const int D = dw_(0);
+    const rsrc_t xr = rows_rsrc(p.x, D, 2, r0);
 #pragma unroll
     for (int s = 0; s < KS0; ++s)
-      xbuf[s] = __builtin_bit_cast(
-          f16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)((n * N::d[0] + 16 * s + 8 * g) * 2), 0, 0));
+      xbuf[s] = (N::gen && 16 * s >= D)
+                    ? f16x8{}
+                    : __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    xr, (int)((n * D + 16 * s + 8 * g) * 2), 0, 0));
   }
 
   // Writes the wave's 32 rows of KS K-steps of features (row-per-lane B
@@ -359,17 +405,21 @@ struct BwdWave {
             dzn[2 * mb] = lo;
             dzn[2 * mb + 1] = hi;
           } else {  // segment: dz of the layer below leaves through p.dx
-            const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2, row0);
-            const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
-            buf_store16(lo, dr, e * 2);
-            buf_store16(hi, dr, e * 2 + 32);
+            const int D = dw_(0);
+            const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
+            const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
+            if (!N::gen || 32 * mb < D) buf_store16(lo, dr, e * 2);
+            if (!N::gen || 32 * mb + 16 < D) buf_store16(hi, dr, e * 2 + 32);
           }
         } else {
-          const rsrc_t dr = rows_rsrc(p.dx, N::d[0], 2, row0);
-          const uint32_t e = (uint32_t)(n * N::d[0] + 32 * mb + 8 * g);
-          buf_store16(pack8(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
-          buf_store16(pack8(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
-                      e * 2 + 32);
+          const int D = dw_(0);  // a multiple of 16 for Gen networks
+          const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
+          const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
+          if (!N::gen || 32 * mb < D)
+            buf_store16(pack8(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
+          if (!N::gen || 32 * mb + 16 < D)
+            buf_store16(pack8(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
+                        e * 2 + 32);
         }
       }
     }
@@ -419,9 +469,19 @@ struct BwdWave {
   // stores it into this workgroup's partial-sum block (p.part non-null).
   template <int l>
   __device__ __forceinline__ void flush_tile(const f32x16& acc, int ti, int to) const {
-    constexpr int K = N::d[l], NO = N::d[l + 1];
+    const int K = dw_(l), NO = dw_(l + 1);
+    int64_t welems = N::weight_elems(), woff = Gm::woff(l);
+    if constexpr (N::gen) {  // partial-sum blocks laid out with the true widths
+      welems = 0;
+      woff = 0;
+#pragma unroll
+      for (int i = 0; i < N::L; ++i) {
+        if (i < l) woff += (int64_t)p.dims[i] * p.dims[i + 1];
+        welems += (int64_t)p.dims[i] * p.dims[i + 1];
+      }
+    }
     const int fo = 32 * to + (lane & 31);
-    float* const part = p.part ? p.part + (int64_t)blockIdx.x * N::weight_elems() + Gm::woff(l) : nullptr;
+    float* const part = p.part ? p.part + (int64_t)blockIdx.x * welems + woff : nullptr;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       // C layout: lane (o, g) holds rows 8a + 4g + b of its column, register 4a + b.
@@ -599,14 +659,17 @@ static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bwd kernel launch");
   if (p.part) {
+    // The dW blocks back to back with the layers' true widths (the same
+    // offsets flush_tile writes the partials at).
     CombineLayout lay = {};
     lay.L = N::L;
-    lay.nelem = N::weight_elems();
+    int64_t o = 0;
     for (int l = 0; l < N::L; ++l) {
-      lay.off[l] = BwdGeom<N, NW, DX, SEG>::woff(l);
+      lay.off[l] = o;
+      o += N::gen ? (int64_t)p.dims[l] * p.dims[l + 1] : (int64_t)N::d[l] * N::d[l + 1];
       lay.dw[l] = p.dw[l];
     }
-    lay.off[N::L] = lay.nelem;
+    lay.off[N::L] = lay.nelem = o;
     hipLaunchKernelGGL(bwd_combine_kernel, dim3((unsigned)((lay.nelem + kCombineCols - 1) / kCombineCols)),
                        dim3(kCombineCols * kCombineGroups), 0, st, p.part, grid, lay);
     e = hipGetLastError();
@@ -620,58 +683,73 @@ static int launch_bwd_any(const BwdParams& p, hipStream_t st) {
   return p.dx ? launch_bwd<N, NW, true>(p, st) : launch_bwd<N, NW, false>(p, st);
 }
 
+static int64_t weight_elems_of(int L, const int* dims) {
+  int64_t e = 0;
+  for (int l = 0; l < L; ++l) e += (int64_t)dims[l] * dims[l + 1];
+  return e;
+}
+
+// Partial-sum bytes: one block of `welems` floats (the dW blocks at their
+// true widths) per workgroup of the grid.
 template <class N, int NW, bool DX, bool SEG = false>
-static int partial_bytes(int64_t M, int64_t* bytes) {
+static int partial_bytes(int64_t M, int64_t welems, int64_t* bytes) {
   int grid = 0;
   const int rc = bwd_grid<N, NW, DX, SEG>(M, &grid);
-  if (rc == MLPMK_OK) *bytes = (int64_t)grid * N::weight_elems() * (int64_t)sizeof(float);
+  if (rc == MLPMK_OK) *bytes = (int64_t)grid * welems * (int64_t)sizeof(float);
   return rc;
 }
 
 template <class N, int NW>
-static int bwd_workspace_any(int64_t M, bool dx, int64_t* bytes) {
-  return dx ? partial_bytes<N, NW, true>(M, bytes) : partial_bytes<N, NW, false>(M, bytes);
+static int bwd_workspace_any(int64_t M, bool dx, int64_t welems, int64_t* bytes) {
+  return dx ? partial_bytes<N, NW, true>(M, welems, bytes) : partial_bytes<N, NW, false>(M, welems, bytes);
 }
 
-// The 5-layer backward: layers 4..2 as a segment (kernel A, 96 KiB of dgrad
-// fragments + 64 KiB of exchange tiles), whose fp16 dz_1 goes through the
-// workspace to layers 1..0 (kernel B, the 2-layer network with dz_1 as its
-// output gradient).  Workspace: dz_1 [M, 128] fp16, then the weight-gradient
-// partials of whichever launch needs more (the launches run in stream order,
-// so they share the block).
+// Deeper networks in two launches: layers L-1..2 as a segment (kernel A, the
+// dgrad fragments of those layers + 64 KiB of exchange tiles), whose fp16 dz_1
+// goes through the workspace to layers 1..0 (kernel B, the 2-layer network
+// with dz_1 as its output gradient).  For the 5-layer 128-wide network the
+// four dgrad weight blocks and the exchange tiles would not fit the 160 KiB of
+// one workgroup together.  Workspace: dz_1 [M, d[2]] fp16, then the
+// weight-gradient partials of whichever launch needs more (the launches run in
+// stream order, so they share the block).
 static int64_t dz_bytes(int64_t M) { return (M * 128 * 2 + 255) / 256 * 256; }
 
-static int bwd5_workspace(int64_t M, bool dx, int64_t* bytes) {
+template <class TOP, class BOT>
+static int bwd_split_workspace(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
   int64_t a = 0, b = 0;
-  int rc = partial_bytes<BNet3L128, 4, true, true>(M, &a);
+  int rc = partial_bytes<TOP, 4, true, true>(M, weight_elems_of(L - 2, dims + 2), &a);
   if (rc != MLPMK_OK) return rc;
-  rc = dx ? partial_bytes<BNet2L128, 4, true>(M, &b) : partial_bytes<BNet2L128, 4, false>(M, &b);
+  const int64_t wb = weight_elems_of(2, dims);
+  rc = dx ? partial_bytes<BOT, 4, true>(M, wb, &b) : partial_bytes<BOT, 4, false>(M, wb, &b);
   if (rc != MLPMK_OK) return rc;
   *bytes = dz_bytes(M) + (a > b ? a : b);
   return MLPMK_OK;
 }
 
-static int launch_bwd5(const BwdParams& p, hipStream_t st) {
+template <class TOP, class BOT>
+static int launch_bwd_split(const BwdParams& p, int L, hipStream_t st) {
+  static_assert(TOP::L >= 2 && BOT::L == 2, "segment shapes");
   if (!p.part)
     return fail(MLPMK_ERR_INVALID_ARG,
-                "the 5-layer backward passes dz between two launches through the workspace: use mlpmk_bwd_ws");
+                "a backward of more than 3 layers passes dz between two launches through the workspace: "
+                "use mlpmk_bwd_ws");
   char* const ws = reinterpret_cast<char*>(p.part);
   _Float16* const dz1 = reinterpret_cast<_Float16*>(ws);
   float* const part = reinterpret_cast<float*>(ws + dz_bytes(p.M));
   BwdParams a = {};
-  for (int l = 0; l < 3; ++l) {
+  for (int l = 0; l < L - 2; ++l) {
     a.w[l] = p.w[2 + l];
     a.dw[l] = p.dw[2 + l];
   }
-  a.stash[0] = p.stash[2];  // h_3
-  a.stash[1] = p.stash[3];  // h_4
-  a.h0 = p.stash[1];        // h_2
+  for (int l = 0; l + 1 < L - 2; ++l) a.stash[l] = p.stash[2 + l];  // h_3 .. h_{L-1}
+  for (int l = 0; l <= L - 2; ++l) a.dims[l] = p.dims[2 + l];
+  a.h0 = p.stash[1];  // h_2
   a.dout = p.dout;
   a.dout_stride = p.dout_stride;
   a.dx = dz1;
   a.M = p.M;
   a.part = part;
-  int rc = launch_bwd<BNet3L128, 4, true, true>(a, st);
+  int rc = launch_bwd<TOP, 4, true, true>(a, st);
   if (rc != MLPMK_OK) return rc;
   BwdParams b = {};
   b.x = p.x;
@@ -679,30 +757,64 @@ static int launch_bwd5(const BwdParams& p, hipStream_t st) {
     b.w[l] = p.w[l];
     b.dw[l] = p.dw[l];
   }
+  for (int l = 0; l <= 2; ++l) b.dims[l] = p.dims[l];
   b.stash[0] = p.stash[0];  // h_1
   b.dout = dz1;
-  b.dout_stride = 128;
+  b.dout_stride = p.dims[2];
   b.dx = p.dx;
   b.M = p.M;
   b.part = part;
-  return launch_bwd_any<BNet2L128, 4>(b, st);
+  return launch_bwd_any<BOT, 4>(b, st);
 }
 
-int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
-  if (bdims_match<BNet3L128>(L, dims)) return bwd_workspace_any<BNet3L128, 4>(M, dx, bytes);
-  if (bdims_match<BNet5L128>(L, dims)) return bwd5_workspace(M, dx, bytes);
-  if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<BNetNarrow, 4>(M, dx, bytes);
-  return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+// Runtime-width networks (compiled at width 128, true widths in BwdParams::dims):
+// 2..5 layers, input and hidden widths multiples of 16 in [16, 128], any
+// output width in [1, 128] -- the forward's generic shapes.  2 and 3 layers run
+// in one launch, 4 and 5 in two (layers L-1..2, then 1..0).
+typedef Gen<BNet2L128> GBNet2;
+typedef Gen<BNet3L128> GBNet3;
+
+bool bwd_generic_dims(int L, const int* dims) {
+  if (L < 2 || L > 5) return false;
+  for (int i = 0; i < L; ++i)
+    if (dims[i] < 16 || dims[i] > 128 || dims[i] % 16 != 0) return false;
+  return dims[L] >= 1 && dims[L] <= 128;
 }
 
-bool bwd_supported_dims(int L, const int* dims) {
+static bool bwd_exact_shape(int L, const int* dims) {
   return bdims_match<BNet3L128>(L, dims) || bdims_match<BNet5L128>(L, dims) || bdims_match<BNetNarrow>(L, dims);
 }
 
+int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
+  const int64_t we = weight_elems_of(L, dims);
+  if (bdims_match<BNet3L128>(L, dims)) return bwd_workspace_any<BNet3L128, 4>(M, dx, we, bytes);
+  if (bdims_match<BNet5L128>(L, dims)) return bwd_split_workspace<BNet3L128, BNet2L128>(L, dims, M, dx, bytes);
+  if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<BNetNarrow, 4>(M, dx, we, bytes);
+  if (bwd_generic_dims(L, dims)) {
+    switch (L) {
+      case 2: return bwd_workspace_any<GBNet2, 4>(M, dx, we, bytes);
+      case 3: return bwd_workspace_any<GBNet3, 4>(M, dx, we, bytes);
+      case 4: return bwd_split_workspace<GBNet2, GBNet2>(L, dims, M, dx, bytes);
+      default: return bwd_split_workspace<GBNet3, GBNet2>(L, dims, M, dx, bytes);
+    }
+  }
+  return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+}
+
+bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims); }
+
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st) {
   if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<BNet3L128, 4>(p, st);
-  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd5(p, st);
+  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<BNet3L128, BNet2L128>(p, L, st);
   if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<BNetNarrow, 4>(p, st);
+  if (bwd_generic_dims(L, dims)) {
+    switch (L) {
+      case 2: return launch_bwd_any<GBNet2, 4>(p, st);
+      case 3: return launch_bwd_any<GBNet3, 4>(p, st);
+      case 4: return launch_bwd_split<GBNet2, GBNet2>(p, L, st);
+      default: return launch_bwd_split<GBNet3, GBNet2>(p, L, st);
+    }
+  }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
 }
 

@@ -162,6 +162,7 @@ __device__ __forceinline__ int opaque(int v) {
 // Compile-time description of a network: widths d[0] (input) .. d[L] (output).
 template <int... Ds>
 struct Net {
+  static constexpr bool gen = false;  // widths fixed at compile time
   static constexpr int L = sizeof...(Ds) - 1;
   static constexpr int d[sizeof...(Ds)] = {Ds...};
   // K-steps (16 input features each) and 32-row output blocks of layer l.
@@ -190,6 +191,16 @@ struct Net {
     for (int i = 0; i < L; ++i) s += (int64_t)d[i] * d[i + 1];
     return s;
   }
+};
+
+// A runtime-width network: the kernel is compiled for Base's widths (all 128)
+// and reads the true widths, each at most Base's, from the launch parameters.
+// Weights past the true widths stage as zeros, so a padded input feature
+// never contributes; a padded hidden feature computes softplus(0) but meets
+// zero weights in the next layer; padded output features are not stored.
+template <class Base>
+struct Gen : Base {
+  static constexpr bool gen = true;
 };
 
 }  // namespace mlpmk

@@ -49,18 +49,26 @@ __device__ __forceinline__ float wscale(int l) {
   return (l == 0 ? kLog2e : 1.0f) * (l == N::L - 1 ? kLn2 : 1.0f);
 }
 
-// Lane `lane` of fragment (mb, s) of layer l.
+// Lane `lane` of fragment (mb, s) of layer l.  For a runtime-width (Gen)
+// network, rows and columns past the true widths (p.dims) stage as zeros.
 template <class N>
 __device__ __forceinline__ f16x8 weight_fragment(const FwdParams& p, int l, int f, int lane) {
-  const int Nout = N::d[l + 1], KS = N::ks(l);
+  const int KS = N::ks(l);
+  const int Nout = N::gen ? p.dims[l + 1] : N::d[l + 1];
   const int mb = f / KS, s = f % KS;
   const int i = lane & 31, g = lane >> 5;
   const int of = outfeat(mb, i);
   f16x8 v;
   if (of < Nout) {
-    const f16* src = p.w[l] + (int64_t)(16 * s + 8 * g) * Nout + of;
+    const int k0 = 16 * s + 8 * g;
+    const f16* src = p.w[l] + (int64_t)k0 * Nout + of;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = scaled_weight(src[(int64_t)j * Nout], wscale<N>(l));
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (N::gen)
+        v[j] = k0 + j < p.dims[l] ? scaled_weight(src[(int64_t)j * Nout], wscale<N>(l)) : (f16)0.0f;
+      else
+        v[j] = scaled_weight(src[(int64_t)j * Nout], wscale<N>(l));
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = (f16)0.0f;
@@ -150,7 +158,7 @@ __device__ __forceinline__ void stage_store_any(f16x8* lds, const f16x8 (&r)[8],
 template <class N, int NT, int RF>
 __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
   constexpr int TOTAL = StageTasks<N>::total();
-  if constexpr (TOTAL >= NT) {
+  if constexpr (TOTAL >= NT && !N::gen) {
     constexpr int TPT = (TOTAL + NT - 1) / NT;
     f16x8 r[TPT][8];
 #pragma unroll
@@ -182,6 +190,7 @@ struct BlockIO {
   rsrc_t x, out;
   rsrc_t stash[kMaxLayers];
   i32x4* stage;  // this wave's LDS staging tile for the output rows (STAGE only)
+  int dl[kMaxLayers + 1];  // true widths (Gen networks only)
 };
 
 // LDS plan of a workgroup (160 KiB on gfx950), in priority order:
@@ -206,7 +215,7 @@ struct LdsPlan {
   static constexpr int kRowChunks = 8;  // 16-byte chunks per staged row segment
   static constexpr int kTileChunks = 32 * NB * kRowChunks;
   static constexpr int wbytes = N::nfrag() * 1024;
-  static constexpr bool stage = N::d[N::L] % 64 == 0 && wbytes + NW * kTileChunks * 16 + 16 <= kLds;
+  static constexpr bool stage = !N::gen && N::d[N::L] % 64 == 0 && wbytes + NW * kTileChunks * 16 + 16 <= kLds;
   static constexpr int stage_bytes = stage ? NW * kTileChunks * 16 : 0;
   static constexpr int reg_frags = wbytes + stage_bytes + 16 <= kLds ? 0 : 1;
   static constexpr bool claim = wbytes - reg_frags * 1024 + stage_bytes + 16 <= kLds;
@@ -236,12 +245,14 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
   const int64_t left = p.M - row0;
   const uint32_t rows = (uint32_t)(left < ROWS ? (left > 0 ? left : 0) : ROWS);
   BlockIO io;
-  io.x = make_rsrc(p.x + row0 * N::d[0], rows * N::d[0] * 2u);
-  io.out = make_rsrc(p.out + row0 * N::d[N::L], rows * N::d[N::L] * 2u);
+#pragma unroll
+  for (int l = 0; l <= N::L; ++l) io.dl[l] = N::gen ? p.dims[l] : N::d[l];
+  io.x = make_rsrc(p.x + row0 * io.dl[0], rows * io.dl[0] * 2u);
+  io.out = make_rsrc(p.out + row0 * io.dl[N::L], rows * io.dl[N::L] * 2u);
   if constexpr (STASH) {
 #pragma unroll
     for (int l = 0; l < N::L - 1; ++l)
-      io.stash[l] = make_rsrc(p.stash[l] + row0 * N::d[l + 1], rows * N::d[l + 1] * 4u);
+      io.stash[l] = make_rsrc(p.stash[l] + row0 * io.dl[l + 1], rows * io.dl[l + 1] * 4u);
   }
   return io;
 }
@@ -249,14 +260,27 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
 // Rows of x as raw dwords: kept as i32x4 until the MFMA reads them, because an
 // f16x8 destination makes the compiler re-pack the halves right after the load
 // (v_bfi copies), which waits for the load at the point of issue.
-template <int KS, int NB>
-__device__ __forceinline__ void load_rows(i32x4 (&xa)[KS][NB], rsrc_t xr, int n, int g) {
+// For a runtime-width network rows are D wide (a multiple of 16): K-steps
+// past D (a wave-uniform test) are zero without a load.
+template <int KS, int NB, bool GEN = false>
+__device__ __forceinline__ void load_rows(i32x4 (&xa)[KS][NB], rsrc_t xr, int n, int g, int D = KS * 16) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      xa[s][nb] = __builtin_amdgcn_raw_buffer_load_b128(
-          xr, (int)(((nb * 32 + n) * (KS * 16) + 16 * s + 8 * g) * 2), 0, 0);
+    for (int s = 0; s < KS; ++s) {
+      if (GEN && 16 * s >= D)
+        xa[s][nb] = i32x4{};
+      else
+        xa[s][nb] = __builtin_amdgcn_raw_buffer_load_b128(xr, ((nb * 32 + n) * D + 16 * s + 8 * g) * 2, 0, 0);
+    }
+}
+
+// x rows of the 32*NB-row block starting at row0 (Gen networks: true width).
+template <class N, int NB>
+__device__ __forceinline__ void load_block_x(i32x4 (&xa)[N::ks(0)][NB], const FwdParams& p, int64_t row0,
+                                             int lane) {
+  load_rows<N::ks(0), NB, N::gen>(xa, block_io<N, false, 32 * NB>(p, row0).x, lane & 31, lane >> 5,
+                                  N::gen ? p.dims[0] : N::d[0]);
 }
 
 __device__ __forceinline__ f16x8 as_f16x8(f16x8 v) { return v; }
@@ -377,6 +401,30 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
           __builtin_bit_cast(i32x4, pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]));
       io.stage[stage_slot(row, c + 2)] =
           __builtin_bit_cast(i32x4, pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]));
+    } else if constexpr (LAST && N::gen) {
+      // Runtime output width OW: whole 8-feature pieces when OW is a multiple
+      // of 8, else one 2-byte store per feature; features past OW are dropped.
+      const f32x16 v = acc[nb] * kIn;
+      const int OW = io.dl[N::L], c = 32 * mb + 8 * g;
+      const uint32_t e = (uint32_t)((nb * 32 + n) * OW + c);
+      const f16x8 lo = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+      const f16x8 hi = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+      if (OW % 8 == 0) {
+        if (c < OW) buf_store16<kStreamStore>(lo, io.out, e * 2);
+        if (c + 16 < OW) buf_store16<kStreamStore>(hi, io.out, e * 2 + 32);
+      } else {
+        // Each element converted on its own: taken out of the packed lo / hi
+        // vectors, the 2-byte store builtin was given element 0 every time.
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (c + j < OW)
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)v[j]), io.out,
+                                                  (int)((e + j) * 2), 0, kStreamStore);
+          if (c + 16 + j < OW)
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)v[8 + j]), io.out,
+                                                  (int)((e + 16 + j) * 2), 0, kStreamStore);
+        }
+      }
     } else if constexpr (LAST) {
       const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
       if (lo_ok) buf_store16<kStreamStore>(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
@@ -394,7 +442,23 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       const f16x8 lo = pack8(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
       const f16x8 hi = pack8(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
       if constexpr (!EXACT) m = sp2_track<!STASH>(m, lo, hi);
-      if constexpr (STASH) {
+      if constexpr (STASH && N::gen) {
+        // Runtime hidden width HW (a multiple of 16): feature groups past it are dropped.
+        const rsrc_t sr = io.stash[l];
+        const int HW = io.dl[l + 1], c = 32 * mb + 8 * g;
+        const uint32_t e4 = (uint32_t)((nb * 32 + n) * HW + c) * 4;
+        float h[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) h[e] = s[e] * kLn2;
+        if (c < HW) {
+          buf_store16<kStashStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, e4);
+          buf_store16<kStashStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, e4 + 16);
+        }
+        if (c + 16 < HW) {
+          buf_store16<kStashStore>((f32x4){h[8], h[9], h[10], h[11]}, sr, e4 + 64);
+          buf_store16<kStashStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, e4 + 80);
+        }
+      } else if constexpr (STASH) {
         const rsrc_t sr = io.stash[l];
         float h[16];
 #pragma unroll
@@ -495,7 +559,7 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
     // Every MFMA that reads x has been issued: refill xa with the next block's
     // rows (past the end the resource is empty and the refill reads zeros).
     MLPMK_SCHED_FENCE();
-    load_rows<N::ks(0), NB>(c.xa, block_io<N, false, ROWS>(p, next * ROWS).x, lane & 31, lane >> 5);
+    load_block_x<N, NB>(c.xa, p, next * ROWS, lane);
   }
   epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.ovf, lane);
   if constexpr (l == N::L - 1 && STAGE) {
@@ -538,7 +602,7 @@ __device__ __forceinline__ void fwd_block_checked(const FwdParams& p, Chain<N, N
   constexpr int ROWS = 32 * NB;
   if (__builtin_expect(fwd_block<N, NB, STASH, STAGE, false, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane),
                        0)) {
-    load_rows<N::ks(0), NB>(c.xa, block_io<N, false, ROWS>(p, b * ROWS).x, lane & 31, lane >> 5);
+    load_block_x<N, NB>(c.xa, p, b * ROWS, lane);
     load_frags<N, 0, KSM, RF>(c.fr, FragBase<N, RF>(lds_b, lane_off), c.rf);
     fwd_block<N, NB, STASH, STAGE, true, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
   }
@@ -558,7 +622,6 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   static_assert(D >= 1 && D <= 4, "prefetch depth");
   using Plan = LdsPlan<N, NB, NW>;
   constexpr int KSM = N::ksmax();
-  constexpr int KS0 = N::ks(0);
   constexpr int ROWS = 32 * NB;
   constexpr bool STAGE = Plan::stage;
   constexpr int TC = Plan::kTileChunks;
@@ -606,7 +669,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   const int lane_off = lane * 16;  // this lane's 16 bytes within a 1 KiB fragment
   int64_t b = claim();
   if (b >= nblk) return;  // no barrier follows
-  load_rows<KS0, NB>(c.xa, block_io<N, false, ROWS>(p, b * ROWS).x, lane & 31, lane >> 5);
+  load_block_x<N, NB>(c.xa, p, b * ROWS, lane);
   load_frags<N, 0, KSM, RF>(c.fr, FragBase<N, RF>(lds_b, lane_off), c.rf);
   // The first block is peeled so that the loop header is entered from two
   // paths with the same outstanding memory operations (the x refill, then
@@ -696,9 +759,26 @@ static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
   return launch_fwd<N, NB, false, NW, D>(p, st);
 }
 
+// Runtime-width networks of 2..5 layers, compiled at width 128: any input
+// and hidden widths that are multiples of 16 in [16, 128] (whole MFMA
+// K-steps, so every width test is wave-uniform) and any output width in
+// [1, 128] (the reference masks its output columns, kernel.py:86-87,121-123;
+// its input and hidden widths are whole tiles, AGENTS.md:84-85).
+typedef Gen<Net<128, 128, 128>> GNet2;
+typedef Gen<Net<128, 128, 128, 128>> GNet3;
+typedef Gen<Net<128, 128, 128, 128, 128>> GNet4;
+typedef Gen<Net<128, 128, 128, 128, 128, 128>> GNet5;
+
+bool fwd_generic_dims(int L, const int* dims) {
+  if (L < 2 || L > 5) return false;
+  for (int i = 0; i < L; ++i)
+    if (dims[i] < 16 || dims[i] > 128 || dims[i] % 16 != 0) return false;
+  return dims[L] >= 1 && dims[L] <= 128;
+}
+
 bool fwd_supported_dims(int L, const int* dims) {
   return dims_match<Net3L128>(L, dims) || dims_match<Net5L128>(L, dims) ||
-         dims_match<NetNarrow>(L, dims);
+         dims_match<NetNarrow>(L, dims) || fwd_generic_dims(L, dims);
 }
 
 int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus);
@@ -714,6 +794,17 @@ int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStre
   if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 1, 8, 1>(p, stash, st);
   if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 1, 8, 1>(p, stash, st);
   if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 16, 1, 16, 1>(p, stash, st);
+  if (fwd_generic_dims(L, dims)) {
+    switch (L) {
+      // At most 8 waves (4 for the 5-layer stash kernel): the runtime
+      // strides cannot fold into immediate offsets, and the 12-wave kernels
+      // (168 VGPRs) spill.
+      case 2: return launch_fwd_any<GNet2, 1, 8, 1, 8, 1>(p, stash, st);
+      case 3: return launch_fwd_any<GNet3, 1, 8, 1, 8, 1>(p, stash, st);
+      case 4: return launch_fwd_any<GNet4, 1, 8, 1, 8, 1>(p, stash, st);
+      default: return launch_fwd_any<GNet5, 1, 8, 1, 4, 1>(p, stash, st);
+    }
+  }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
 }
 

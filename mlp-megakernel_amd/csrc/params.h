@@ -12,6 +12,9 @@ struct FwdParams {
   const _Float16* w[kMaxLayersHost];
   float* stash[kMaxLayersHost];  // stash[l] = h_{l+1}, fp32 [M, d[l+1]]; unused if no stash
   int64_t M;
+  // The network's widths d[0] .. d[L].  Read only by the runtime-width
+  // kernels (Gen networks), whose compile-time widths are padded to 128.
+  int dims[kMaxLayersHost + 1];
 };
 
 }  // namespace mlpmk
@@ -35,6 +38,9 @@ struct BwdParams {
   // Segment mode only (the upper layers of a deeper network): the fp32
   // activation feeding layer 0, h_{l0} of the full network, in place of x.
   const float* h0;
+  // The widths d[0] .. d[L] of the layers this launch runs (as for FwdParams,
+  // read only by the runtime-width kernels).
+  int dims[kMaxLayersHost + 1];
 };
 
 }  // namespace mlpmk

@@ -192,7 +192,13 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
         raise TypeError("dout must be fp16 on the same device as x")
     if tuple(dout.shape) != (M, dims[-1]) or dout.stride(1) != 1:
         raise ValueError(f"dout must be [M, OUT]={M, dims[-1]} with unit column stride")
-    row_stride = int(dout.stride(0)) if M > 1 else dims[-1]
+    row_stride = int(dout.stride(0)) if M > 1 else -(-dims[-1] // 8) * 8
+    if row_stride % 8 != 0:
+        # The library reads dout rows from 16-byte boundaries: an output width
+        # that is not a multiple of 8 gets rows padded to the next multiple.
+        padded = torch.zeros((M, -(-dims[-1] // 8) * 8), dtype=torch.float16, device=dev)
+        padded[:, : dims[-1]] = dout
+        dout, row_stride = padded, padded.shape[1]
     if dx is not None:
         _require(dx, "dx", torch.float16, dev)
         if tuple(dx.shape) != (M, dims[0]):

@@ -45,10 +45,17 @@ def test_version_and_status_strings():
 @pytest.mark.parametrize(
     "dims,ok",
     [((128, 128, 128, 128), True), ((128,) * 6, True), ((32, 64, 64, 16), True),
-     ((128, 64, 128, 128), False), ((128, 128), False), ((100, 128, 128, 128), False)],
+     # runtime-width kernels: 2..5 layers, input/hidden multiples of 16 up to
+     # 128, any output width up to 128
+     ((128, 64, 128, 128), True), ((32, 128, 3), True), ((16, 48, 80, 112, 7), True), ((128,) * 5, True),
+     ((64, 128, 128, 1), True),
+     ((128, 128), False), ((100, 128, 128, 128), False), ((128, 136, 128, 128), False),
+     ((128, 256, 128), False), ((128, 128, 129), False), ((128,) * 7, False)],
 )
 def test_forward_support_table(dims, ok):
     assert ops.fwd_supported(list(dims)) is ok
+    # the backward covers the same shapes
+    assert ops.bwd_supported(list(dims)) is ok
 
 
 def _fwd(dims, x=A, w=(A, A, A), out=A, stash=None, m=256):
@@ -63,7 +70,7 @@ def test_fwd_validation_codes():
     lib = _lib.get()
     d = [128, 128, 128, 128]
     assert _fwd(d, m=-1) == INVALID
-    assert _fwd([128, 64, 128, 128]) == UNSUPPORTED
+    assert _fwd([128, 100, 128, 128]) == UNSUPPORTED
     assert _fwd([128, 128]) == UNSUPPORTED  # one layer
     assert _fwd(d, x=A + 2) == MISALIGNED
     assert _fwd(d, out=None) == INVALID
@@ -120,8 +127,8 @@ def test_wn_and_copy_validation_codes():
     assert lib.mlpmk_wn_fwd(3, pd, 7, A, A, A, A, None) == INVALID  # bad dtype
     assert lib.mlpmk_wn_fwd(3, pd, 0, A, None, A, A, None) == INVALID
     assert lib.mlpmk_wn_bwd(3, pd, 1, A, A, A, A, A + 2, A, None) == MISALIGNED
-    pbad, _k2 = _lib.int_array([128, 100, 128, 128])
-    assert lib.mlpmk_wn_fwd(3, pbad, 0, A, A, A, A, None) == UNSUPPORTED
+    pbad, _k2 = _lib.int_array([128, 0, 128, 128])
+    assert lib.mlpmk_wn_fwd(3, pbad, 0, A, A, A, A, None) == INVALID  # any positive widths
     assert lib.mlpmk_copy(A, A, 17, None) == INVALID
     assert lib.mlpmk_copy(A, A, 0, None) == OK
 
