@@ -259,6 +259,69 @@ def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3):
     }
 
 
+def backward_comparison(torch, ops, m, steps=50, warmup=10):
+    """The 3-layer backward at M rows, loss = out.sum(): the library's fused
+    backward (mlpmk_bwd_ws + combine, dW zero-filled first, as autograd does)
+    beside the reference's large-M fallback restated with PyTorch GPU ops
+    (/root/reference/mlp_fused.md:114-146: data-gradient GEMMs on
+    rocBLAS/hipBLASLt in fp16 with fp32 accumulation, weight-gradient GEMMs
+    in fp32, the sigmoid-times-gradient step as one elementwise expression,
+    weight gradients interleaved with the data gradients).  Both
+    read the same fp32 stash written by the library's training forward; HIP
+    events around `steps` back-to-back calls, eager and as a replayed graph."""
+    dims = (128, 128, 128, 128)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((m, 128), generator=g, device="cuda").half()
+    ws = [(torch.randn((128, 128), generator=g, device="cuda") / 128 ** 0.5).half() for _ in range(3)]
+    _, hs = ops.fwd(x, ws, stash=True)
+    dout = torch.ones((1, 128), dtype=torch.float16, device="cuda").expand(m, 128)
+    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+
+    def library(_):
+        for d in dws:
+            d.zero_()
+        ops.bwd(x, ws, hs, dout, dws)
+
+    h1, h2 = hs
+    wts = [w.t().contiguous() for w in ws]  # W^T, as the fallback keeps them for dgrad
+    out_t = {}
+
+    def fallback(_):
+        # data gradients as fp16 GEMMs; weight gradients in fp32 (sums over
+        # M rows overflow fp16 beyond ~1e4 rows), from the fp32 stash
+        grad = dout.contiguous()
+        dh2 = grad @ wts[2]
+        out_t["dw3"] = h2.t() @ grad.float()
+        dz2 = (1 - torch.exp(-h2)) * dh2
+        dh1 = dz2.half() @ wts[1]
+        out_t["dw2"] = h1.t() @ dz2
+        dz1 = (1 - torch.exp(-h1)) * dh1
+        out_t["dw1"] = x.float().t() @ dz1
+
+    res = {}
+    for name, fn in (("library", library), ("pytorch_fallback", fallback)):
+        with gc_paused():
+            ramp_clock(torch, fn, seconds=0.1)
+            eager = time_launches(torch, fn, steps, warmup)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(3):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn(0)
+        with gc_paused():
+            replay = time_launches(torch, lambda i: graph.replay(), steps, warmup)
+        res[name] = {"eager_ms": round(eager, 5), "graph_ms": round(replay, 5)}
+    torch.cuda.synchronize()
+    # the two compute the same gradients (fp16 GEMM outputs in the fallback)
+    rel = max(float((dws[i] - out_t[f"dw{i + 1}"]).norm() / dws[i].norm()) for i in range(3))
+    res["max_rel_frobenius_difference"] = round(rel, 5)
+    return res
+
+
 def load_traffic(workload):
     """HBM bytes per launch of the workload's kernel, from the calibrated
     rocprofv3 FETCH_SIZE + WRITE_SIZE runs recorded in profiles/traffic.json
@@ -401,6 +464,8 @@ def main():
     if args.train:
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
         result["training_5l"] = {str(mt): train_step_bench(torch, mt, n_layers=5) for mt in (65536, 131072)}
+        result["backward_vs_pytorch_fallback"] = {str(mt): backward_comparison(torch, ops, mt)
+                                                  for mt in (4096, 32768, 131072, 1048576)}
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(orc, dims, uniform, budget_s=args.cpu_budget)

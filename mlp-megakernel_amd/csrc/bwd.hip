@@ -121,6 +121,8 @@ struct BwdGeom {
     return o;
   }
   static constexpr bool valid() {
+    for (int i = 0; i <= L; ++i)
+      if (N::d[i] > 128) return false;  // dgrad staging holds at most 4 x 8 fragments per layer
     for (int i = 1; i < L; ++i)
       if (N::d[i] % 32 != 0) return false;  // hidden widths in whole 32-feature blocks
     if (DX && N::d[0] % 32 != 0) return false;
@@ -128,36 +130,71 @@ struct BwdGeom {
   }
 };
 
+// Fragment lane `item` (fragment-major, 64 lanes each) of layer l's dgrad A
+// operands: 16 contiguous bytes of one W_l row.  For a runtime-width (Gen)
+// network the true widths come from p.dims: W_l rows are p.dims[l + 1] wide
+// (any width for the last layer), read element by element, and entries past
+// the true widths stage as zeros.
+template <class N, class Gm>
+__device__ __forceinline__ f16x8 dgrad_fragment(const BwdParams& p, int l, int item) {
+  const int Nout = N::gen ? p.dims[l + 1] : N::d[l + 1];
+  const int KS = Gm::dks(l);
+  const int f = item >> 6, lane = item & 63;
+  const int mb = f / KS, s = f % KS;
+  const int i = lane & 31, g = lane >> 5;
+  const int row = outfeat(mb, i);
+  const f16* __restrict__ w = p.w[l];
+  if constexpr (N::gen) {
+    f16x8 v;
+    const int k0 = 16 * s + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[j] = (row < p.dims[l] && k0 + j < Nout) ? w[(int64_t)row * Nout + k0 + j] : (f16)0.0f;
+    return v;
+  } else {
+    return *reinterpret_cast<const f16x8*>(w + (int64_t)row * Nout + 16 * s + 8 * g);
+  }
+}
+
 // Stages the dgrad A fragments: fragment (mb, s) of layer l, lane (i, g) holds
-// W_l[outfeat(mb, i)][16s + 8g + j], j = 0..7 -- one 16-byte load per lane.
-// For a runtime-width (Gen) network the true widths come from p.dims: W_l
-// rows are p.dims[l + 1] wide (any width for the last layer), read element by
-// element, and entries past the true widths stage as zeros.
+// W_l[outfeat(mb, i)][16s + 8g + j], j = 0..7.  A thread issues the loads of
+// all its fragment lanes, of every layer, before writing any of them to LDS:
+// one memory round trip for the whole staging (3L-128 at NW = 4: 16 loads per
+// thread; one at a time they took 12.6 K cycles, one layer at a time 6.2 K).
+template <class N, class Gm>
+struct DgradStage {
+  static constexpr int kMaxItems = 4 * 8 * 64;  // 4 x 8 fragments of 64 lanes: a 128 x 128 layer
+  template <int NT>
+  static constexpr int per() { return (kMaxItems + NT - 1) / NT; }
+};
+
+template <class N, class Gm, int NT, int l = 0>
+__device__ __forceinline__ void dgrad_load_all(const BwdParams& p, f16x8 (&v)[N::L][DgradStage<N, Gm>::template per<NT>()]) {
+  if constexpr (l < N::L) {
+    if constexpr (Gm::has_dgrad(l)) {
+      constexpr int items = Gm::dmb(l) * Gm::dks(l) * 64;  // <= kMaxItems: widths are at most 128
+#pragma unroll
+      for (int k = 0; k < DgradStage<N, Gm>::template per<NT>(); ++k) {
+        const int item = threadIdx.x + k * NT;
+        if (item < items) v[l][k] = dgrad_fragment<N, Gm>(p, l, item);
+      }
+    }
+    dgrad_load_all<N, Gm, NT, l + 1>(p, v);
+  }
+}
+
 template <class N, class Gm, int NT>
 __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* lds) {
+  f16x8 v[N::L][DgradStage<N, Gm>::template per<NT>()];
+  dgrad_load_all<N, Gm, NT>(p, v);
 #pragma unroll
   for (int l = 0; l < N::L; ++l) {
     if (!Gm::has_dgrad(l)) continue;
-    const int Nout = N::gen ? p.dims[l + 1] : N::d[l + 1];
-    const int KS = Gm::dks(l);
-    const int items = Gm::dmb(l) * KS * 64;
-    const f16* __restrict__ w = p.w[l];
-    for (int item = threadIdx.x; item < items; item += NT) {
-      const int f = item >> 6, lane = item & 63;
-      const int mb = f / KS, s = f % KS;
-      const int i = lane & 31, g = lane >> 5;
-      const int row = outfeat(mb, i);
-      if constexpr (N::gen) {
-        f16x8 v;
-        const int k0 = 16 * s + 8 * g;
+    const int items = Gm::dmb(l) * Gm::dks(l) * 64;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          v[j] = (row < p.dims[l] && k0 + j < Nout) ? w[(int64_t)row * Nout + k0 + j] : (f16)0.0f;
-        lds[(Gm::dfrag_off(l) + f) * 64 + lane] = v;
-      } else {
-        lds[(Gm::dfrag_off(l) + f) * 64 + lane] =
-            *reinterpret_cast<const f16x8*>(w + (int64_t)row * Nout + 16 * s + 8 * g);
-      }
+    for (int k = 0; k < DgradStage<N, Gm>::template per<NT>(); ++k) {
+      const int item = threadIdx.x + k * NT;
+      if (item < items) lds[Gm::dfrag_off(l) * 64 + item] = v[l][k];
     }
   }
 }
@@ -530,9 +567,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   __shared__ f16x8 wfr[Gm::ndfrag() * 64];
   __shared__ f16 ta[Gm::fa() * R];
   __shared__ f16 tz[Gm::fz() * R];
-  stage_dgrad_weights<N, Gm, NW * 64>(p, wfr);
-  __syncthreads();
-
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   f32x16 wacc[Gm::ntpw()];
@@ -542,6 +576,8 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   wv.init_slots();
 
   // Every wave of a workgroup runs the same rounds (the barriers need all of them).
+  // The first round's rows are requested before the weight staging, so the
+  // two memory round trips overlap.
   const int64_t nrounds = (p.M + R - 1) / R;
   wv.row0 = (int64_t)blockIdx.x * R + wid * 32;
   wv.load_dout(wv.row0);
@@ -550,6 +586,8 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   } else if constexpr (N::L >= 2) {
     wv.template load_h<N::L - 1>(wv.row0);
   }
+  stage_dgrad_weights<N, Gm, NW * 64>(p, wfr);
+  __syncthreads();
   for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
     wv.round();
     wv.row0 += wv.rstep;
