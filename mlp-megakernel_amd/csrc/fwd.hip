@@ -630,12 +630,6 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   __shared__ f16x8 lds[(N::nfrag() - RF) * 64];
   __shared__ i32x4 stage_tiles[STAGE ? NW * TC : 1];
   unsigned int* const claim_ctr = ClaimSlot<CLAIM>::get();
-  if constexpr (CLAIM) {
-    if (threadIdx.x == 0) *claim_ctr = 0;
-  }
-  stage_weights<N, NW * 64, RF>(p, lds);
-  __syncthreads();
-
   const int lane = threadIdx.x & 63;
   // readfirstlane marks the wave index as wave-uniform, so the block index and
   // every buffer resource derived from it live in SGPRs (a per-lane resource
@@ -643,10 +637,29 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nblk = (p.M + ROWS - 1) / ROWS;
   const int64_t G = gridDim.x;
+  // Wave w's first block is the workgroup's w-th (static); later blocks are
+  // claimed from the counter, which starts past the first NW.  The persistent
+  // kernels (more than 8 waves) request the first block's x rows before the
+  // weight staging (5L-128 at 1M rows: 315 -> 203 us in separate-process
+  // runs; 3L-128 unchanged); the 4- and 8-wave kernels of smaller batches
+  // request them after it (M = 65536: 11.7 / 19.3 us against 12.8 / 21.7 us
+  // with the early request, 3L / 5L).  Past the end a block's resource is
+  // empty: reads zeros.
+  static_assert(D == 1, "one block of x rows in flight per wave");
+  constexpr bool kEarlyX = NW > 8;
+  Chain<N, NB, KSM> c;
+  const int64_t b0 = (int64_t)blockIdx.x + (int64_t)wid * G;
+  if constexpr (kEarlyX) load_block_x<N, NB>(c.xa, p, b0 * ROWS, lane);
+  if constexpr (CLAIM) {
+    if (threadIdx.x == 0) *claim_ctr = NW;
+  }
+  stage_weights<N, NW * 64, RF>(p, lds);
+  __syncthreads();
+
   i32x4* stage = stage_tiles + (STAGE ? wid * TC : 0);
   // Next block of this workgroup (>= nblk once its share is exhausted).  Without
   // LDS room for the counter, wave w takes the workgroup's blocks w, w + NW, ...
-  unsigned int seq = (unsigned int)wid;
+  unsigned int seq = (unsigned int)wid + NW;
   auto claim = [&]() -> int64_t {
     unsigned int j;
     if constexpr (CLAIM) {
@@ -661,15 +674,12 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
     return (int64_t)blockIdx.x + (int64_t)j * G;
   };
 
-  // Past the end a block's resource is empty: its prefetch reads zeros.
-  static_assert(D == 1, "one block of x rows in flight per wave");
-  Chain<N, NB, KSM> c;
   c.rf = RF ? weight_fragment<N>(p, 0, 0, lane) : f16x8{};
   const char* lds_b = reinterpret_cast<const char*>(lds);
   const int lane_off = lane * 16;  // this lane's 16 bytes within a 1 KiB fragment
-  int64_t b = claim();
+  int64_t b = b0;
   if (b >= nblk) return;  // no barrier follows
-  load_block_x<N, NB>(c.xa, p, b * ROWS, lane);
+  if constexpr (!kEarlyX) load_block_x<N, NB>(c.xa, p, b * ROWS, lane);
   load_frags<N, 0, KSM, RF>(c.fr, FragBase<N, RF>(lds_b, lane_off), c.rf);
   // The first block is peeled so that the loop header is entered from two
   // paths with the same outstanding memory operations (the x refill, then
