@@ -206,16 +206,31 @@ def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
 
 
 
-def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3):
+def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None):
     """One training step of BASELINE config 5 through the drop-in module:
     weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
     megakernel + weight-norm backward, x without grad.  Timed with HIP events
     around `steps` back-to-back autograd steps (Python dispatch included), and
     around `steps` replays of the whole step captured as one HIP graph."""
     import fused_mlp
+    from mlpmk import autograd as mag
+
+    policy = mag.RECOMPUTE
+    if recompute is not None:
+        mag.RECOMPUTE = recompute
+    try:
+        return _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers)
+    finally:
+        mag.RECOMPUTE = policy
+
+
+def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers):
+    from mlpmk import autograd as mag
 
     torch.manual_seed(0)
     model = fused_mlp.FusedMLPSoftplusWN(n_layers=n_layers).cuda()
+    dims = tuple(model.dims)
+    rc = mag._use_recompute(dims, m, False)
     x = torch.randn(m, 128, device="cuda").half()
 
     def step(_):
@@ -244,9 +259,11 @@ def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3):
     with gc_paused():
         gms = time_launches(torch, lambda i: graph.replay(), steps, warmup)
     # per row: x + out + stash written in the forward; dout, stash, x read
-    # back (no dx).  Flops: forward 2*sum(in*out), dgrad of layers 1.., wgrad.
-    nbytes = 256 + 256 + 512 * (n_layers - 1) + 256 + 512 * (n_layers - 1) + 256
-    flop = 32768 * (3 * n_layers - 1)
+    # back (no dx).  Flops: forward 2*sum(in*out), dgrad of layers 1.., wgrad
+    # (+ the recomputed layer).
+    nstash = n_layers - 1 - (1 if rc else 0)
+    nbytes = 256 + 256 + 512 * nstash + 256 + 512 * nstash + 256
+    flop = 32768 * (3 * n_layers - 1 + (1 if rc else 0))
     return {
         "ms_per_step": round(ms, 5),
         "rows_per_s": m / (ms * 1e-3),
@@ -256,6 +273,7 @@ def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3):
         "graph_rows_per_s": m / (gms * 1e-3),
         "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd" if n_layers == 3 else
                     "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..2, then 1..0) + wn_bwd",
+        "recompute_h_last": rc,
     }
 
 
@@ -464,6 +482,9 @@ def main():
     if args.train:
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
         result["training_5l"] = {str(mt): train_step_bench(torch, mt, n_layers=5) for mt in (65536, 131072)}
+        result["training_stash_vs_recompute"] = {
+            str(mt): {pol: train_step_bench(torch, mt, steps=20, warmup=5, recompute=pol) for pol in ("never", "always")}
+            for mt in (131072, 1048576)}
         result["backward_vs_pytorch_fallback"] = {str(mt): backward_comparison(torch, ops, mt)
                                                   for mt in (4096, 32768, 131072, 1048576)}
 

@@ -69,6 +69,21 @@ int mlpmk_fwd_supported(int num_layers, const int* dims);
 int mlpmk_bwd_supported(int num_layers, const int* dims);
 
 /*
+ * 1 if mlpmk_bwd / mlpmk_bwd_ws accept stash[num_layers-2] == NULL for
+ * (num_layers, dims), else 0.  Host only.  The backward then recomputes the
+ * last hidden activation h_{L-1} = softplus(h_{L-2} W_{L-2}) at the start of
+ * each row block, from the stashed h_{L-2} and W_{L-2}, instead of reading it:
+ * the training forward writes, and the backward reads, one fp32 activation
+ * block less (M x 512 bytes for the 3-layer 128-wide network, half of its
+ * stash) for one more layer of MFMA and softplus work.  The reference lists
+ * this trade as future work ("skip saving H in forward, recompute from X +
+ * weights in backward", /root/reference/mlp_fused.md:451-452).  Supported:
+ * the 3-layer 128-wide network, without dx (the recomputed layer's weight
+ * fragments take the LDS that the dx layer's would need).
+ */
+int mlpmk_bwd_recompute_supported(int num_layers, const int* dims);
+
+/*
  * Forward megakernel (one launch).
  *
  * Replaces the reference's inference launcher `_fused_mlp_fwd(x, w1, w2, w3)`
@@ -80,7 +95,9 @@ int mlpmk_bwd_supported(int num_layers, const int* dims);
  *   w[l]   [dims[l], dims[l+1]]    fp16, device, l = 0 .. num_layers-1
  *   out    [M, dims[num_layers]]   fp16, device (written)
  *   stash  NULL for inference, or an array of num_layers-1 device pointers,
- *          stash[l] = h_{l+1} [M, dims[l+1]] fp32 (post-activation, written)
+ *          stash[l] = h_{l+1} [M, dims[l+1]] fp32 (post-activation, written);
+ *          a NULL entry is not written (the recomputing backward below
+ *          needs no h_{num_layers-1})
  */
 int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const* w, void* out,
               float* const* stash, int64_t M, void* stream);
@@ -96,7 +113,11 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
  *
  *   x                [M, dims[0]] fp16
  *   w[l]             as in mlpmk_fwd
- *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd
+ *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd;
+ *                    stash[num_layers-2] may be NULL where
+ *                    mlpmk_bwd_recompute_supported says so: the kernel then
+ *                    recomputes h_{num_layers-1} from h_{num_layers-2}
+ *                    (dx must be NULL in that mode)
  *   dout             dL/dout, fp16, row l at dout + l * dout_row_stride
  *                    elements; dout_row_stride = 0 broadcasts one row
  *                    (the expanded ones of loss = out.sum()), otherwise a

@@ -22,6 +22,7 @@ SIGNATURES = {
     "mlpmk_last_error": (c_char_p, []),
     "mlpmk_fwd_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_supported": (c_int, [c_int, P_INT]),
+    "mlpmk_bwd_recompute_supported": (c_int, [c_int, P_INT]),
     "mlpmk_fwd": (c_int, [c_int, P_INT, c_void_p, P_VOIDP, c_void_p, P_VOIDP, c_int64, c_void_p]),
     "mlpmk_bwd": (
         c_int,

@@ -10,6 +10,10 @@ Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
 * backward: one backward-megakernel launch (``mlpmk_bwd``) producing every fp32
   weight gradient (and ``dx`` when ``x`` needs it); with weight norm, one more
   launch turning all ``dW`` into ``dv, dg`` (``mlpmk_wn_bwd``).
+* activation recomputation (``RECOMPUTE``): for networks with a recomputing
+  backward (``ops.bwd_recompute_supported``) and ``x`` without grad, the
+  forward stashes h_1 .. h_{L-2} only and the backward recomputes h_{L-1}
+  (/root/reference/mlp_fused.md:451-452 lists this trade as future work).
 * AMP: ``custom_fwd(device_type="cuda", cast_inputs=torch.float16)`` and
   ``custom_bwd`` as mlp_fused.md:168-172 describes.
 
@@ -20,6 +24,28 @@ from __future__ import annotations
 import torch
 
 from . import ops
+
+# Activation recomputation policy: "auto" recomputes h_{L-1} from
+# RECOMPUTE_MIN_ROWS rows on, where the training step is faster with it
+# (3-layer 128-wide network on MI355X, forward + backward replayed as one HIP
+# graph: 374 -> 352 us at 524288 rows, 716 -> 655 us at 1048576; within 2 %
+# either way at 4096 .. 131072 rows) and the stash is half the size;
+# "always" / "never" force the choice where the shape allows it.
+RECOMPUTE = "auto"
+RECOMPUTE_MIN_ROWS = 1 << 19
+
+_rc_shapes = {}
+
+
+def _use_recompute(dims, m, need_dx):
+    if need_dx or RECOMPUTE == "never":
+        return False
+    if RECOMPUTE not in ("auto", "always"):
+        raise ValueError(f"RECOMPUTE must be 'auto', 'always' or 'never', got {RECOMPUTE!r}")
+    ok = _rc_shapes.get(dims)
+    if ok is None:
+        ok = _rc_shapes[dims] = ops.bwd_recompute_supported(list(dims))
+    return ok and (RECOMPUTE == "always" or m >= RECOMPUTE_MIN_ROWS)
 
 
 def _as_row_broadcast(dout):
@@ -47,9 +73,12 @@ class FusedMLPFunction(torch.autograd.Function):
         x = x.contiguous()
         weights = [w.contiguous() for w in weights]
         if any(ctx.needs_input_grad):
-            out, hs = ops.fwd(x, weights, stash=True)
-            ctx.save_for_backward(x, *weights, *hs)
+            dims = (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights)
+            rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0])
+            out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
+            ctx.save_for_backward(x, *weights, *[h for h in hs if h is not None])
             ctx.n_layers = len(weights)
+            ctx.recompute = rc
         else:
             out = ops.fwd(x, weights)
         return out
@@ -60,6 +89,8 @@ class FusedMLPFunction(torch.autograd.Function):
         L = ctx.n_layers
         saved = ctx.saved_tensors
         x, weights, hs = saved[0], list(saved[1 : 1 + L]), list(saved[1 + L :])
+        if ctx.recompute:
+            hs.append(None)  # h_{L-1}: recomputed by the backward kernel
         dout = _as_row_broadcast(dout.to(torch.float16))
         dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
@@ -89,9 +120,11 @@ class FusedMLPWNFunction(torch.autograd.Function):
         ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
         weights = _split(w_all, dims)
         if any(ctx.needs_input_grad):
-            out, hs = ops.fwd(x, weights, stash=True)
-            ctx.save_for_backward(x, v_all, g_all, w_all, inv_all, *hs)
+            rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0])
+            out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
+            ctx.save_for_backward(x, v_all, g_all, w_all, inv_all, *[h for h in hs if h is not None])
             ctx.dims = dims
+            ctx.recompute = rc
         else:
             out = ops.fwd(x, weights)
         return out
@@ -101,6 +134,8 @@ class FusedMLPWNFunction(torch.autograd.Function):
     def backward(ctx, dout):
         dims = ctx.dims
         x, v_all, g_all, w_all, inv_all, *hs = ctx.saved_tensors
+        if ctx.recompute:
+            hs.append(None)  # h_{L-1}: recomputed by the backward kernel
         weights = _split(w_all, dims)
         dout = _as_row_broadcast(dout.to(torch.float16))
         dw_all = torch.zeros(w_all.numel(), dtype=torch.float32, device=x.device)

@@ -15,6 +15,7 @@ namespace mlpmk {
 bool fwd_supported_dims(int L, const int* dims);
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st);
 bool bwd_supported_dims(int L, const int* dims);
+bool bwd_recompute_supported(int L, const int* dims);
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st);
 int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes);
 int wn_fwd_dispatch(int L, const int* dims, int dtype, const void* v, const void* g, void* w_out,
@@ -121,6 +122,11 @@ int mlpmk_bwd_supported(int num_layers, const int* dims) {
   return bwd_supported_dims(num_layers, dims) ? 1 : 0;
 }
 
+int mlpmk_bwd_recompute_supported(int num_layers, const int* dims) {
+  if (!dims || num_layers < 2 || num_layers > kMaxLayersHost) return 0;
+  return bwd_recompute_supported(num_layers, dims) ? 1 : 0;
+}
+
 int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const* w, void* out,
               float* const* stash, int64_t M, void* stream) {
   g_last_error[0] = 0;
@@ -142,6 +148,7 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
   if ((rc = check_ptr(out, "out"))) return rc;
   if (stash) {
     for (int l = 0; l < num_layers - 1; ++l) {
+      if (!stash[l]) continue;  // not written
       char name[16];
       snprintf(name, sizeof(name), "stash[%d]", l);
       if ((rc = check_ptr(stash[l], name))) return rc;
@@ -190,6 +197,10 @@ static int bwd_common(int num_layers, const int* dims, const void* x, const void
   for (int l = 0; l < num_layers - 1; ++l) {
     char name[16];
     snprintf(name, sizeof(name), "stash[%d]", l);
+    if (!stash[l] && l == num_layers - 2 && num_layers > 2 && bwd_recompute_supported(num_layers, dims)) {
+      if (dx) return fail(MLPMK_ERR_INVALID_ARG, "%s is NULL (recompute mode), which computes no dx", name);
+      continue;  // the kernel recomputes h_{L-1}
+    }
     if ((rc = check_ptr(stash[l], name))) return rc;
     p.stash[l] = stash[l];
   }

@@ -105,7 +105,12 @@ struct BwdGeom {
     for (int i = SEG ? 0 : 1; i < L; ++i) m = N::d[i] / 16 > m ? N::d[i] / 16 : m;
     return m;
   }
-  static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
+  // Recompute mode (N::rc): a_{L-1} = h_{L-1} is not read from the stash but
+  // recomputed at the start of every round from h_{L-2} with W_{L-2}, whose
+  // forward A fragments take rc_frags() KiB of LDS.
+  static constexpr bool RC = N::rc;
+  static constexpr int rc_frags() { return RC ? N::mbs(L - 2) * N::ks(L - 2) : 0; }
+  static constexpr int lds_bytes() { return (ndfrag() + rc_frags()) * 1024 + (fa() + fz()) * R * 2; }
   // Per-layer prefetch: every stash layer (and x) gets its own register
   // buffer, reloaded for the next round right after its last use, so each
   // load has a whole round to arrive instead of one wgrad.  Measured at
@@ -126,6 +131,7 @@ struct BwdGeom {
     for (int i = 1; i < L; ++i)
       if (N::d[i] % 32 != 0) return false;  // hidden widths in whole 32-feature blocks
     if (DX && N::d[0] % 32 != 0) return false;
+    if (RC && (L != 3 || DX || SEG || N::gen)) return false;  // recompute: the 3-layer network, no dx
     return N::valid() && R >= 128 && lds_bytes() <= 163840;
   }
 };
@@ -199,6 +205,42 @@ __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* l
   }
 }
 
+// Recompute mode: the forward A fragments of W_{L-2} (hidden to hidden, so
+// unscaled, as the forward stages them): fragment (mb, s), lane (i, g) holds
+// W[16s + 8g + j][outfeat(mb, i)].  Thread t loads the 8 x 8 tile at rows
+// 8kb.., columns 8cb.. with 16-byte row loads and transposes it in registers:
+// column q of the tile is lane (i, g)'s 16 bytes of fragment (mb, s), with
+// s = kb / 2, g = kb % 2, mb = cb / 4 and i = 16 (cb/2 % 2) + 8 (q/4) + 4 (cb % 2) + q % 4.
+template <class N, int NT>
+__device__ __forceinline__ void stage_rc_weights(const BwdParams& p, f16x8* lds) {
+  constexpr int l = N::L - 2;
+  constexpr int Nout = N::d[l + 1], KS = N::ks(l), CB = N::mbs(l) * 4, TASKS = (N::d[l] / 8) * CB;
+  static_assert(N::d[l + 1] % 32 == 0, "whole 32-feature blocks");
+  for (int t = threadIdx.x; t < TASKS; t += NT) {
+    const int kb = t / CB, cb = t % CB;
+    const f16* src = p.w[l] + (int64_t)(8 * kb) * Nout + 8 * cb;
+    f16x8 r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = *reinterpret_cast<const f16x8*>(src + (int64_t)j * Nout);
+    const int s = kb >> 1, g = kb & 1, mb = cb >> 2;
+    const int ibase = 16 * ((cb >> 1) & 1) + 4 * (cb & 1);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      f16x8 v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = r[j][q];
+      lds[(mb * KS + s) * 64 + 32 * g + ibase + 8 * (q >> 2) + (q & 3)] = v;
+    }
+  }
+}
+
+// Recompute mode for a network type: the backward recomputes h_{L-1} instead
+// of reading it (the forward then stashes only h_1 .. h_{L-2}).
+template <class Base>
+struct Recompute : Base {
+  static constexpr bool rc = true;
+};
+
 template <class N, int NW, bool DX, bool SEG>
 struct BwdWave {
   using Gm = BwdGeom<N, NW, DX, SEG>;
@@ -211,7 +253,7 @@ struct BwdWave {
   static constexpr int FA = Gm::fa(), FZ = Gm::fz();  // features per exchange-tile row
 
   const BwdParams& p;
-  const f16x8* wfr;  // staged dgrad fragments
+  const f16x8* wfr;  // staged dgrad fragments (followed by the recompute fragments in RC mode)
   f16* ta;           // exchange tile: a_l, [row][feature] (FA features per row)
   f16* tz;           // exchange tile: dz_l, [row][feature] (FZ features per row)
   int lane, n, g, wid;
@@ -472,7 +514,10 @@ struct BwdWave {
       load_x(row0);
     } else {  // the next round of this workgroup (empty resources past the end)
       load_dout(row0 + rstep);
-      if constexpr (L >= 2) load_h<L - 1>(row0 + rstep);
+      if constexpr (Gm::RC)
+        load_h<L - 2>(row0 + rstep);  // the round recomputes h_{L-1} from it
+      else if constexpr (L >= 2)
+        load_h<L - 1>(row0 + rstep);
     }
     wgrad<l>();
     __syncthreads();  // the tiles are free for the next layer
@@ -494,7 +539,81 @@ struct BwdWave {
     if constexpr (l > 0) phases_from<l - 1>(dzn, dz);
   }
 
+  // Recompute mode, start of a round: hbuf holds h_{L-2} (fp32, natural
+  // units, as the stash keeps it); replace it by h_{L-1} = softplus(h_{L-2}
+  // W_{L-2}).  The MFMA operands are those of the forward -- h_{L-2} in base-2
+  // units packed to fp16 (the stash holds that value times ln 2) against the
+  // unscaled fragments -- and the stored value is sp2 of the product times
+  // ln 2 (u itself past 2^u's overflow, as in the forward's exact form).  The
+  // fp32 round trip through ln 2 can move a packed operand by one fp16 ulp,
+  // so h_{L-1} agrees with the stashed value to fp16 operand rounding, not
+  // bit for bit.  Where some operand of the wave would overflow fp16 (h above
+  // ~45400), the operands are halved and the products doubled, as the
+  // forward's exact form does.
+  template <bool HALF>
+  __device__ __forceinline__ void recompute_t() {
+    constexpr int l = L - 2;
+    constexpr int KSI = N::d[l] / 16, MBO = N::d[l + 1] / 32;
+    constexpr float sc = HALF ? 0.5f * kLog2e : kLog2e;
+    f16x8 bop[KSI];
+#pragma unroll
+    for (int s = 0; s < KSI; ++s)
+      bop[s] = pack8(hbuf[0][s][0] * sc, hbuf[0][s][1] * sc, hbuf[0][s][2] * sc, hbuf[0][s][3] * sc,
+                     hbuf[0][s][4] * sc, hbuf[0][s][5] * sc, hbuf[0][s][6] * sc, hbuf[0][s][7] * sc);
+    const int fbase = (Gm::ndfrag() * 64 + lane) * 16;
+    const char* wb = reinterpret_cast<const char*>(wfr);
+    // Software pipeline over the 32-feature blocks: block mb's MFMA chain
+    // shares a scheduling region with block mb - 1's activations, and the
+    // fences keep the compiler from hoisting later blocks' fragment reads
+    // (all 32 at once would not fit beside the weight-gradient accumulators).
+    f32x16 acc[2];
+#pragma unroll
+    for (int mb = 0; mb <= MBO; ++mb) {
+      if (mb < MBO) {
+        const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSI * 1024));
+        f32x16 a = {};
+#pragma unroll
+        for (int s = 0; s < KSI; ++s) a = mfma32x32x16(frag[s * 64], bop[s], a);
+        acc[mb & 1] = a;
+      }
+      if (mb > 0) {
+        // Registers 0..7: features 32q + 8g + [0..7] (K-step 2q); 8..15: K-step 2q + 1.
+        const int q = mb - 1;
+        const f32x16& a = acc[q & 1];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float u0 = HALF ? 2.0f * a[j] : a[j], u1 = HALF ? 2.0f * a[8 + j] : a[8 + j];
+          hbuf[0][2 * q][j] = sp2_fix(u0, sp2(u0)) * kLn2;
+          hbuf[0][2 * q + 1][j] = sp2_fix(u1, sp2(u1)) * kLn2;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __device__ __forceinline__ void recompute() {
+    constexpr int KSI = N::d[L - 2] / 16;
+    float m = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KSI; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) m = fmaxf(m, fmaxf(hbuf[0][s][j], hbuf[0][s][j + 1]));
+    if (__builtin_amdgcn_ballot_w64(m * kLog2e > 65504.0f) != 0)
+      recompute_t<true>();
+    else
+      recompute_t<false>();
+    // Rows past M read h_{L-2} = 0 and would recompute softplus(0) = ln 2,
+    // where a stash reads 0: with a broadcast dout (row stride 0) those rows
+    // see a nonzero gradient, so their h_{L-1} must be 0 as well.
+    if (nrows_at(row0) < 32 && row0 + n >= p.M) {
+#pragma unroll
+      for (int s = 0; s < N::d[L - 1] / 16; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hbuf[0][s][j] = 0.0f;
+    }
+  }
+
   __device__ __forceinline__ void round() {
+    if constexpr (Gm::RC) recompute();
     f16x8 dz[KSM], dzn[KSM];
 #pragma unroll
     for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
@@ -564,7 +683,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   using Gm = BwdGeom<N, NW, DX, SEG>;
   static_assert(Gm::valid(), "unsupported backward shape");
   constexpr int R = Gm::R;
-  __shared__ f16x8 wfr[Gm::ndfrag() * 64];
+  __shared__ f16x8 wfr[(Gm::ndfrag() + Gm::rc_frags()) * 64];
   __shared__ f16 ta[Gm::fa() * R];
   __shared__ f16 tz[Gm::fz() * R];
   const int lane = threadIdx.x & 63;
@@ -583,10 +702,13 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   wv.load_dout(wv.row0);
   if constexpr (BwdWave<N, NW, DX, SEG>::PF) {
     wv.template prefetch_all<N::L - 1>(wv.row0);
+  } else if constexpr (Gm::RC) {
+    wv.template load_h<N::L - 2>(wv.row0);
   } else if constexpr (N::L >= 2) {
     wv.template load_h<N::L - 1>(wv.row0);
   }
   stage_dgrad_weights<N, Gm, NW * 64>(p, wfr);
+  if constexpr (Gm::RC) stage_rc_weights<N, NW * 64>(p, wfr + Gm::ndfrag() * 64);
   __syncthreads();
   for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
     wv.round();
@@ -841,7 +963,19 @@ int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* byt
 
 bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims); }
 
+// The 3-layer 128-wide network also runs in recompute mode: with a NULL
+// stash for h_2 (the forward then writes only h_1) the backward recomputes
+// h_2 from h_1 at the start of every round; no dx in that mode (the W_2
+// forward fragments take the LDS that dx's W_1 dgrad fragments would need).
+typedef Recompute<BNet3L128> RBNet3L128;
+
+bool bwd_recompute_supported(int L, const int* dims) { return bdims_match<BNet3L128>(L, dims); }
+
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st) {
+  if (bdims_match<BNet3L128>(L, dims) && !p.stash[1]) {
+    if (p.dx) return fail(MLPMK_ERR_INVALID_ARG, "recomputing h_2 (stash[1] == NULL) has no dx");
+    return launch_bwd<RBNet3L128, 4, false>(p, st);
+  }
   if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<BNet3L128, 4>(p, st);
   if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<BNet3L128, BNet2L128>(p, L, st);
   if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<BNetNarrow, 4>(p, st);

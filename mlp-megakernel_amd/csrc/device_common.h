@@ -163,6 +163,7 @@ __device__ __forceinline__ int opaque(int v) {
 template <int... Ds>
 struct Net {
   static constexpr bool gen = false;  // widths fixed at compile time
+  static constexpr bool rc = false;   // backward: h_{L-1} read from the stash (see Recompute in bwd.hip)
   static constexpr int L = sizeof...(Ds) - 1;
   static constexpr int d[sizeof...(Ds)] = {Ds...};
   // K-steps (16 input features each) and 32-row output blocks of layer l.

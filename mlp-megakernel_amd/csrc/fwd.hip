@@ -252,7 +252,8 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
   if constexpr (STASH) {
 #pragma unroll
     for (int l = 0; l < N::L - 1; ++l)
-      io.stash[l] = make_rsrc(p.stash[l] + row0 * io.dl[l + 1], rows * io.dl[l + 1] * 4u);
+      io.stash[l] = p.stash[l] ? make_rsrc(p.stash[l] + row0 * io.dl[l + 1], rows * io.dl[l + 1] * 4u)
+                               : make_rsrc(nullptr, 0u);  // not requested: every store dropped
   }
   return io;
 }

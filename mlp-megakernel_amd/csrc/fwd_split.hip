@@ -253,7 +253,8 @@ __device__ __forceinline__ void layer(const FwdParams& p, const Frags<N>& f, con
     const f16x8 hi = pack8(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
     if constexpr (!EXACT) m = sp2_track<true>(m, lo, hi);
     if constexpr (STASH) {
-      const rsrc_t sr = make_rsrc(p.stash[l] + row0 * Nout, rows * Nout * 4u);
+      const rsrc_t sr = p.stash[l] ? make_rsrc(p.stash[l] + row0 * Nout, rows * Nout * 4u)
+                                   : make_rsrc(nullptr, 0u);  // not requested: every store dropped
       float h[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) h[e] = s[e] * kLn2;

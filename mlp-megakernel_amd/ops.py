@@ -55,6 +55,14 @@ def bwd_supported(dims):
     return bool(lib.mlpmk_bwd_supported(len(dims) - 1, p))
 
 
+def bwd_recompute_supported(dims):
+    """True if the backward recomputes h_{L-1} when its stash entry is None
+    (``mlpmk_bwd_recompute_supported``; no dx in that mode)."""
+    lib = _lib.get()
+    p, _keep = _lib.int_array(dims)
+    return bool(lib.mlpmk_bwd_recompute_supported(len(dims) - 1, p))
+
+
 def _require(t, name, dtype, device):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
@@ -92,8 +100,9 @@ def fwd_into(x, weights, out, stash=None):
     """Run the forward megakernel writing ``out`` (and ``stash`` if given).
 
     ``x`` [M, D] fp16, ``weights`` list of [in, out] fp16, ``out`` [M, OUT]
-    fp16, ``stash`` list of L-1 fp32 [M, H_l] tensors or None.  All contiguous
-    on one CUDA (HIP) device.
+    fp16, ``stash`` list of L-1 fp32 [M, H_l] tensors (an entry may be None:
+    that activation is not written) or None.  All contiguous on one CUDA
+    (HIP) device.
     """
     dev = x.device
     if dev.type != "cuda":
@@ -113,10 +122,12 @@ def fwd_into(x, weights, out, stash=None):
         if len(stash) != len(weights) - 1:
             raise ValueError(f"stash needs {len(weights) - 1} tensors, got {len(stash)}")
         for i, s in enumerate(stash):
+            if s is None:
+                continue
             _require(s, f"stash[{i}]", torch.float32, dev)
             if tuple(s.shape) != (M, dims[i + 1]):
                 raise ValueError(f"stash[{i}] has shape {tuple(s.shape)}, expected {(M, dims[i + 1])}")
-        stash_ptrs = [s.data_ptr() for s in stash]
+        stash_ptrs = [s.data_ptr() if s is not None else None for s in stash]
     lib = _lib.get()
     pd, _k1 = _lib.int_array(dims)
     pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
@@ -126,10 +137,12 @@ def fwd_into(x, weights, out, stash=None):
     return out
 
 
-def fwd(x, weights, stash=False):
+def fwd(x, weights, stash=False, recompute=False):
     """Allocate ``out`` (and the fp32 stash when ``stash``) and run the forward.
 
-    Returns ``out`` or ``(out, [h1, ..., h_{L-1}])``.
+    Returns ``out`` or ``(out, [h1, ..., h_{L-1}])``.  With ``recompute`` the
+    last entry is None and h_{L-1} is not written: the backward recomputes it
+    (``bwd_recompute_supported``).
     """
     dims = _dims_of(x, weights)
     M = int(x.shape[0])
@@ -137,6 +150,8 @@ def fwd(x, weights, stash=False):
     hs = None
     if stash:
         hs = [torch.empty((M, d), device=x.device, dtype=torch.float32) for d in dims[1:-1]]
+        if recompute:
+            hs[-1] = None
     fwd_into(x, weights, out, hs)
     return (out, hs) if stash else out
 
@@ -170,7 +185,8 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     With ``workspace`` (default) the weight-gradient partials of the
     workgroups go through a workspace from torch's allocator and a second
     kernel (``mlpmk_bwd_ws``); otherwise every workgroup adds its partials
-    with fp32 atomics (``mlpmk_bwd``).
+    with fp32 atomics (``mlpmk_bwd``).  A None last stash entry selects the
+    recomputing backward (``bwd_recompute_supported``; no dx).
     """
     dev = x.device
     _require(x, "x", torch.float16, dev)
@@ -181,6 +197,8 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     if len(stash) != len(weights) - 1:
         raise ValueError(f"stash needs {len(weights) - 1} tensors, got {len(stash)}")
     for i, s in enumerate(stash):
+        if s is None and i == len(stash) - 1:
+            continue  # recompute mode: the library checks that the shape has it
         _require(s, f"stash[{i}]", torch.float32, dev)
         if tuple(s.shape) != (M, dims[i + 1]):
             raise ValueError(f"stash[{i}] has shape {tuple(s.shape)}, expected {(M, dims[i + 1])}")
@@ -206,7 +224,7 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     lib = _lib.get()
     pd, _k1 = _lib.int_array(dims)
     pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
-    ps, _k3 = _lib.ptr_array([s.data_ptr() for s in stash])
+    ps, _k3 = _lib.ptr_array([s.data_ptr() if s is not None else None for s in stash])
     pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
     dxp = dx.data_ptr() if dx is not None else None
     if workspace and M > 0:

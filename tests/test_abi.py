@@ -75,15 +75,17 @@ def test_fwd_validation_codes():
     assert _fwd(d, x=A + 2) == MISALIGNED
     assert _fwd(d, out=None) == INVALID
     assert _fwd(d, w=(A, A + 8, A)) == MISALIGNED
-    assert _fwd(d, stash=(A, None)) == INVALID
+    assert _fwd(d, stash=(A, A + 4)) == MISALIGNED
     assert b"stash[1]" in lib.mlpmk_last_error()
     assert lib.mlpmk_fwd(3, None, A, None, A, None, 1, None) == INVALID
     # M == 0 succeeds without touching a device (x/out may even be NULL)
     assert _fwd(d, x=None, out=None, m=0) == OK
-    # valid arguments reach the device query, which fails without a GPU
+    # valid arguments reach the device query, which fails without a GPU; a
+    # NULL stash entry is valid (that activation is not written)
     if not torch.cuda.is_available():
         assert _fwd(d) in (NODEV, HIPERR)
         assert lib.mlpmk_last_error() != b""
+        assert _fwd(d, stash=(A, None)) in (NODEV, HIPERR)
 
 
 def test_bwd_validation_codes():
@@ -106,6 +108,34 @@ def test_bwd_validation_codes():
         assert call(m=0) == OK
     else:
         assert call() == UNSUPPORTED
+
+
+@pytest.mark.parametrize("dims,ok", [((128, 128, 128, 128), True), ((128,) * 6, False), ((32, 64, 64, 16), False),
+                                     ((128, 128, 128), False), ((128, 64, 128, 128), False)])
+def test_recompute_support_table(dims, ok):
+    assert ops.bwd_recompute_supported(list(dims)) is ok
+
+
+def test_recompute_validation_codes():
+    # stash[L-2] == NULL selects the recomputing backward where it exists;
+    # every other NULL stash entry, and dx in that mode, is rejected on the host.
+    lib = _lib.get()
+    pw, _k2 = _lib.ptr_array([A, A, A])
+    pg, _k4 = _lib.ptr_array([A, A, A])
+    pd, _k1 = _lib.int_array([128] * 4)
+
+    def call(stash, dx=None, dims=pd, n=3, w=pw, g=pg):
+        ps, _k = _lib.ptr_array(list(stash))
+        return lib.mlpmk_bwd(n, dims, A, w, ps, A, 128, dx, g, 256, None)
+
+    assert call((A, None), dx=A) == INVALID
+    assert b"stash[1]" in lib.mlpmk_last_error() and b"dx" in lib.mlpmk_last_error()
+    assert call((None, A)) == INVALID
+    assert b"stash[0]" in lib.mlpmk_last_error()
+    pn, _k5 = _lib.int_array([32, 64, 64, 16])
+    assert call((A, None), dims=pn) == INVALID  # no recomputing kernel for this shape
+    if not torch.cuda.is_available():
+        assert call((A, None)) in (NODEV, HIPERR)  # valid: reaches the device query
 
 
 def test_5l_backward_is_supported_but_needs_a_workspace():
