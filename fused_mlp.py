@@ -27,6 +27,12 @@ import _mlpmk  # noqa: F401  (registers the package as ``mlpmk``)
 from mlpmk.autograd import FusedMLPFunction, FusedMLPWNFunction, _split
 
 
+def _elem_dtype(x):
+    """Element type the kernels run in for input ``x``: bf16 for bf16 input,
+    else fp16 (the reference's modules cast to fp16, README.md:24-34)."""
+    return torch.bfloat16 if x.dtype == torch.bfloat16 else torch.float16
+
+
 def _dims(D, H, out_features, n_layers):
     return (D,) + (H,) * (n_layers - 1) + (out_features,)
 
@@ -44,9 +50,11 @@ class FusedMLPSoftplus(nn.Module):
         )
 
     def forward(self, x):
-        # The kernels take fp16; under autocast custom_fwd casts, otherwise cast here
-        # (autograd carries the gradient back through the casts).
-        return FusedMLPFunction.apply(x.to(torch.float16), *[w.to(torch.float16) for w in self.weights])
+        # The kernels take fp16 or bf16: under autocast custom_fwd casts to fp16;
+        # otherwise a bf16 x runs the bf16 kernels and anything else is cast to
+        # fp16 (autograd carries the gradient back through the casts).
+        dt = _elem_dtype(x)
+        return FusedMLPFunction.apply(x.to(dt), *[w.to(dt) for w in self.weights])
 
     def extra_repr(self):
         return f"dims={self.dims}"
@@ -79,7 +87,7 @@ class FusedMLPSoftplusWN(nn.Module):
     def forward(self, x):
         if torch.is_autocast_enabled("cuda"):
             return FusedMLPWNFunction.apply(x, self.v_all, self.g_all, self.dims)
-        return FusedMLPWNFunction.apply(x.to(torch.float16), self.v_all, self.g_all, self.dims)
+        return FusedMLPWNFunction.apply(x.to(_elem_dtype(x)), self.v_all, self.g_all, self.dims)
 
     def extra_repr(self):
         return f"dims={self.dims}"

@@ -41,8 +41,13 @@ typedef enum mlpmk_status {
   MLPMK_ERR_NO_DEVICE = 5          /* no usable gfx950 device */
 } mlpmk_status;
 
-/* Parameter dtypes of the weight-norm entry points. */
-enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1 };
+/* Element types.  The megakernels (mlpmk_fwd, mlpmk_bwd*) take fp16 or bf16
+ * tensors (x, w, out, dout, dx all of that type; fp32 accumulation, fp32
+ * stash and weight gradients either way; fp32 tensors are rejected with
+ * MLPMK_ERR_UNSUPPORTED_SHAPE).  The weight-norm parameters may be fp32,
+ * fp16 or bf16.  The reference's kernels take their element type as the
+ * INPUT_DTYPE constexpr (/root/reference/mlp_fused.md:159-166). */
+enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1, MLPMK_DTYPE_BF16 = 2 };
 
 /* Library ABI version (major * 100 + minor). */
 int mlpmk_version(void);
@@ -91,15 +96,18 @@ int mlpmk_bwd_recompute_supported(int num_layers, const int* dims);
  * and its training-forward variant that stores the hidden activations
  * (/root/reference/mlp_fused.md:52-61, fp32 storage README.md:30).
  *
- *   x      [M, dims[0]]            fp16, device
- *   w[l]   [dims[l], dims[l+1]]    fp16, device, l = 0 .. num_layers-1
- *   out    [M, dims[num_layers]]   fp16, device (written)
+ *   dtype  MLPMK_DTYPE_F16 or MLPMK_DTYPE_BF16: element type of x, w and out
+ *          (bf16: bf16 MFMA operands, hidden activations rounded to bf16
+ *          between layers, as the reference's casts to INPUT_DTYPE do)
+ *   x      [M, dims[0]]            dtype, device
+ *   w[l]   [dims[l], dims[l+1]]    dtype, device, l = 0 .. num_layers-1
+ *   out    [M, dims[num_layers]]   dtype, device (written)
  *   stash  NULL for inference, or an array of num_layers-1 device pointers,
  *          stash[l] = h_{l+1} [M, dims[l+1]] fp32 (post-activation, written);
  *          a NULL entry is not written (the recomputing backward below
  *          needs no h_{num_layers-1})
  */
-int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const* w, void* out,
+int mlpmk_fwd(int num_layers, const int* dims, int dtype, const void* x, const void* const* w, void* out,
               float* const* stash, int64_t M, void* stream);
 
 /*
@@ -111,25 +119,26 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
  * function (/root/reference/mlp_fused.md:88-112, README.md:32) -- the file that
  * held it (fused_mlp.py, README.md:18) is not in the reference snapshot.
  *
- *   x                [M, dims[0]] fp16
+ *   dtype            as in mlpmk_fwd: element type of x, w, dout and dx
+ *   x                [M, dims[0]] dtype
  *   w[l]             as in mlpmk_fwd
  *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd;
  *                    stash[num_layers-2] may be NULL where
  *                    mlpmk_bwd_recompute_supported says so: the kernel then
  *                    recomputes h_{num_layers-1} from h_{num_layers-2}
  *                    (dx must be NULL in that mode)
- *   dout             dL/dout, fp16, row l at dout + l * dout_row_stride
+ *   dout             dL/dout, dtype, row l at dout + l * dout_row_stride
  *                    elements; dout_row_stride = 0 broadcasts one row
  *                    (the expanded ones of loss = out.sum()), otherwise a
  *                    multiple of 8 (16-byte rows) not below the output width
- *   dx               NULL, or [M, dims[0]] fp16 (written)
+ *   dx               NULL, or [M, dims[0]] dtype (written)
  *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
  *                    caller zeroes them for a fresh gradient
  * Networks of 4 and 5 layers are supported through mlpmk_bwd_ws only (they
  * hand dz between two launches through the workspace); here they return
  * MLPMK_ERR_INVALID_ARG without touching the device.
  */
-int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
+int mlpmk_bwd(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
               const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
               float* const* dw, int64_t M, void* stream);
 
@@ -151,10 +160,11 @@ int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const*
  * launch: the in-register chain also hands dz on as fp16.
  *   workspace        device memory, 16-byte aligned, at least the size that
  *                    mlpmk_bwd_workspace_size reports for the same
- *                    (num_layers, dims, M, dx != NULL) on the current device;
+ *                    (num_layers, dims, dtype, M, dx != NULL) on the current
+ *                    device;
  *                    free again once both launches have run (stream order)
  */
-int mlpmk_bwd_ws(int num_layers, const int* dims, const void* x, const void* const* w,
+int mlpmk_bwd_ws(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
                  const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
                  float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream);
 
@@ -164,7 +174,7 @@ int mlpmk_bwd_ws(int num_layers, const int* dims, const void* x, const void* con
  * network the dz block of the hand-over between its two launches (0 when
  * M == 0).
  */
-int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int64_t M, int with_dx, int64_t* bytes);
+int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t M, int with_dx, int64_t* bytes);
 
 /*
  * Weight-norm forward for all layers in ONE launch:
@@ -172,12 +182,14 @@ int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int64_t M, int wit
  * Replaces `_wn_fwd_kernel` (/root/reference/mlp_fused.md:473-477; code absent
  * from the snapshot).  v and g live in two contiguous blocks, layer after layer
  * (v_all / g_all, mlp_fused.md:478-480):
+ *   param_dtype  MLPMK_DTYPE_F32, _F16 or _BF16: element type of v and g
+ *   w_dtype      MLPMK_DTYPE_F16 or _BF16: element type of w_out
  *   v      sum_l dims[l]*dims[l+1] elements of param_dtype, layer l = [dims[l], dims[l+1]]
  *   g      sum_l dims[l+1] elements of param_dtype
- *   w_out  same element layout as v, fp16 (written)
+ *   w_out  same element layout as v, w_dtype (written)
  *   inv_norm  sum_l dims[l+1] fp32 (written)
  */
-int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, const void* v, const void* g,
+int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, int w_dtype, const void* v, const void* g,
                  void* w_out, float* inv_norm, void* stream);
 
 /*

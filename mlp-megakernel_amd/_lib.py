@@ -23,18 +23,18 @@ SIGNATURES = {
     "mlpmk_fwd_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_recompute_supported": (c_int, [c_int, P_INT]),
-    "mlpmk_fwd": (c_int, [c_int, P_INT, c_void_p, P_VOIDP, c_void_p, P_VOIDP, c_int64, c_void_p]),
+    "mlpmk_fwd": (c_int, [c_int, P_INT, c_int, c_void_p, P_VOIDP, c_void_p, P_VOIDP, c_int64, c_void_p]),
     "mlpmk_bwd": (
         c_int,
-        [c_int, P_INT, c_void_p, P_VOIDP, P_VOIDP, c_void_p, c_int64, c_void_p, P_VOIDP, c_int64, c_void_p],
+        [c_int, P_INT, c_int, c_void_p, P_VOIDP, P_VOIDP, c_void_p, c_int64, c_void_p, P_VOIDP, c_int64, c_void_p],
     ),
     "mlpmk_bwd_ws": (
         c_int,
-        [c_int, P_INT, c_void_p, P_VOIDP, P_VOIDP, c_void_p, c_int64, c_void_p, P_VOIDP, c_void_p, c_int64,
+        [c_int, P_INT, c_int, c_void_p, P_VOIDP, P_VOIDP, c_void_p, c_int64, c_void_p, P_VOIDP, c_void_p, c_int64,
          c_int64, c_void_p],
     ),
-    "mlpmk_bwd_workspace_size": (c_int, [c_int, P_INT, c_int64, c_int, ctypes.POINTER(c_int64)]),
-    "mlpmk_wn_fwd": (c_int, [c_int, P_INT, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "mlpmk_bwd_workspace_size": (c_int, [c_int, P_INT, c_int, c_int64, c_int, ctypes.POINTER(c_int64)]),
+    "mlpmk_wn_fwd": (c_int, [c_int, P_INT, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "mlpmk_wn_bwd": (
         c_int,
         [c_int, P_INT, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
@@ -50,7 +50,7 @@ STATUS = {
     4: "MLPMK_ERR_HIP",
     5: "MLPMK_ERR_NO_DEVICE",
 }
-DTYPE_F32, DTYPE_F16 = 0, 1
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _lock = threading.Lock()
 _lib = None

@@ -63,8 +63,8 @@ def _as_row_broadcast(dout):
 class FusedMLPFunction(torch.autograd.Function):
     """``out = softplus(... softplus(x @ W1) ...) @ WL`` with the fused backward.
 
-    Inputs: ``x`` [M, D] fp16 and L weights [in, out] fp16 (cast to fp16 under
-    autocast).  Returns fp16 ``out`` [M, OUT].
+    Inputs: ``x`` [M, D] and L weights [in, out], all fp16 or all bf16 (cast
+    to fp16 under autocast).  Returns ``out`` [M, OUT] of x's dtype.
     """
 
     @staticmethod
@@ -91,7 +91,7 @@ class FusedMLPFunction(torch.autograd.Function):
         x, weights, hs = saved[0], list(saved[1 : 1 + L]), list(saved[1 + L :])
         if ctx.recompute:
             hs.append(None)  # h_{L-1}: recomputed by the backward kernel
-        dout = _as_row_broadcast(dout.to(torch.float16))
+        dout = _as_row_broadcast(dout.to(x.dtype))
         dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
         ops.bwd(x, weights, hs, dout, dws, dx)
@@ -115,7 +115,7 @@ class FusedMLPWNFunction(torch.autograd.Function):
         L = len(dims) - 1
         dev = x.device
         nw = sum(dims[i] * dims[i + 1] for i in range(L))
-        w_all = torch.empty(nw, dtype=torch.float16, device=dev)
+        w_all = torch.empty(nw, dtype=x.dtype, device=dev)  # the megakernels' element type
         inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=dev)
         ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
         weights = _split(w_all, dims)
@@ -137,7 +137,7 @@ class FusedMLPWNFunction(torch.autograd.Function):
         if ctx.recompute:
             hs.append(None)  # h_{L-1}: recomputed by the backward kernel
         weights = _split(w_all, dims)
-        dout = _as_row_broadcast(dout.to(torch.float16))
+        dout = _as_row_broadcast(dout.to(x.dtype))
         dw_all = torch.zeros(w_all.numel(), dtype=torch.float32, device=x.device)
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
         ops.bwd(x, weights, hs, dout, _split(dw_all, dims), dx)

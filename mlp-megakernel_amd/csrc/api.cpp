@@ -13,12 +13,12 @@
 namespace mlpmk {
 
 bool fwd_supported_dims(int L, const int* dims);
-int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st);
+int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st);
 bool bwd_supported_dims(int L, const int* dims);
 bool bwd_recompute_supported(int L, const int* dims);
-int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st);
-int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes);
-int wn_fwd_dispatch(int L, const int* dims, int dtype, const void* v, const void* g, void* w_out,
+int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st);
+int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, bool bf, int64_t* bytes);
+int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* v, const void* g, void* w_out,
                     float* inv_norm, hipStream_t st);
 int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const void* v, const void* g,
                     const float* inv_norm, void* dv, void* dg, hipStream_t st);
@@ -75,6 +75,15 @@ int kernel_occupancy(const void* kernel, int threads, int* wgs_per_cu) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Element format of the 16-bit tensors of the megakernels.
+static int check_elem_dtype(int dtype) {
+  if (dtype == MLPMK_DTYPE_F16 || dtype == MLPMK_DTYPE_BF16) return MLPMK_OK;
+  if (dtype == MLPMK_DTYPE_F32)
+    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE,
+                "dtype=fp32: the megakernels take fp16 or bf16 tensors (fp32 accumulation); cast first");
+  return fail(MLPMK_ERR_INVALID_ARG, "dtype=%d (1 = fp16, 2 = bf16)", dtype);
+}
+
 static int check_dims(int L, const int* dims) {
   if (!dims) return fail(MLPMK_ERR_INVALID_ARG, "dims is NULL");
   if (L < 2 || L > kMaxLayersHost)
@@ -96,7 +105,7 @@ using namespace mlpmk;
 
 extern "C" {
 
-int mlpmk_version(void) { return 100; }
+int mlpmk_version(void) { return 200; }
 
 const char* mlpmk_status_string(int status) {
   switch (status) {
@@ -127,11 +136,12 @@ int mlpmk_bwd_recompute_supported(int num_layers, const int* dims) {
   return bwd_recompute_supported(num_layers, dims) ? 1 : 0;
 }
 
-int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const* w, void* out,
+int mlpmk_fwd(int num_layers, const int* dims, int dtype, const void* x, const void* const* w, void* out,
               float* const* stash, int64_t M, void* stream) {
   g_last_error[0] = 0;
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
+  if ((rc = check_elem_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   if (!w) return fail(MLPMK_ERR_INVALID_ARG, "w is NULL");
   if (!fwd_supported_dims(num_layers, dims))
@@ -159,14 +169,16 @@ int mlpmk_fwd(int num_layers, const int* dims, const void* x, const void* const*
   p.out = static_cast<_Float16*>(out);
   p.M = M;
   for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
-  return fwd_dispatch(num_layers, dims, p, stash != nullptr, static_cast<hipStream_t>(stream));
+  return fwd_dispatch(num_layers, dims, p, stash != nullptr, dtype == MLPMK_DTYPE_BF16,
+                      static_cast<hipStream_t>(stream));
 }
 
-static int bwd_common(int num_layers, const int* dims, const void* x, const void* const* w,
+static int bwd_common(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
                       const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
                       float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream) {
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
+  if ((rc = check_elem_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   if (dout_row_stride < 0)
     return fail(MLPMK_ERR_INVALID_ARG, "dout_row_stride=%lld is negative", (long long)dout_row_stride);
@@ -214,61 +226,65 @@ static int bwd_common(int num_layers, const int* dims, const void* x, const void
   if (workspace) {
     if ((rc = check_ptr(workspace, "workspace"))) return rc;
     int64_t need = 0;
-    if ((rc = bwd_workspace_bytes(num_layers, dims, M, dx != nullptr, &need))) return rc;
+    if ((rc = bwd_workspace_bytes(num_layers, dims, M, dx != nullptr, dtype == MLPMK_DTYPE_BF16, &need)))
+      return rc;
     if (workspace_bytes < need)
       return fail(MLPMK_ERR_INVALID_ARG, "workspace_bytes=%lld is below the %lld bytes needed",
                   (long long)workspace_bytes, (long long)need);
     p.part = static_cast<float*>(workspace);
   }
-  return bwd_dispatch(num_layers, dims, p, static_cast<hipStream_t>(stream));
+  return bwd_dispatch(num_layers, dims, p, dtype == MLPMK_DTYPE_BF16, static_cast<hipStream_t>(stream));
 }
 
-int mlpmk_bwd(int num_layers, const int* dims, const void* x, const void* const* w,
+int mlpmk_bwd(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
               const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
               float* const* dw, int64_t M, void* stream) {
   g_last_error[0] = 0;
-  return bwd_common(num_layers, dims, x, w, stash, dout, dout_row_stride, dx, dw, nullptr, 0, M, stream);
+  return bwd_common(num_layers, dims, dtype, x, w, stash, dout, dout_row_stride, dx, dw, nullptr, 0, M, stream);
 }
 
-int mlpmk_bwd_ws(int num_layers, const int* dims, const void* x, const void* const* w,
+int mlpmk_bwd_ws(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
                  const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
                  float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream) {
   g_last_error[0] = 0;
   if (!workspace) return fail(MLPMK_ERR_INVALID_ARG, "workspace is NULL");
-  return bwd_common(num_layers, dims, x, w, stash, dout, dout_row_stride, dx, dw, workspace, workspace_bytes,
-                    M, stream);
+  return bwd_common(num_layers, dims, dtype, x, w, stash, dout, dout_row_stride, dx, dw, workspace,
+                    workspace_bytes, M, stream);
 }
 
-int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int64_t M, int with_dx, int64_t* bytes) {
+int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t M, int with_dx, int64_t* bytes) {
   g_last_error[0] = 0;
   if (!bytes) return fail(MLPMK_ERR_INVALID_ARG, "bytes is NULL");
   *bytes = 0;
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
+  if ((rc = check_elem_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   if (!bwd_supported_dims(num_layers, dims))
     return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
   if (M == 0) return MLPMK_OK;
-  return bwd_workspace_bytes(num_layers, dims, M, with_dx != 0, bytes);
+  return bwd_workspace_bytes(num_layers, dims, M, with_dx != 0, dtype == MLPMK_DTYPE_BF16, bytes);
 }
 
 static int check_wn(int num_layers, const int* dims, int dtype) {
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
-  if (dtype != MLPMK_DTYPE_F32 && dtype != MLPMK_DTYPE_F16)
-    return fail(MLPMK_ERR_INVALID_ARG, "param_dtype=%d (0 = fp32, 1 = fp16)", dtype);
+  if (dtype != MLPMK_DTYPE_F32 && dtype != MLPMK_DTYPE_F16 && dtype != MLPMK_DTYPE_BF16)
+    return fail(MLPMK_ERR_INVALID_ARG, "param_dtype=%d (0 = fp32, 1 = fp16, 2 = bf16)", dtype);
   return MLPMK_OK;  // element-wise kernels: any positive widths
 }
 
-int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, const void* v, const void* g,
+int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, int w_dtype, const void* v, const void* g,
                  void* w_out, float* inv_norm, void* stream) {
   g_last_error[0] = 0;
   int rc = check_wn(num_layers, dims, param_dtype);
   if (rc) return rc;
+  if (w_dtype != MLPMK_DTYPE_F16 && w_dtype != MLPMK_DTYPE_BF16)
+    return fail(MLPMK_ERR_INVALID_ARG, "w_dtype=%d (1 = fp16, 2 = bf16)", w_dtype);
   if ((rc = check_ptr(v, "v")) || (rc = check_ptr(g, "g")) || (rc = check_ptr(w_out, "w_out")) ||
       (rc = check_ptr(inv_norm, "inv_norm")))
     return rc;
-  return wn_fwd_dispatch(num_layers, dims, param_dtype, v, g, w_out, inv_norm,
+  return wn_fwd_dispatch(num_layers, dims, param_dtype, w_dtype, v, g, w_out, inv_norm,
                          static_cast<hipStream_t>(stream));
 }
 

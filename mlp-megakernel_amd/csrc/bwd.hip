@@ -413,10 +413,10 @@ struct BwdWave {
           const int fi = 64 * (q / QO), fo = 64 * (q % QO);
           const f16x8 a0 = xread<FA>(ta, fi, kk), a1 = xread<FA>(ta, fi + 32, kk);
           const f16x8 b0 = xread<FZ>(tz, fo, kk), b1 = xread<FZ>(tz, fo + 32, kk);
-          wacc[OFF + 4 * k + 0] = mfma32x32x16(a0, b0, wacc[OFF + 4 * k + 0]);
-          wacc[OFF + 4 * k + 1] = mfma32x32x16(a0, b1, wacc[OFF + 4 * k + 1]);
-          wacc[OFF + 4 * k + 2] = mfma32x32x16(a1, b0, wacc[OFF + 4 * k + 2]);
-          wacc[OFF + 4 * k + 3] = mfma32x32x16(a1, b1, wacc[OFF + 4 * k + 3]);
+          wacc[OFF + 4 * k + 0] = mfma32x32x16<N::bf>(a0, b0, wacc[OFF + 4 * k + 0]);
+          wacc[OFF + 4 * k + 1] = mfma32x32x16<N::bf>(a0, b1, wacc[OFF + 4 * k + 1]);
+          wacc[OFF + 4 * k + 2] = mfma32x32x16<N::bf>(a1, b0, wacc[OFF + 4 * k + 2]);
+          wacc[OFF + 4 * k + 3] = mfma32x32x16<N::bf>(a1, b1, wacc[OFF + 4 * k + 3]);
         }
       } else {
         constexpr int WOB = Gm::wob(l);
@@ -425,7 +425,7 @@ struct BwdWave {
           const int t = wid + k * NW;
           if (Gm::tiles(l) % NW == 0 || t < Gm::tiles(l))
             wacc[OFF + k] =
-                mfma32x32x16(xread<FA>(ta, 32 * (t / WOB), kk), xread<FZ>(tz, 32 * (t % WOB), kk), wacc[OFF + k]);
+                mfma32x32x16<N::bf>(xread<FA>(ta, 32 * (t / WOB), kk), xread<FZ>(tz, 32 * (t % WOB), kk), wacc[OFF + k]);
         }
       }
     }
@@ -453,7 +453,7 @@ struct BwdWave {
       f16x8 as[KSA];
 #pragma unroll
       for (int s = 0; s < KSA; ++s)
-        as[s] = pack8(hbuf[B][s][0], hbuf[B][s][1], hbuf[B][s][2], hbuf[B][s][3], hbuf[B][s][4], hbuf[B][s][5],
+        as[s] = pack8<N::bf>(hbuf[B][s][0], hbuf[B][s][1], hbuf[B][s][2], hbuf[B][s][3], hbuf[B][s][4], hbuf[B][s][5],
                       hbuf[B][s][6], hbuf[B][s][7]);
       xwrite<FA>(ta, as);
     } else {
@@ -468,7 +468,7 @@ struct BwdWave {
         const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSZ * 1024));
         f32x16 acc = {};
 #pragma unroll
-        for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16(frag[s * 64], dz[s], acc);
+        for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16<N::bf>(frag[s * 64], dz[s], acc);
         // Registers 0..7: features 32mb + 8g + [0..7] (K-step 2mb of a_l);
         // 8..15: 32mb + 16 + 8g + [0..7] (K-step 2mb + 1).
         if constexpr (HA) {
@@ -478,8 +478,8 @@ struct BwdWave {
             v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[B][2 * mb][j] * kLog2e));
             v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[B][2 * mb + 1][j] * kLog2e));
           }
-          const f16x8 lo = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-          const f16x8 hi = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+          const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+          const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
           if constexpr (l >= 1) {
             dzn[2 * mb] = lo;
             dzn[2 * mb + 1] = hi;
@@ -495,9 +495,9 @@ struct BwdWave {
           const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
           const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
           if (!N::gen || 32 * mb < D)
-            buf_store16(pack8(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
+            buf_store16(pack8<N::bf>(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
           if (!N::gen || 32 * mb + 16 < D)
-            buf_store16(pack8(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
+            buf_store16(pack8<N::bf>(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
                         e * 2 + 32);
         }
       }
@@ -558,7 +558,7 @@ struct BwdWave {
     f16x8 bop[KSI];
 #pragma unroll
     for (int s = 0; s < KSI; ++s)
-      bop[s] = pack8(hbuf[0][s][0] * sc, hbuf[0][s][1] * sc, hbuf[0][s][2] * sc, hbuf[0][s][3] * sc,
+      bop[s] = pack8<N::bf>(hbuf[0][s][0] * sc, hbuf[0][s][1] * sc, hbuf[0][s][2] * sc, hbuf[0][s][3] * sc,
                      hbuf[0][s][4] * sc, hbuf[0][s][5] * sc, hbuf[0][s][6] * sc, hbuf[0][s][7] * sc);
     const int fbase = (Gm::ndfrag() * 64 + lane) * 16;
     const char* wb = reinterpret_cast<const char*>(wfr);
@@ -573,7 +573,7 @@ struct BwdWave {
         const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSI * 1024));
         f32x16 a = {};
 #pragma unroll
-        for (int s = 0; s < KSI; ++s) a = mfma32x32x16(frag[s * 64], bop[s], a);
+        for (int s = 0; s < KSI; ++s) a = mfma32x32x16<N::bf>(frag[s * 64], bop[s], a);
         acc[mb & 1] = a;
       }
       if (mb > 0) {
@@ -597,7 +597,7 @@ struct BwdWave {
     for (int s = 0; s < KSI; ++s)
 #pragma unroll
       for (int j = 0; j < 8; j += 2) m = fmaxf(m, fmaxf(hbuf[0][s][j], hbuf[0][s][j + 1]));
-    if (__builtin_amdgcn_ballot_w64(m * kLog2e > 65504.0f) != 0)
+    if (!N::bf && __builtin_amdgcn_ballot_w64(m * kLog2e > 65504.0f) != 0)  // bf16 has fp32's range
       recompute_t<true>();
     else
       recompute_t<false>();
@@ -945,20 +945,32 @@ static bool bwd_exact_shape(int L, const int* dims) {
   return bdims_match<BNet3L128>(L, dims) || bdims_match<BNet5L128>(L, dims) || bdims_match<BNetNarrow>(L, dims);
 }
 
-int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
+// B: bf16 tensors (every shape is instantiated for both element formats; the
+// grids, and so the workspace sizes, are taken from the kernels that run).
+template <bool B>
+static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
+  typedef typename ElemNet<B, BNet3L128>::type N3;
+  typedef typename ElemNet<B, BNet2L128>::type N2;
+  typedef typename ElemNet<B, BNetNarrow>::type NN;
+  typedef typename ElemNet<B, GBNet2>::type G2;
+  typedef typename ElemNet<B, GBNet3>::type G3;
   const int64_t we = weight_elems_of(L, dims);
-  if (bdims_match<BNet3L128>(L, dims)) return bwd_workspace_any<BNet3L128, 4>(M, dx, we, bytes);
-  if (bdims_match<BNet5L128>(L, dims)) return bwd_split_workspace<BNet3L128, BNet2L128>(L, dims, M, dx, bytes);
-  if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<BNetNarrow, 4>(M, dx, we, bytes);
+  if (bdims_match<BNet3L128>(L, dims)) return bwd_workspace_any<N3, 4>(M, dx, we, bytes);
+  if (bdims_match<BNet5L128>(L, dims)) return bwd_split_workspace<N3, N2>(L, dims, M, dx, bytes);
+  if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<NN, 4>(M, dx, we, bytes);
   if (bwd_generic_dims(L, dims)) {
     switch (L) {
-      case 2: return bwd_workspace_any<GBNet2, 4>(M, dx, we, bytes);
-      case 3: return bwd_workspace_any<GBNet3, 4>(M, dx, we, bytes);
-      case 4: return bwd_split_workspace<GBNet2, GBNet2>(L, dims, M, dx, bytes);
-      default: return bwd_split_workspace<GBNet3, GBNet2>(L, dims, M, dx, bytes);
+      case 2: return bwd_workspace_any<G2, 4>(M, dx, we, bytes);
+      case 3: return bwd_workspace_any<G3, 4>(M, dx, we, bytes);
+      case 4: return bwd_split_workspace<G2, G2>(L, dims, M, dx, bytes);
+      default: return bwd_split_workspace<G3, G2>(L, dims, M, dx, bytes);
     }
   }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+}
+
+int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, bool bf, int64_t* bytes) {
+  return bf ? bwd_workspace_t<true>(L, dims, M, dx, bytes) : bwd_workspace_t<false>(L, dims, M, dx, bytes);
 }
 
 bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims); }
@@ -967,27 +979,37 @@ bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims
 // stash for h_2 (the forward then writes only h_1) the backward recomputes
 // h_2 from h_1 at the start of every round; no dx in that mode (the W_2
 // forward fragments take the LDS that dx's W_1 dgrad fragments would need).
-typedef Recompute<BNet3L128> RBNet3L128;
-
+// Its grid equals the stashing no-dx kernel's (one 160 KiB workgroup per CU
+// against one 128 KiB one), so the workspace size is that kernel's.
 bool bwd_recompute_supported(int L, const int* dims) { return bdims_match<BNet3L128>(L, dims); }
 
-int bwd_dispatch(int L, const int* dims, const BwdParams& p, hipStream_t st) {
+template <bool B>
+static int bwd_dispatch_t(int L, const int* dims, const BwdParams& p, hipStream_t st) {
+  typedef typename ElemNet<B, BNet3L128>::type N3;
+  typedef typename ElemNet<B, BNet2L128>::type N2;
+  typedef typename ElemNet<B, BNetNarrow>::type NN;
+  typedef typename ElemNet<B, GBNet2>::type G2;
+  typedef typename ElemNet<B, GBNet3>::type G3;
   if (bdims_match<BNet3L128>(L, dims) && !p.stash[1]) {
     if (p.dx) return fail(MLPMK_ERR_INVALID_ARG, "recomputing h_2 (stash[1] == NULL) has no dx");
-    return launch_bwd<RBNet3L128, 4, false>(p, st);
+    return launch_bwd<Recompute<N3>, 4, false>(p, st);
   }
-  if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<BNet3L128, 4>(p, st);
-  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<BNet3L128, BNet2L128>(p, L, st);
-  if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<BNetNarrow, 4>(p, st);
+  if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<N3, 4>(p, st);
+  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<N3, N2>(p, L, st);
+  if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<NN, 4>(p, st);
   if (bwd_generic_dims(L, dims)) {
     switch (L) {
-      case 2: return launch_bwd_any<GBNet2, 4>(p, st);
-      case 3: return launch_bwd_any<GBNet3, 4>(p, st);
-      case 4: return launch_bwd_split<GBNet2, GBNet2>(p, L, st);
-      default: return launch_bwd_split<GBNet3, GBNet2>(p, L, st);
+      case 2: return launch_bwd_any<G2, 4>(p, st);
+      case 3: return launch_bwd_any<G3, 4>(p, st);
+      case 4: return launch_bwd_split<G2, G2>(p, L, st);
+      default: return launch_bwd_split<G3, G2>(p, L, st);
     }
   }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+}
+
+int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st) {
+  return bf ? bwd_dispatch_t<true>(L, dims, p, st) : bwd_dispatch_t<false>(L, dims, p, st);
 }
 
 }  // namespace mlpmk

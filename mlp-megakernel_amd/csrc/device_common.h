@@ -27,6 +27,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
@@ -68,8 +71,31 @@ constexpr float kLn2 = 0.69314718055994531f;
 
 constexpr int kMaxLayers = 8;
 
+// Element format of the 16-bit tensors (x, W, out, dout, dx): fp16, or bf16
+// when BF.  Kernels carry either as 16-bit payloads in f16 vectors and
+// interpret them only in the helpers taking BF: the MFMA, the conversions
+// from fp32 (RNE) and the overflow tracking of packed activations.
+template <bool BF = false>
 __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+template <bool BF = false>
+__device__ __forceinline__ float elem_to_f32(f16 v) {
+  if constexpr (BF)
+    return (float)__builtin_bit_cast(__bf16, v);
+  else
+    return (float)v;
+}
+template <bool BF = false>
+__device__ __forceinline__ f16 f32_to_elem(float v) {
+  if constexpr (BF)
+    return __builtin_bit_cast(f16, (__bf16)v);
+  else
+    return (f16)v;
 }
 
 // Output-feature permutation of an MFMA row block.  Row i = 8a + 4g + b of
@@ -98,8 +124,17 @@ __device__ __forceinline__ float sp2(float u) {
 // Replaces an overflowed sp2 by u (u >= 128); every other value is kept as is.
 __device__ __forceinline__ float sp2_fix(float u, float s) { return u >= 128.0f ? u : s; }
 
+template <bool BF = false>
 __device__ __forceinline__ f16x2 cvt2(float a, float b) {
-  return __builtin_convertvector((f32x2){a, b}, f16x2);  // v_cvt_pk_f16_f32 (RNE)
+  if constexpr (BF) {
+    f16x2 r = __builtin_bit_cast(f16x2, __builtin_convertvector((f32x2){a, b}, bf16x2));  // v_cvt_pk_bf16_f32
+    // An empty statement that takes the packed pair as is: without it the
+    // compiler re-derived some pairs read as fp16 (the overflow tracking)
+    // from two single conversions and a repack, which spilled.
+    asm("" : "+v"(r));
+    return r;
+  } else
+    return __builtin_convertvector((f32x2){a, b}, f16x2);  // v_cvt_pk_f16_f32 (RNE)
 }
 
 // A staged weight: w * sc rounded to fp32, then to fp16 (RNE both times).  The
@@ -108,15 +143,17 @@ __device__ __forceinline__ f16x2 cvt2(float a, float b) {
 // the two roundings differ by one fp16 ulp for a few weights, and every
 // kernel (any launch shape, inference or training forward) must stage the
 // same bits.
+template <bool BF = false>
 __device__ __forceinline__ f16 scaled_weight(f16 w, float sc) {
-  float t = (float)w * sc;
+  float t = elem_to_f32<BF>(w) * sc;
   asm volatile("" : "+v"(t));
-  return (f16)t;
+  return f32_to_elem<BF>(t);
 }
 
+template <bool BF = false>
 __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, float a4, float a5,
                                        float a6, float a7) {
-  f16x2 p0 = cvt2(a0, a1), p1 = cvt2(a2, a3), p2 = cvt2(a4, a5), p3 = cvt2(a6, a7);
+  f16x2 p0 = cvt2<BF>(a0, a1), p1 = cvt2<BF>(a2, a3), p2 = cvt2<BF>(a4, a5), p3 = cvt2<BF>(a6, a7);
   f16x4 q0 = __builtin_shufflevector(p0, p1, 0, 1, 2, 3);
   f16x4 q1 = __builtin_shufflevector(p2, p3, 0, 1, 2, 3);
   return __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -126,6 +163,11 @@ __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, f
 // CHAIN: max(max(m, a), b) folds into one v_pk_maximum3_f16 per two packed
 // values (4 per call); the pairwise tree costs ~6 per call but leaves the
 // scheduler more freedom, which the stash kernels need to stay spill-free.
+// The same code tracks bf16 payloads: read as fp16, a non-negative bf16
+// pattern orders like its value below 0x7C00 (finite positive fp16), every
+// larger pattern reads as fp16 inf or NaN, which the maximum keeps, and a
+// negative one (only -0 or a NaN can occur: sp2 >= 0) is a negative fp16 or
+// a NaN.  Only the threshold in sp2_overflowed differs.
 template <bool CHAIN>
 __device__ __forceinline__ f16x2 sp2_track(f16x2 m, f16x8 lo, f16x8 hi) {
   if constexpr (CHAIN) {
@@ -144,9 +186,13 @@ __device__ __forceinline__ f16x2 sp2_track(f16x2 m, f16x8 lo, f16x8 hi) {
 // 128.  A finite sp2 below 2^7 rounds to at most 128 in fp16, so this catches
 // every overflow (+inf) -- and every NaN, which the exact path reproduces
 // unchanged.
+// bf16 payloads (BF): 128.0 is the pattern 0x4300, which reads as fp16 3.5;
+// likewise a finite sp2 below 2^7 rounds to at most that pattern.
+template <bool BF = false>
 __device__ __forceinline__ bool sp2_overflowed(f16x2 m) {
   const f16 m1 = __builtin_elementwise_maximum(m.x, m.y);
-  return __builtin_amdgcn_ballot_w64(!(m1 < (f16)128.0f)) != 0;
+  const f16 thr = BF ? __builtin_bit_cast(f16, (unsigned short)0x4300) : (f16)128.0f;
+  return __builtin_amdgcn_ballot_w64(!(m1 < thr)) != 0;
 }
 
 // An opaque copy of a wave-uniform offset.  Weight fragments never change
@@ -164,6 +210,7 @@ template <int... Ds>
 struct Net {
   static constexpr bool gen = false;  // widths fixed at compile time
   static constexpr bool rc = false;   // backward: h_{L-1} read from the stash (see Recompute in bwd.hip)
+  static constexpr bool bf = false;   // 16-bit tensors are fp16 (see BF16)
   static constexpr int L = sizeof...(Ds) - 1;
   static constexpr int d[sizeof...(Ds)] = {Ds...};
   // K-steps (16 input features each) and 32-row output blocks of layer l.
@@ -202,6 +249,21 @@ struct Net {
 template <class Base>
 struct Gen : Base {
   static constexpr bool gen = true;
+};
+
+// The same network with bf16 tensors (x, W, out, dout, dx) and bf16 MFMA
+// operands; accumulation, softplus and the stash stay fp32.
+template <class Base>
+struct BF16 : Base {
+  static constexpr bool bf = true;
+};
+template <bool B, class N>
+struct ElemNet {
+  typedef N type;
+};
+template <class N>
+struct ElemNet<true, N> {
+  typedef BF16<N> type;
 };
 
 }  // namespace mlpmk

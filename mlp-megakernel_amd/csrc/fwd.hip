@@ -65,9 +65,9 @@ __device__ __forceinline__ f16x8 weight_fragment(const FwdParams& p, int l, int 
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (N::gen)
-        v[j] = k0 + j < p.dims[l] ? scaled_weight(src[(int64_t)j * Nout], wscale<N>(l)) : (f16)0.0f;
+        v[j] = k0 + j < p.dims[l] ? scaled_weight<N::bf>(src[(int64_t)j * Nout], wscale<N>(l)) : (f16)0.0f;
       else
-        v[j] = scaled_weight(src[(int64_t)j * Nout], wscale<N>(l));
+        v[j] = scaled_weight<N::bf>(src[(int64_t)j * Nout], wscale<N>(l));
     }
   } else {
 #pragma unroll
@@ -126,7 +126,7 @@ __device__ __forceinline__ void stage_store(f16x8* lds, const f16x8 (&r)[8], int
     const int i = ibase + 8 * (q >> 2) + (q & 3);
     f16x8 v;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = scaled_weight(r[j][q], sc);
+    for (int j = 0; j < 8; ++j) v[j] = scaled_weight<N::bf>(r[j][q], sc);
     lds[(f - RF) * 64 + 32 * g + i] = v;
   }
 }
@@ -366,7 +366,7 @@ __device__ __forceinline__ void chain(f32x16 (&acc)[NB], Frags<KSM>& f, const T 
 #pragma unroll
   for (int s = S0; s < S1; ++s) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16(f.a[s], as_f16x8(in[s][nb]), acc[nb]);
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32x32x16<N::bf>(f.a[s], as_f16x8(in[s][nb]), acc[nb]);
     if (s < KSN) f.a[s] = frag<N, TN, RF>(s, fb, rf);
   }
 }
@@ -399,17 +399,17 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       const int row = nb * 32 + n;
       const int c = 4 * (mb & 1) + g;  // chunk within the staged 128-byte row segment
       io.stage[stage_slot(row, c)] =
-          __builtin_bit_cast(i32x4, pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]));
+          __builtin_bit_cast(i32x4, pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]));
       io.stage[stage_slot(row, c + 2)] =
-          __builtin_bit_cast(i32x4, pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]));
+          __builtin_bit_cast(i32x4, pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]));
     } else if constexpr (LAST && N::gen) {
       // Runtime output width OW: whole 8-feature pieces when OW is a multiple
       // of 8, else one 2-byte store per feature; features past OW are dropped.
       const f32x16 v = acc[nb] * kIn;
       const int OW = io.dl[N::L], c = 32 * mb + 8 * g;
       const uint32_t e = (uint32_t)((nb * 32 + n) * OW + c);
-      const f16x8 lo = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-      const f16x8 hi = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+      const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+      const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
       if (OW % 8 == 0) {
         if (c < OW) buf_store16<kStreamStore>(lo, io.out, e * 2);
         if (c + 16 < OW) buf_store16<kStreamStore>(hi, io.out, e * 2 + 32);
@@ -419,18 +419,18 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           if (c + j < OW)
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)v[j]), io.out,
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, f32_to_elem<N::bf>(v[j])), io.out,
                                                   (int)((e + j) * 2), 0, kStreamStore);
           if (c + 16 + j < OW)
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)v[8 + j]), io.out,
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, f32_to_elem<N::bf>(v[8 + j])), io.out,
                                                   (int)((e + 16 + j) * 2), 0, kStreamStore);
         }
       }
     } else if constexpr (LAST) {
       const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
-      if (lo_ok) buf_store16<kStreamStore>(pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
+      if (lo_ok) buf_store16<kStreamStore>(pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
       if (hi_ok)
-        buf_store16<kStreamStore>(pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
+        buf_store16<kStreamStore>(pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
     } else {
       // log2 e is folded into the staged W_1, so acc is u in base-2 units.
       const f32x16 u = acc[nb] * kIn;
@@ -440,8 +440,8 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
         s[e] = EXACT ? sp2_fix(u[e], sp2(u[e])) : sp2(u[e]);
         q[e] = EXACT ? 0.5f * s[e] : s[e];
       }
-      const f16x8 lo = pack8(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
-      const f16x8 hi = pack8(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
+      const f16x8 lo = pack8<N::bf>(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
+      const f16x8 hi = pack8<N::bf>(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
       if constexpr (!EXACT) m = sp2_track<!STASH>(m, lo, hi);
       if constexpr (STASH && N::gen) {
         // Runtime hidden width HW (a multiple of 16): feature groups past it are dropped.
@@ -589,7 +589,7 @@ __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>&
   chain<N, T1, RF, 0, N::ks(0), NB>(c.acc[0], c.fr, c.xa, fb, c.rf);
   load_frags<N, T1, KSM, RF, N::ks(0)>(c.fr, fb, c.rf);
   step<N, 0, NB, STASH, STAGE, EXACT, KSM, RF>(p, io, c, fb, next, lane);
-  return !EXACT && sp2_overflowed(c.ovf);
+  return !EXACT && sp2_overflowed<N::bf>(c.ovf);
 }
 
 // Block b with the fast softplus form, then -- only if one of its wave's sp2
@@ -792,31 +792,40 @@ bool fwd_supported_dims(int L, const int* dims) {
          dims_match<NetNarrow>(L, dims) || fwd_generic_dims(L, dims);
 }
 
-int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus);
+int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus);
 
-int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
-  int cus = 0;
-  const int rc = current_device_cus(&cus);
-  if (rc != MLPMK_OK) return rc;
-  // Small batches run the feature-split kernel (fwd_split.hip) when it has one
-  // for these widths and batch size.
-  const int rs = fwd_split_dispatch(L, dims, p, stash, st, cus);
-  if (rs != MLPMK_ERR_UNSUPPORTED_SHAPE) return rs;
-  if (dims_match<Net3L128>(L, dims)) return launch_fwd_any<Net3L128, 1, 12, 1, 8, 1>(p, stash, st);
-  if (dims_match<Net5L128>(L, dims)) return launch_fwd_any<Net5L128, 1, 12, 1, 8, 1>(p, stash, st);
-  if (dims_match<NetNarrow>(L, dims)) return launch_fwd_any<NetNarrow, 2, 16, 1, 16, 1>(p, stash, st);
+// B: bf16 tensors (every shape is instantiated for both element formats).
+template <bool B>
+static int fwd_dispatch_t(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
+  if (dims_match<Net3L128>(L, dims))
+    return launch_fwd_any<typename ElemNet<B, Net3L128>::type, 1, 12, 1, 8, 1>(p, stash, st);
+  if (dims_match<Net5L128>(L, dims))
+    return launch_fwd_any<typename ElemNet<B, Net5L128>::type, 1, 12, 1, 8, 1>(p, stash, st);
+  if (dims_match<NetNarrow>(L, dims))
+    return launch_fwd_any<typename ElemNet<B, NetNarrow>::type, 2, 16, 1, 16, 1>(p, stash, st);
   if (fwd_generic_dims(L, dims)) {
     switch (L) {
       // At most 8 waves (4 for the 5-layer stash kernel): the runtime
       // strides cannot fold into immediate offsets, and the 12-wave kernels
       // (168 VGPRs) spill.
-      case 2: return launch_fwd_any<GNet2, 1, 8, 1, 8, 1>(p, stash, st);
-      case 3: return launch_fwd_any<GNet3, 1, 8, 1, 8, 1>(p, stash, st);
-      case 4: return launch_fwd_any<GNet4, 1, 8, 1, 8, 1>(p, stash, st);
-      default: return launch_fwd_any<GNet5, 1, 8, 1, 4, 1>(p, stash, st);
+      case 2: return launch_fwd_any<typename ElemNet<B, GNet2>::type, 1, 8, 1, 8, 1>(p, stash, st);
+      case 3: return launch_fwd_any<typename ElemNet<B, GNet3>::type, 1, 8, 1, 8, 1>(p, stash, st);
+      case 4: return launch_fwd_any<typename ElemNet<B, GNet4>::type, 1, 8, 1, 8, 1>(p, stash, st);
+      default: return launch_fwd_any<typename ElemNet<B, GNet5>::type, 1, 8, 1, 4, 1>(p, stash, st);
     }
   }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
+}
+
+int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st) {
+  int cus = 0;
+  const int rc = current_device_cus(&cus);
+  if (rc != MLPMK_OK) return rc;
+  // Small batches run the feature-split kernel (fwd_split.hip) when it has one
+  // for these widths and batch size.
+  const int rs = fwd_split_dispatch(L, dims, p, stash, bf, st, cus);
+  if (rs != MLPMK_ERR_UNSUPPORTED_SHAPE) return rs;
+  return bf ? fwd_dispatch_t<true>(L, dims, p, stash, st) : fwd_dispatch_t<false>(L, dims, p, stash, st);
 }
 
 }  // namespace mlpmk

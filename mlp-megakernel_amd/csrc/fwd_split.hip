@@ -125,7 +125,7 @@ __device__ __forceinline__ void frag_build(f16x8 (&fr)[N::ksmax()], const f16x8 
       const int i = ibase + 8 * (q >> 2) + (q & 3);
       f16x8 v;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = scaled_weight(r[j][q], sc);
+      for (int j = 0; j < 8; ++j) v[j] = scaled_weight<N::bf>(r[j][q], sc);
       scratch[s * 64 + 32 * g + i] = v;
     }
   }
@@ -225,14 +225,14 @@ __device__ __forceinline__ void layer(const FwdParams& p, const Frags<N>& f, con
   for (int s = 0; s < KS; ++s) bv[s] = __builtin_bit_cast(f16x8, tin[slot<CH>(n, 2 * s + g)]);
   f32x16 acc = {};
 #pragma unroll
-  for (int s = 0; s < KS; ++s) acc = mfma32x32x16(f.fr[l][s], bv[s], acc);
+  for (int s = 0; s < KS; ++s) acc = mfma32x32x16<N::bf>(f.fr[l][s], bv[s], acc);
   constexpr float kIn = (EXACT && l > 0) ? 2.0f : 1.0f;
   const bool lo_ok = 32 * w + 16 <= Nout, hi_ok = 32 * w + 32 <= Nout;
   const uint32_t elem = (uint32_t)(n * Nout + 32 * w + 8 * g);
   if constexpr (LAST) {
     const f32x16 v = acc * kIn;  // ln 2 is folded into the staged W_L
-    const f16x8 lo = pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-    const f16x8 hi = pack8(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+    const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+    const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
     if constexpr (G::STAGE_OUT) {
       tout[slot<CH>(n, 4 * w + g)] = __builtin_bit_cast(i32x4, lo);
       tout[slot<CH>(n, 4 * w + 2 + g)] = __builtin_bit_cast(i32x4, hi);
@@ -249,8 +249,8 @@ __device__ __forceinline__ void layer(const FwdParams& p, const Frags<N>& f, con
       s[e] = EXACT ? sp2_fix(u[e], sp2(u[e])) : sp2(u[e]);
       q[e] = EXACT ? 0.5f * s[e] : s[e];
     }
-    const f16x8 lo = pack8(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
-    const f16x8 hi = pack8(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
+    const f16x8 lo = pack8<N::bf>(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
+    const f16x8 hi = pack8<N::bf>(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
     if constexpr (!EXACT) m = sp2_track<true>(m, lo, hi);
     if constexpr (STASH) {
       const rsrc_t sr = p.stash[l] ? make_rsrc(p.stash[l] + row0 * Nout, rows * Nout * 4u)
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(Geo<N>::NWV * 64) void fwd_split_kernel(FwdParams p
     if (threadIdx.x == 0) redo[par ^ 1] = 0;
     f16x2 m = f16x2{};
     layers<N, STASH, false>(p, f, tiles, row0, rows, w, n, g, m);
-    if (sp2_overflowed(m) && lane == 0) redo[par] = 1;
+    if (sp2_overflowed<N::bf>(m) && lane == 0) redo[par] = 1;
     __syncthreads();
     if (__builtin_expect(redo[par] != 0, 0)) {
       // Exact recompute by the whole workgroup (the flag is the same for all
@@ -424,15 +424,21 @@ static int split_if_small(const FwdParams& p, bool stash, hipStream_t st, int cu
 
 // Launches the feature-split kernel when one exists for these widths and the
 // batch is small enough; otherwise returns MLPMK_ERR_UNSUPPORTED_SHAPE without
-// recording an error, and the caller runs fwd.hip's kernels.
-int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus) {
+// recording an error, and the caller runs fwd.hip's kernels.  B: bf16 tensors.
+template <bool B>
+static int fwd_split_dispatch_t(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus) {
   if (split_dims_match<SNet3L128>(L, dims))
-    return split_if_small<SNet3L128>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU_3L);
+    return split_if_small<typename ElemNet<B, SNet3L128>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU_3L);
   if (split_dims_match<SNet5L128>(L, dims))
-    return split_if_small<SNet5L128>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU);
+    return split_if_small<typename ElemNet<B, SNet5L128>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU);
   if (split_dims_match<SNetNarrow>(L, dims))
-    return split_if_small<SNetNarrow>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU);
+    return split_if_small<typename ElemNet<B, SNetNarrow>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU);
   return MLPMK_ERR_UNSUPPORTED_SHAPE;
+}
+
+int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus) {
+  return bf ? fwd_split_dispatch_t<true>(L, dims, p, stash, st, cus)
+            : fwd_split_dispatch_t<false>(L, dims, p, stash, st, cus);
 }
 
 }  // namespace mlpmk

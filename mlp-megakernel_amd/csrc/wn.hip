@@ -57,9 +57,10 @@ __device__ __forceinline__ float wn_colsum(float part, float (&red)[kWnRowGroups
 // loop over chunks.
 constexpr int kWnRegRows = 16;
 
-template <class P>
+// P: parameter type (float, fp16 or bf16); O: element type of W (fp16 or bf16).
+template <class P, class O>
 __global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const P* __restrict__ v,
-                                                            const P* __restrict__ g, f16* __restrict__ w,
+                                                            const P* __restrict__ g, O* __restrict__ w,
                                                             float* __restrict__ inv_norm) {
   __shared__ float red[kWnRowGroups][kWnCols];
   const int l = wn_layer_of(lay, blockIdx.x);
@@ -88,12 +89,12 @@ __global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const 
 #pragma unroll
     for (int i = 0; i < kWnRegRows; ++i) {
       const int k = rg + i * kWnRowGroups;
-      if (k < K) w[base + (int64_t)k * N] = (f16)(t[i] * scale);
+      if (k < K) w[base + (int64_t)k * N] = (O)(t[i] * scale);
     }
   } else {
     for (int k = rg; k < K; k += kWnRowGroups) {
       const int64_t e = base + (int64_t)k * N;
-      w[e] = (f16)(ldp(v, e) * scale);
+      w[e] = (O)(ldp(v, e) * scale);
     }
   }
   if (rg == 0) inv_norm[lay.g_off[l] + j] = inv;
@@ -166,7 +167,23 @@ static int wn_layout(int L, const int* dims, WnLayout* lay) {
   return MLPMK_OK;
 }
 
-int wn_fwd_dispatch(int L, const int* dims, int dtype, const void* v, const void* g, void* w_out,
+template <class P, class O>
+static void launch_wn_fwd(const WnLayout& lay, const void* v, const void* g, void* w_out, float* inv_norm,
+                          hipStream_t st) {
+  hipLaunchKernelGGL((wn_fwd_kernel<P, O>), dim3(lay.blk_off[lay.L]), dim3(kWnThreads), 0, st, lay,
+                     (const P*)v, (const P*)g, (O*)w_out, inv_norm);
+}
+
+template <class P>
+static void launch_wn_fwd_p(const WnLayout& lay, int w_dtype, const void* v, const void* g, void* w_out,
+                            float* inv_norm, hipStream_t st) {
+  if (w_dtype == MLPMK_DTYPE_BF16)
+    launch_wn_fwd<P, __bf16>(lay, v, g, w_out, inv_norm, st);
+  else
+    launch_wn_fwd<P, f16>(lay, v, g, w_out, inv_norm, st);
+}
+
+int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* v, const void* g, void* w_out,
                     float* inv_norm, hipStream_t st) {
   WnLayout lay;
   int rc = wn_layout(L, dims, &lay);
@@ -175,11 +192,11 @@ int wn_fwd_dispatch(int L, const int* dims, int dtype, const void* v, const void
   if ((rc = current_device_cus(&cus))) return rc;
   (void)hipGetLastError();
   if (dtype == MLPMK_DTYPE_F32)
-    hipLaunchKernelGGL(wn_fwd_kernel<float>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay,
-                       (const float*)v, (const float*)g, (f16*)w_out, inv_norm);
+    launch_wn_fwd_p<float>(lay, w_dtype, v, g, w_out, inv_norm, st);
+  else if (dtype == MLPMK_DTYPE_BF16)
+    launch_wn_fwd_p<__bf16>(lay, w_dtype, v, g, w_out, inv_norm, st);
   else
-    hipLaunchKernelGGL(wn_fwd_kernel<f16>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay,
-                       (const f16*)v, (const f16*)g, (f16*)w_out, inv_norm);
+    launch_wn_fwd_p<f16>(lay, w_dtype, v, g, w_out, inv_norm, st);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? MLPMK_OK : hip_fail(e, "wn_fwd kernel launch");
 }
@@ -195,6 +212,9 @@ int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const vo
   if (dtype == MLPMK_DTYPE_F32)
     hipLaunchKernelGGL(wn_bwd_kernel<float>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay, dw,
                        (const float*)v, (const float*)g, inv_norm, (float*)dv, (float*)dg);
+  else if (dtype == MLPMK_DTYPE_BF16)
+    hipLaunchKernelGGL(wn_bwd_kernel<__bf16>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay, dw,
+                       (const __bf16*)v, (const __bf16*)g, inv_norm, (__bf16*)dv, (__bf16*)dg);
   else
     hipLaunchKernelGGL(wn_bwd_kernel<f16>, dim3(lay.blk_off[L]), dim3(kWnThreads), 0, st, lay, dw,
                        (const f16*)v, (const f16*)g, inv_norm, (f16*)dv, (f16*)dg);

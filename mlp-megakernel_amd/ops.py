@@ -63,6 +63,17 @@ def bwd_recompute_supported(dims):
     return bool(lib.mlpmk_bwd_recompute_supported(len(dims) - 1, p))
 
 
+# Element types of the megakernels' 16-bit tensors (x, weights, out, dout, dx).
+_ELEM = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _elem_code(dtype, name="x"):
+    code = _ELEM.get(dtype)
+    if code is None:
+        raise TypeError(f"{name} must be float16 or bfloat16, got {dtype} (cast first: fp32 accumulation either way)")
+    return code
+
+
 def _require(t, name, dtype, device):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
@@ -99,22 +110,23 @@ def _launch(device, fn, *args):
 def fwd_into(x, weights, out, stash=None):
     """Run the forward megakernel writing ``out`` (and ``stash`` if given).
 
-    ``x`` [M, D] fp16, ``weights`` list of [in, out] fp16, ``out`` [M, OUT]
-    fp16, ``stash`` list of L-1 fp32 [M, H_l] tensors (an entry may be None:
+    ``x`` [M, D] fp16 or bf16, ``weights`` list of [in, out] and ``out``
+    [M, OUT] of x's dtype, ``stash`` list of L-1 fp32 [M, H_l] tensors (an entry may be None:
     that activation is not written) or None.  All contiguous on one CUDA
     (HIP) device.
     """
     dev = x.device
     if dev.type != "cuda":
         raise ValueError(f"x must be on a GPU device, got {dev}")
-    _require(x, "x", torch.float16, dev)
+    code = _elem_code(x.dtype)
+    _require(x, "x", x.dtype, dev)
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
     for i, w in enumerate(weights):
-        _require(w, f"w{i + 1}", torch.float16, dev)
+        _require(w, f"w{i + 1}", x.dtype, dev)
     dims = _dims_of(x, weights)
     M = int(x.shape[0])
-    _require(out, "out", torch.float16, dev)
+    _require(out, "out", x.dtype, dev)
     if tuple(out.shape) != (M, dims[-1]):
         raise ValueError(f"out has shape {tuple(out.shape)}, expected {(M, dims[-1])}")
     stash_ptrs = None
@@ -132,7 +144,7 @@ def fwd_into(x, weights, out, stash=None):
     pd, _k1 = _lib.int_array(dims)
     pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
     ps, _k3 = (_lib.ptr_array(stash_ptrs) if stash_ptrs is not None else (None, None))
-    rc = _launch(dev, lib.mlpmk_fwd, len(weights), pd, x.data_ptr(), pw, out.data_ptr(), ps, M)
+    rc = _launch(dev, lib.mlpmk_fwd, len(weights), pd, code, x.data_ptr(), pw, out.data_ptr(), ps, M)
     _check("mlpmk_fwd", rc)
     return out
 
@@ -146,7 +158,7 @@ def fwd(x, weights, stash=False, recompute=False):
     """
     dims = _dims_of(x, weights)
     M = int(x.shape[0])
-    out = torch.empty((M, dims[-1]), device=x.device, dtype=torch.float16)
+    out = torch.empty((M, dims[-1]), device=x.device, dtype=x.dtype)
     hs = None
     if stash:
         hs = [torch.empty((M, d), device=x.device, dtype=torch.float32) for d in dims[1:-1]]
@@ -159,18 +171,19 @@ def fwd(x, weights, stash=False, recompute=False):
 _ws_bytes = {}
 
 
-def bwd_workspace_bytes(dims, M, with_dx, device=None):
+def bwd_workspace_bytes(dims, M, with_dx, device=None, dtype=torch.float16):
     """Bytes of workspace ``mlpmk_bwd_ws`` needs on ``device`` (default: the
-    current device); cached per device, shape and M."""
+    current device) for tensors of ``dtype``; cached per device, shape and M."""
     idx = torch.cuda.current_device() if device is None or device.index is None else device.index
-    key = (idx, tuple(dims), int(M), bool(with_dx))
+    code = _elem_code(dtype)
+    key = (idx, tuple(dims), int(M), bool(with_dx), code)
     n = _ws_bytes.get(key)
     if n is None:
         lib = _lib.get()
         pd, _k = _lib.int_array(dims)
         out = ctypes.c_int64(0)
         with torch.cuda.device(idx):
-            rc = lib.mlpmk_bwd_workspace_size(len(dims) - 1, pd, M, int(with_dx), ctypes.byref(out))
+            rc = lib.mlpmk_bwd_workspace_size(len(dims) - 1, pd, code, M, int(with_dx), ctypes.byref(out))
         _check("mlpmk_bwd_workspace_size", rc)
         n = _ws_bytes[key] = out.value
     return n
@@ -189,9 +202,10 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     recomputing backward (``bwd_recompute_supported``; no dx).
     """
     dev = x.device
-    _require(x, "x", torch.float16, dev)
+    code = _elem_code(x.dtype)
+    _require(x, "x", x.dtype, dev)
     for i, w in enumerate(weights):
-        _require(w, f"w{i + 1}", torch.float16, dev)
+        _require(w, f"w{i + 1}", x.dtype, dev)
     dims = _dims_of(x, weights)
     M = int(x.shape[0])
     if len(stash) != len(weights) - 1:
@@ -206,19 +220,19 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
         _require(d, f"dw[{i}]", torch.float32, dev)
         if tuple(d.shape) != (dims[i], dims[i + 1]):
             raise ValueError(f"dw[{i}] has shape {tuple(d.shape)}, expected {(dims[i], dims[i + 1])}")
-    if dout.dtype != torch.float16 or dout.device != dev:
-        raise TypeError("dout must be fp16 on the same device as x")
+    if dout.dtype != x.dtype or dout.device != dev:
+        raise TypeError(f"dout must be {x.dtype} on the same device as x")
     if tuple(dout.shape) != (M, dims[-1]) or dout.stride(1) != 1:
         raise ValueError(f"dout must be [M, OUT]={M, dims[-1]} with unit column stride")
     row_stride = int(dout.stride(0)) if M > 1 else -(-dims[-1] // 8) * 8
     if row_stride % 8 != 0:
         # The library reads dout rows from 16-byte boundaries: an output width
         # that is not a multiple of 8 gets rows padded to the next multiple.
-        padded = torch.zeros((M, -(-dims[-1] // 8) * 8), dtype=torch.float16, device=dev)
+        padded = torch.zeros((M, -(-dims[-1] // 8) * 8), dtype=x.dtype, device=dev)
         padded[:, : dims[-1]] = dout
         dout, row_stride = padded, padded.shape[1]
     if dx is not None:
-        _require(dx, "dx", torch.float16, dev)
+        _require(dx, "dx", x.dtype, dev)
         if tuple(dx.shape) != (M, dims[0]):
             raise ValueError(f"dx has shape {tuple(dx.shape)}, expected {(M, dims[0])}")
     lib = _lib.get()
@@ -228,13 +242,13 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
     dxp = dx.data_ptr() if dx is not None else None
     if workspace and M > 0:
-        nbytes = bwd_workspace_bytes(dims, M, dx is not None, dev)
+        nbytes = bwd_workspace_bytes(dims, M, dx is not None, dev, x.dtype)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        rc = _launch(dev, lib.mlpmk_bwd_ws, len(weights), pd, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
+        rc = _launch(dev, lib.mlpmk_bwd_ws, len(weights), pd, code, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
                      dxp, pg, ws.data_ptr(), nbytes, M)
         _check("mlpmk_bwd_ws", rc)
     else:
-        rc = _launch(dev, lib.mlpmk_bwd, len(weights), pd, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
+        rc = _launch(dev, lib.mlpmk_bwd, len(weights), pd, code, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
                      dxp, pg, M)
         _check("mlpmk_bwd", rc)
     return dws, dx
@@ -245,7 +259,9 @@ def _param_dtype(t):
         return _lib.DTYPE_F32
     if t.dtype == torch.float16:
         return _lib.DTYPE_F16
-    raise TypeError(f"weight-norm parameters must be fp32 or fp16, got {t.dtype}")
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    raise TypeError(f"weight-norm parameters must be fp32, fp16 or bf16, got {t.dtype}")
 
 
 def wn_fwd(dims, v_all, g_all, w_all, inv_all):
@@ -254,7 +270,8 @@ def wn_fwd(dims, v_all, g_all, w_all, inv_all):
     dt = _param_dtype(v_all)
     _require(v_all, "v_all", v_all.dtype, dev)
     _require(g_all, "g_all", v_all.dtype, dev)
-    _require(w_all, "w_all", torch.float16, dev)
+    wcode = _elem_code(w_all.dtype, "w_all")
+    _require(w_all, "w_all", w_all.dtype, dev)
     _require(inv_all, "inv_all", torch.float32, dev)
     nw = sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
     ng = sum(dims[1:])
@@ -262,7 +279,7 @@ def wn_fwd(dims, v_all, g_all, w_all, inv_all):
         raise ValueError("weight-norm block sizes do not match dims")
     lib = _lib.get()
     pd, _k = _lib.int_array(dims)
-    rc = _launch(dev, lib.mlpmk_wn_fwd, len(dims) - 1, pd, dt, v_all.data_ptr(), g_all.data_ptr(),
+    rc = _launch(dev, lib.mlpmk_wn_fwd, len(dims) - 1, pd, dt, wcode, v_all.data_ptr(), g_all.data_ptr(),
                  w_all.data_ptr(), inv_all.data_ptr())
     _check("mlpmk_wn_fwd", rc)
     return w_all, inv_all

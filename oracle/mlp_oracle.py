@@ -15,7 +15,11 @@ It restates, in plain numpy, the math of the reference's eager path and of the
                               (kernel.py:168-171, profile.py:102-106) for any depth
                               (5-layer chain: README.md:9, mlp_fused.md:11)
 * ``forward`` with ``round_hidden=True`` mirrors the megakernel's fp16 re-cast of
-  every hidden activation before the next GEMM (kernel.py:110,117,121).
+  every hidden activation before the next GEMM (kernel.py:110,117,121); with
+  ``elem="bf16"`` the re-cast is to bf16, as the reference's ``.to(INPUT_DTYPE)``
+  does for a bf16 INPUT_DTYPE (mlp_fused.md:159-163).
+* ``to_bf16``             -- fp32 -> bf16 rounding (round to nearest, ties to
+                              even; NaN stays NaN), values returned as fp32.
 * ``backward``            -- closed form of mlp_fused.md:84-95:
                               ``dz_L = g``, ``dW_l = h_{l-1}^T dz_l``,
                               ``dz_{l-1} = (dz_l W_l^T) * (1 - exp(-h_{l-1}))``,
@@ -38,6 +42,8 @@ Pinning (what checks this restatement, in tests/test_oracle.py):
                W instead of W^T in the data gradient).
   wn_*      -> torch._weight_norm (library) and its autograd; invariants
                ||W[:, j]|| = |g_j|, <dv[:, j], v[:, j]> = 0.
+  to_bf16   -> torch's float32 -> bfloat16 conversion (library) on random and
+               edge values (ties, overflow to inf, NaN, subnormals).
 No function of this module is "parity unpinned".
 """
 from __future__ import annotations
@@ -61,6 +67,25 @@ def softplus(z, dtype=np.float32):
     return np.where(z > SOFTPLUS_THRESHOLD, z, lin).astype(dtype, copy=False)
 
 
+def to_bf16(a):
+    """Round fp32 values to bf16 (8 significant bits; round to nearest, ties
+    to even) and return them as fp32.  Adds 0x7FFF plus the lowest kept bit
+    to the bit pattern and clears the low 16 bits; NaNs are kept as NaNs."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(a), a, r).astype(np.float32)
+
+
+def round_elem(a, elem):
+    """``a`` rounded to the 16-bit element format ``elem`` ("f16" or "bf16"), as fp32."""
+    if elem == "bf16":
+        return to_bf16(a)
+    if elem == "f16":
+        return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+    raise ValueError(f"elem must be 'f16' or 'bf16', got {elem!r}")
+
+
 def softplus_grad_from_h(h, dtype=np.float32):
     """``softplus'(z) = sigmoid(z) = 1 - exp(-h)`` with ``h = softplus(z)``
     (mlp_fused.md:57,84).  Uses ``-expm1(-h)`` for accuracy at small ``h``."""
@@ -68,14 +93,15 @@ def softplus_grad_from_h(h, dtype=np.float32):
     return (-np.expm1(-h)).astype(dtype, copy=False)
 
 
-def forward(x, weights, *, round_hidden=False, dtype=np.float32, return_hidden=False):
+def forward(x, weights, *, round_hidden=False, dtype=np.float32, return_hidden=False, elem="f16"):
     """Eager chain ``softplus(... softplus(x @ W1) ...) @ WL`` (kernel.py:168-171).
 
     ``x`` and ``weights`` are upcast to ``dtype`` (their fp16 values are exact in
-    fp32).  With ``round_hidden`` each hidden activation is rounded to fp16 before
-    it feeds the next GEMM, as the Triton megakernel's ``.to(tl.float16)`` does
-    (kernel.py:110,117).  Returns ``out`` (and the list of hidden activations
-    ``[h1, ..., h_{L-1}]`` in ``dtype`` when ``return_hidden``).
+    fp32).  With ``round_hidden`` each hidden activation is rounded to fp16
+    (``elem="bf16"``: bf16) before it feeds the next GEMM, as the Triton
+    megakernel's ``.to(tl.float16)`` does (kernel.py:110,117).  Returns ``out``
+    (and the list of hidden activations ``[h1, ..., h_{L-1}]`` in ``dtype`` when
+    ``return_hidden``).
     """
     a = np.asarray(x).astype(dtype)
     hidden = []
@@ -87,7 +113,7 @@ def forward(x, weights, *, round_hidden=False, dtype=np.float32, return_hidden=F
             break
         h = softplus(z, dtype)
         hidden.append(h)
-        a = h.astype(np.float16).astype(dtype) if round_hidden else h
+        a = round_elem(h, elem).astype(dtype) if round_hidden else h
     if return_hidden:
         return out, hidden
     return out
@@ -154,19 +180,23 @@ CONFIGS = {
 }
 
 
-def make_inputs(dims, m, seed=0, x_dist="normal"):
+def make_inputs(dims, m, seed=0, x_dist="normal", elem="f16"):
     """fp16 ``x`` ``[m, dims[0]]`` (N(0,1) or U(-1,1)) and fp16 weights
-    ``W_l ~ N(0, 1/in)`` ``[in, out]`` from one numpy generator."""
+    ``W_l ~ N(0, 1/in)`` ``[in, out]`` from one numpy generator.  With
+    ``elem="bf16"`` the same draws rounded to bf16, as fp32 arrays (numpy has
+    no bf16 type; the values convert exactly)."""
     rng = np.random.default_rng(seed)
     if x_dist == "normal":
         x = rng.standard_normal((m, dims[0]), dtype=np.float32)
     else:
         x = rng.uniform(-1.0, 1.0, size=(m, dims[0])).astype(np.float32)
     ws = [
-        (rng.standard_normal((dims[i], dims[i + 1]), dtype=np.float32) / np.sqrt(dims[i])).astype(np.float16)
+        rng.standard_normal((dims[i], dims[i + 1]), dtype=np.float32) / np.sqrt(dims[i])
         for i in range(len(dims) - 1)
     ]
-    return x.astype(np.float16), ws
+    if elem == "bf16":
+        return to_bf16(x), [to_bf16(w) for w in ws]
+    return x.astype(np.float16), [w.astype(np.float16) for w in ws]
 
 
 def make_wn_params(dims, seed=0):

@@ -58,12 +58,12 @@ def test_forward_support_table(dims, ok):
     assert ops.bwd_supported(list(dims)) is ok
 
 
-def _fwd(dims, x=A, w=(A, A, A), out=A, stash=None, m=256):
+def _fwd(dims, x=A, w=(A, A, A), out=A, stash=None, m=256, dtype=1):
     lib = _lib.get()
     pd, _k1 = _lib.int_array(dims)
     pw, _k2 = _lib.ptr_array(list(w))
     ps, _k3 = (_lib.ptr_array(list(stash)) if stash is not None else (None, None))
-    return lib.mlpmk_fwd(len(dims) - 1, pd, x, pw, out, ps, m, None)
+    return lib.mlpmk_fwd(len(dims) - 1, pd, dtype, x, pw, out, ps, m, None)
 
 
 def test_fwd_validation_codes():
@@ -77,7 +77,12 @@ def test_fwd_validation_codes():
     assert _fwd(d, w=(A, A + 8, A)) == MISALIGNED
     assert _fwd(d, stash=(A, A + 4)) == MISALIGNED
     assert b"stash[1]" in lib.mlpmk_last_error()
-    assert lib.mlpmk_fwd(3, None, A, None, A, None, 1, None) == INVALID
+    assert lib.mlpmk_fwd(3, None, 1, A, None, A, None, 1, None) == INVALID
+    # element types: fp16 (1) and bf16 (2); fp32 (0) has no megakernel, others are invalid
+    assert _fwd(d, dtype=0) == UNSUPPORTED
+    assert b"fp32" in lib.mlpmk_last_error()
+    assert _fwd(d, dtype=7) == INVALID
+    assert _fwd(d, dtype=2, m=0) == OK
     # M == 0 succeeds without touching a device (x/out may even be NULL)
     assert _fwd(d, x=None, out=None, m=0) == OK
     # valid arguments reach the device query, which fails without a GPU; a
@@ -86,6 +91,7 @@ def test_fwd_validation_codes():
         assert _fwd(d) in (NODEV, HIPERR)
         assert lib.mlpmk_last_error() != b""
         assert _fwd(d, stash=(A, None)) in (NODEV, HIPERR)
+        assert _fwd(d, dtype=2) in (NODEV, HIPERR)
 
 
 def test_bwd_validation_codes():
@@ -96,11 +102,13 @@ def test_bwd_validation_codes():
     ps, _k3 = _lib.ptr_array([A, A])
     pg, _k4 = _lib.ptr_array([A, A, A])
     call = lambda **kw: lib.mlpmk_bwd(  # noqa: E731
-        3, pd, kw.get("x", A), pw, kw.get("stash", ps), kw.get("dout", A), kw.get("stride", 128),
+        3, pd, kw.get("dtype", 1), kw.get("x", A), pw, kw.get("stash", ps), kw.get("dout", A), kw.get("stride", 128),
         kw.get("dx", None), kw.get("dw", pg), kw.get("m", 256), None)
     assert call(m=-1) == INVALID
     assert call(stride=-1) == INVALID
     assert call(dw=None) == INVALID
+    assert call(dtype=0) == UNSUPPORTED
+    assert call(dtype=3) == INVALID
     if ops.bwd_supported(d):
         assert call(stride=64) == INVALID  # below the output width
         assert call(stride=130) == MISALIGNED
@@ -126,7 +134,7 @@ def test_recompute_validation_codes():
 
     def call(stash, dx=None, dims=pd, n=3, w=pw, g=pg):
         ps, _k = _lib.ptr_array(list(stash))
-        return lib.mlpmk_bwd(n, dims, A, w, ps, A, 128, dx, g, 256, None)
+        return lib.mlpmk_bwd(n, dims, 1, A, w, ps, A, 128, dx, g, 256, None)
 
     assert call((A, None), dx=A) == INVALID
     assert b"stash[1]" in lib.mlpmk_last_error() and b"dx" in lib.mlpmk_last_error()
@@ -147,18 +155,20 @@ def test_5l_backward_is_supported_but_needs_a_workspace():
     ps, _k3 = _lib.ptr_array([A] * 4)
     pg, _k4 = _lib.ptr_array([A] * 5)
     # Rejected before any device call: dz travels between two launches through the workspace.
-    assert lib.mlpmk_bwd(5, pd, A, pw, ps, A, 128, None, pg, 256, None) == INVALID
+    assert lib.mlpmk_bwd(5, pd, 1, A, pw, ps, A, 128, None, pg, 256, None) == INVALID
     assert b"mlpmk_bwd_ws" in lib.mlpmk_last_error()
 
 
 def test_wn_and_copy_validation_codes():
     lib = _lib.get()
     pd, _k = _lib.int_array([128, 128, 128, 128])
-    assert lib.mlpmk_wn_fwd(3, pd, 7, A, A, A, A, None) == INVALID  # bad dtype
-    assert lib.mlpmk_wn_fwd(3, pd, 0, A, None, A, A, None) == INVALID
+    assert lib.mlpmk_wn_fwd(3, pd, 7, 1, A, A, A, A, None) == INVALID  # bad dtype
+    assert lib.mlpmk_wn_fwd(3, pd, 0, 0, A, A, A, A, None) == INVALID  # W must be fp16 or bf16
+    assert b"w_dtype" in lib.mlpmk_last_error()
+    assert lib.mlpmk_wn_fwd(3, pd, 0, 1, A, None, A, A, None) == INVALID
     assert lib.mlpmk_wn_bwd(3, pd, 1, A, A, A, A, A + 2, A, None) == MISALIGNED
     pbad, _k2 = _lib.int_array([128, 0, 128, 128])
-    assert lib.mlpmk_wn_fwd(3, pbad, 0, A, A, A, A, None) == INVALID  # any positive widths
+    assert lib.mlpmk_wn_fwd(3, pbad, 0, 1, A, A, A, A, None) == INVALID  # any positive widths
     assert lib.mlpmk_copy(A, A, 17, None) == INVALID
     assert lib.mlpmk_copy(A, A, 0, None) == OK
 

@@ -212,7 +212,7 @@ def test_workspace_too_small_is_rejected():
     pw, _k2 = _lib.ptr_array([w.data_ptr() for w in wd])
     ps, _k3 = _lib.ptr_array([h.data_ptr() for h in hs])
     pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
-    rc = lib.mlpmk_bwd_ws(3, pd, xd.data_ptr(), pw, ps, dout.data_ptr(), 0, None, pg, buf.data_ptr(), need - 16,
+    rc = lib.mlpmk_bwd_ws(3, pd, 1, xd.data_ptr(), pw, ps, dout.data_ptr(), 0, None, pg, buf.data_ptr(), need - 16,
                           4096, torch.cuda.current_stream().cuda_stream)
     assert rc == 1 and b"workspace_bytes" in lib.mlpmk_last_error()
     assert all(d.abs().max().item() == 0 for d in dws)  # nothing launched

@@ -119,6 +119,37 @@ def test_round_hidden_variant_stays_within_fp16_error():
     assert np.max(np.abs(a - b)) < 5e-3
 
 
+def test_to_bf16_matches_torch_conversion():
+    # Random values over many binades, exact ties (even and odd kept bit),
+    # values past the largest bf16 (round to inf), subnormals, signed zeros,
+    # infinities and NaN: torch's float32 -> bfloat16 conversion is the check.
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal(200000) * np.exp2(rng.integers(-140, 127, 200000))).astype(np.float32)
+    ties = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7F8000, 0x7F7FFFFF, 0x00008000, 0x00018000],
+                    dtype=np.uint32).view(np.float32)
+    edge = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 3.4e38, -3.4e38, 1e-45, 1.17549435e-38], np.float32)
+    a = np.concatenate([a, ties, edge])
+    ref = torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    got = orc.to_bf16(a)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    # 1 + 2^-8 is a tie between 1 and 1 + 2^-7: even (1) wins; 1 + 3*2^-8 rounds up to 1 + 2^-6.
+    assert orc.to_bf16(np.float32(1 + 2.0 ** -8)) == 1.0
+    assert orc.to_bf16(np.float32(1 + 3 * 2.0 ** -8)) == np.float32(1 + 2.0 ** -6)
+
+
+def test_round_hidden_bf16_variant_stays_within_bf16_error():
+    x, ws = orc.make_inputs((128, 128, 128, 128), 512, seed=1, elem="bf16")
+    assert np.array_equal(orc.to_bf16(x), x) and all(np.array_equal(orc.to_bf16(w), w) for w in ws)
+    a = orc.forward(x, ws)
+    b = orc.forward(x, ws, round_hidden=True, elem="bf16")
+    c = orc.forward(x, ws, round_hidden=True)
+    # bf16 keeps 8 significant bits against fp16's 11: about 8x the fp16 error.
+    assert np.max(np.abs(a - b)) < 4e-2
+    assert np.max(np.abs(a - c)) < np.max(np.abs(a - b))
+
+
 # ---------------------------------------------------------------- backward --
 def torch_grads(x, ws, dout):
     xt = torch.from_numpy(np.asarray(x, np.float64)).requires_grad_(True)
