@@ -130,7 +130,10 @@ __device__ __forceinline__ f16x2 cvt2(float a, float b) {
     f16x2 r = __builtin_bit_cast(f16x2, __builtin_convertvector((f32x2){a, b}, bf16x2));  // v_cvt_pk_bf16_f32
     // An empty statement that takes the packed pair as is: without it the
     // compiler re-derived some pairs read as fp16 (the overflow tracking)
-    // from two single conversions and a repack, which spilled.
+    // from two single conversions and a repack, which spilled.  It emits no
+    // instruction, and the compiler still spaces the conversion and the
+    // MFMA that reads it as for fp16 (at least two instructions apart in
+    // every kernel's generated code).
     asm("" : "+v"(r));
     return r;
   } else
