@@ -163,6 +163,8 @@ def fwd(x, weights, stash=False, recompute=False):
     if stash:
         hs = [torch.empty((M, d), device=x.device, dtype=torch.float32) for d in dims[1:-1]]
         if recompute:
+            if not bwd_recompute_supported(dims):
+                raise ValueError(f"no recomputing backward for widths {dims}: stash every activation")
             hs[-1] = None
     fwd_into(x, weights, out, hs)
     return (out, hs) if stash else out

@@ -124,6 +124,14 @@ def test_recompute_support_table(dims, ok):
     assert ops.bwd_recompute_supported(list(dims)) is ok
 
 
+def test_recompute_needs_a_supported_shape_in_the_python_layer():
+    x = torch.zeros((4, 32), dtype=torch.float16)
+    ws = [torch.zeros((32, 64), dtype=torch.float16), torch.zeros((64, 64), dtype=torch.float16),
+          torch.zeros((64, 16), dtype=torch.float16)]
+    with pytest.raises(ValueError, match="recomputing"):
+        ops.fwd(x, ws, stash=True, recompute=True)
+
+
 def test_recompute_validation_codes():
     # stash[L-2] == NULL selects the recomputing backward where it exists;
     # every other NULL stash entry, and dx in that mode, is rejected on the host.
