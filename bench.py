@@ -206,7 +206,7 @@ def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
 
 
 
-def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None):
+def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, dtype=None):
     """One training step of BASELINE config 5 through the drop-in module:
     weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
     megakernel + weight-norm backward, x without grad.  Timed with HIP events
@@ -219,19 +219,19 @@ def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None):
     if recompute is not None:
         mag.RECOMPUTE = recompute
     try:
-        return _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers)
+        return _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype or torch.float16)
     finally:
         mag.RECOMPUTE = policy
 
 
-def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers):
+def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
     from mlpmk import autograd as mag
 
     torch.manual_seed(0)
     model = fused_mlp.FusedMLPSoftplusWN(n_layers=n_layers).cuda()
     dims = tuple(model.dims)
     rc = mag._use_recompute(dims, m, False)
-    x = torch.randn(m, 128, device="cuda").half()
+    x = torch.randn(m, 128, device="cuda").to(dtype)  # bf16 x runs the bf16 kernels
 
     def step(_):
         model.v_all.grad = None
@@ -274,6 +274,7 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers):
         "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd" if n_layers == 3 else
                     "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..2, then 1..0) + wn_bwd",
         "recompute_h_last": rc,
+        "dtype": str(dtype).replace("torch.", ""),
     }
 
 
@@ -493,6 +494,8 @@ def main():
     if args.train:
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
         result["training_5l"] = {str(mt): train_step_bench(torch, mt, n_layers=5) for mt in (65536, 131072)}
+        result["training_bf16"] = {str(mt): train_step_bench(torch, mt, steps=20, warmup=5, dtype=torch.bfloat16)
+                                   for mt in (16384, 131072)}
         result["training_stash_vs_recompute"] = {
             str(mt): {pol: train_step_bench(torch, mt, steps=20, warmup=5, recompute=pol) for pol in ("never", "always")}
             for mt in (131072, 1048576)}
