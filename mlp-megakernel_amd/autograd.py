@@ -26,13 +26,13 @@ import torch
 from . import ops
 
 # Activation recomputation policy: "auto" recomputes h_{L-1} from
-# RECOMPUTE_MIN_ROWS rows on, where the training step is faster with it
-# (3-layer 128-wide network on MI355X, forward + backward replayed as one HIP
-# graph: 374 -> 352 us at 524288 rows, 716 -> 655 us at 1048576; within 2 %
-# either way at 4096 .. 131072 rows) and the stash is half the size;
-# "always" / "never" force the choice where the shape allows it.
+# RECOMPUTE_MIN_ROWS rows on, where the training step is as fast or faster
+# with it (3-layer 128-wide network on MI355X, forward + backward replayed as
+# one HIP graph: 101.9 -> 101.8 us at 131072 rows, 377 -> 339 us at 524288,
+# 713 -> 633 us at 1048576; 46.1 -> 48.0 us at 16384) and the stash is half
+# the size; "always" / "never" force the choice where the shape allows it.
 RECOMPUTE = "auto"
-RECOMPUTE_MIN_ROWS = 1 << 19
+RECOMPUTE_MIN_ROWS = 1 << 17
 
 _rc_shapes = {}
 

@@ -550,8 +550,11 @@ struct BwdWave {
   // bit for bit.  Where some operand of the wave would overflow fp16 (h above
   // ~45400), the operands are halved and the products doubled, as the
   // forward's exact form does.
-  template <bool HALF>
-  __device__ __forceinline__ void recompute_t() {
+  // FIX: the exact form (sp2_fix per value); the fast form instead tracks the
+  // largest u and returns whether some u reached 128 (2^u overflowed), in
+  // which case the caller reloads h_{L-2} and runs the exact form.
+  template <bool HALF, bool FIX>
+  __device__ __forceinline__ bool recompute_t() {
     constexpr int l = L - 2;
     constexpr int KSI = N::d[l] / 16, MBO = N::d[l + 1] / 32;
     constexpr float sc = HALF ? 0.5f * kLog2e : kLog2e;
@@ -567,6 +570,7 @@ struct BwdWave {
     // fences keep the compiler from hoisting later blocks' fragment reads
     // (all 32 at once would not fit beside the weight-gradient accumulators).
     f32x16 acc[2];
+    float umax = -INFINITY;
 #pragma unroll
     for (int mb = 0; mb <= MBO; ++mb) {
       if (mb < MBO) {
@@ -583,11 +587,26 @@ struct BwdWave {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float u0 = HALF ? 2.0f * a[j] : a[j], u1 = HALF ? 2.0f * a[8 + j] : a[8 + j];
-          hbuf[0][2 * q][j] = sp2_fix(u0, sp2(u0)) * kLn2;
-          hbuf[0][2 * q + 1][j] = sp2_fix(u1, sp2(u1)) * kLn2;
+          if constexpr (FIX) {
+            hbuf[0][2 * q][j] = sp2_fix(u0, sp2(u0)) * kLn2;
+            hbuf[0][2 * q + 1][j] = sp2_fix(u1, sp2(u1)) * kLn2;
+          } else {
+            hbuf[0][2 * q][j] = sp2(u0) * kLn2;
+            hbuf[0][2 * q + 1][j] = sp2(u1) * kLn2;
+            umax = fmaxf(umax, fmaxf(u0, u1));
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+    }
+    return !FIX && __builtin_amdgcn_ballot_w64(umax >= 128.0f) != 0;
+  }
+  template <bool HALF>
+  __device__ __forceinline__ void recompute_h() {
+    if (__builtin_expect(recompute_t<HALF, false>(), 0)) {
+      // Some 2^u overflowed: h_{L-2} again (an L2 hit), then the exact form.
+      load_h<L - 2>(row0);
+      recompute_t<HALF, true>();
     }
   }
   __device__ __forceinline__ void recompute() {
@@ -598,9 +617,9 @@ struct BwdWave {
 #pragma unroll
       for (int j = 0; j < 8; j += 2) m = fmaxf(m, fmaxf(hbuf[0][s][j], hbuf[0][s][j + 1]));
     if (!N::bf && __builtin_amdgcn_ballot_w64(m * kLog2e > 65504.0f) != 0)  // bf16 has fp32's range
-      recompute_t<true>();
+      recompute_h<true>();
     else
-      recompute_t<false>();
+      recompute_h<false>();
     // Rows past M read h_{L-2} = 0 and would recompute softplus(0) = ln 2,
     // where a stash reads 0: with a broadcast dout (row stride 0) those rows
     // see a nonzero gradient, so their h_{L-1} must be 0 as well.
