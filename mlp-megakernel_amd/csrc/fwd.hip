@@ -19,9 +19,9 @@
 //  * Activations run in base-2 units: W_1 is staged pre-scaled by log2(e) and
 //    W_L by ln(2), hidden layers chain with no scaling at all (ln2 and log2e
 //    cancel between W^T h' and the next exp2), so the epilogue is exp2, add,
-//    log2 per element in fp32 and one pack per pair (see sp2), after a
-//    wave-uniform overflow test per 16 values.  The stash stores natural-unit
-//    h = ln2 * h' in fp32.
+//    log2 per element in fp32 and one pack per pair (see sp2); overflow is
+//    detected one layer later by a class test of one accumulator per row.
+//    The stash stores natural-unit h = ln2 * h' in fp32.
 //  * Each layer is software-pipelined by 32-feature output block: the MFMA
 //    chain of block mb+1 is issued ahead of block mb's activation, so the
 //    matrix core and the VALU work concurrently within one wave.
@@ -374,19 +374,39 @@ __device__ __forceinline__ void chain(f32x16 (&acc)[NB], Frags<KSM>& f, const T 
 // Activation and hand-off of output block mb: hidden layers apply softplus
 // (base-2 units), optionally store the fp32 stash, and pack the next layer's
 // B operands; the last layer stores fp16 rows of `out`.  The fast form
-// (EXACT false) evaluates sp2 directly and folds the packed values into the
-// running maximum `m`.  The exact form replaces overflowed values by u and
-// hands on sp2 / 2: in base-2 units a hidden activation is 1.44x its natural
-// value, so values above ~45,400 (natural) would not fit fp16, whereas the
-// reference's fp16 h (kernel.py:110) holds them up to 65,504.  Halving (and
-// doubling every later accumulator, kIn) keeps the whole range; both are
-// exact power-of-two scalings.
+// (EXACT false) evaluates sp2 directly; an overflow there (sp2 = +inf for
+// u >= 128, or an fp16 operand past 65,504) or a NaN is caught one layer
+// later, by `bad` (see below).  The exact form replaces overflowed values by
+// u and hands on sp2 / 2: in base-2 units a hidden activation is 1.44x its
+// natural value, so values above ~45,400 (natural) would not fit fp16,
+// whereas the reference's fp16 h (kernel.py:110) holds them up to 65,504.
+// Halving (and doubling every later accumulator, kIn) keeps the whole range;
+// both are exact power-of-two scalings.
+//
+// Overflow detection by propagation: every accumulator of a row in layer
+// l >= 1 sums that row's whole input vector, and a product with an infinite
+// or NaN operand is infinite or NaN whatever the weight (inf * 0 = NaN), so
+// one non-finite input makes every accumulator of the row non-finite.  A
+// finite input row keeps the fp32 accumulators finite (at most 128 products
+// of fp16 magnitudes, far below the fp32 range).  Testing one accumulator
+// per row and layer -- element 0 of output block 0, which every lane holds
+// for its row -- therefore detects every overflow and NaN of the layer
+// below: one class test per lane and layer instead of folding every packed
+// activation into a running maximum (33 v_pk_maximum3_f16 per 32-row block
+// of the 3-layer network).  Layer 0's inputs are the caller's x, and a
+// non-finite x also triggers the exact pass, which reproduces it.
 template <class N, int l, int NB, bool STASH, bool STAGE, bool EXACT, int KSM>
 __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[NB], int mb,
-                                         f16x8 (&nxt)[KSM][NB], f16x2& m, int lane) {
+                                         f16x8 (&nxt)[KSM][NB], bool& bad, int lane) {
   constexpr int Nout = N::d[l + 1];
   constexpr bool LAST = (l == N::L - 1);
   const int n = lane & 31, g = lane >> 5;
+  if constexpr (!EXACT && l > 0) {
+    if (mb == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bad = bad || !__builtin_isfinite(acc[nb][0]);
+    }
+  }
   // Registers 0..7 -> features 32mb + 8g + [0..7]; 8..15 -> 32mb + 16 + 8g + [0..7].
   const bool lo_ok = (32 * mb + 16 <= Nout);  // folded after unrolling
   const bool hi_ok = (32 * mb + 32 <= Nout);
@@ -440,9 +460,12 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
         s[e] = EXACT ? sp2_fix(u[e], sp2(u[e])) : sp2(u[e]);
         q[e] = EXACT ? 0.5f * s[e] : s[e];
       }
-      const f16x8 lo = pack8<N::bf>(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
-      const f16x8 hi = pack8<N::bf>(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
-      if constexpr (!EXACT) m = sp2_track<!STASH>(m, lo, hi);
+      f16x8 lo = pack8<N::bf>(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
+      f16x8 hi = pack8<N::bf>(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
+      // Ordering anchor (no instruction): the stash kernels keep more values
+      // live per step, and without an anchor the scheduler interleaved
+      // consecutive epilogues far enough to spill.
+      if constexpr (STASH) asm volatile("" : "+v"(lo), "+v"(hi));
       if constexpr (STASH && N::gen) {
         // Runtime hidden width HW (a multiple of 16): feature groups past it are dropped.
         const rsrc_t sr = io.stash[l];
@@ -511,7 +534,7 @@ struct Chain {
   f16x8 b0[KSM][NB], b1[KSM][NB];  // hidden activations, ping-pong between layers
   f32x16 acc[2][NB];             // accumulators of the current and the next step
   Frags<KSM> fr;                 // fragments of the next chain to issue
-  f16x2 ovf;                     // running maximum of the block's packed sp2 values
+  bool bad;                      // some row's accumulator of layer >= 1 was not finite
   f16x8 rf;                      // register-resident fragment (LdsPlan::reg_frags)
 
   // Layer l reads x (l = 0), b0 (odd l) or b1 (even l >= 2) and writes b0
@@ -562,7 +585,7 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
     MLPMK_SCHED_FENCE();
     load_block_x<N, NB>(c.xa, p, next * ROWS, lane);
   }
-  epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.ovf, lane);
+  epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.bad, lane);
   if constexpr (l == N::L - 1 && STAGE) {
     if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
   }
@@ -576,7 +599,8 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
 // One row block: the whole layer chain, stores, and the x refill for block
 // `next`.  On entry c.xa holds the block's x rows and c.fr the fragments of
 // step 0; on exit they hold the same for block `next`.  Returns (wave-
-// uniform) whether some sp2 of the fast form overflowed or was NaN.
+// uniform) whether some row of the fast form met a non-finite accumulator in
+// a layer >= 1: an overflowed or NaN activation below it (see epilogue).
 template <class N, int NB, bool STASH, bool STAGE, bool EXACT, int KSM, int RF>
 __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
                                           int lane_off, i32x4* stage, int64_t b, int64_t next, int lane) {
@@ -585,16 +609,17 @@ __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>&
   BlockIO io = block_io<N, STASH, ROWS>(p, b * ROWS);
   io.stage = stage;
   const FragBase<N, RF> fb(lds_b, lane_off);
-  c.ovf = f16x2{};
+  c.bad = false;
   chain<N, T1, RF, 0, N::ks(0), NB>(c.acc[0], c.fr, c.xa, fb, c.rf);
   load_frags<N, T1, KSM, RF, N::ks(0)>(c.fr, fb, c.rf);
   step<N, 0, NB, STASH, STAGE, EXACT, KSM, RF>(p, io, c, fb, next, lane);
-  return !EXACT && sp2_overflowed<N::bf>(c.ovf);
+  return !EXACT && __builtin_amdgcn_ballot_w64(c.bad) != 0;
 }
 
-// Block b with the fast softplus form, then -- only if one of its wave's sp2
-// values overflowed (some u >= 128) -- again with the exact form, from a
-// fresh read of its x rows and step-0 fragments.  The second pass rewrites
+// Block b with the fast softplus form, then -- only if one of its wave's rows
+// overflowed (some u >= 128 or an fp16 activation past 65,504) or met a NaN
+// -- again with the exact form, from a fresh read of its x rows and step-0
+// fragments.  The second pass rewrites
 // every output (and stash) row of the block and leaves c as the first did.
 template <class N, int NB, bool STASH, bool STAGE, int KSM, int RF>
 __device__ __forceinline__ void fwd_block_checked(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,

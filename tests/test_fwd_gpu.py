@@ -185,8 +185,9 @@ def test_threshold_edges_through_identity_weights():
     assert abs(out[0, 4] - np.log(3.0)) < 2e-3  # z = 0: softplus(softplus(0)) = log(1 + 2)
 
 
-# M = 256 runs the feature-split kernel, M = 16384 the one-block-per-wave one.
-@pytest.mark.parametrize("m", [256, 16384])
+# M = 256 runs the feature-split kernel, M = 16384 the one-block-per-wave
+# one, M = 131072 the persistent 12-wave one (3 waves per SIMD).
+@pytest.mark.parametrize("m", [256, 16384, 131072])
 @pytest.mark.parametrize("stash", [False, True])
 def test_large_preactivations_take_the_exact_path(stash, m):
     # Past z = 88.7 the kernel's direct softplus form overflows (2^u in base-2
@@ -214,7 +215,7 @@ def test_large_preactivations_take_the_exact_path(stash, m):
             assert ok, f"stash h{i + 1}: max|err| {err}"
 
 
-@pytest.mark.parametrize("m", [4096, 20000])
+@pytest.mark.parametrize("m", [4096, 20000, 131072])
 @pytest.mark.parametrize("dims,stash", [((128, 128, 128, 128), False), ((128, 128, 128, 128), True),
                                         ((128,) * 6, False), ((32, 64, 64, 16), False)])
 def test_scaled_inputs_overflow_many_blocks(dims, stash, m):
@@ -242,7 +243,7 @@ def test_scaled_inputs_overflow_many_blocks(dims, stash, m):
         assert torch.equal(res[0], ops.fwd(xd, wd))
 
 
-@pytest.mark.parametrize("m", [128, 16384])
+@pytest.mark.parametrize("m", [128, 16384, 131072])
 def test_inf_and_nan_inputs_propagate_like_the_oracle(m):
     # inf * 0 inside the products gives NaN, as in the reference's fp32 dot;
     # rows without non-finite inputs are unaffected.
@@ -258,6 +259,39 @@ def test_inf_and_nan_inputs_propagate_like_the_oracle(m):
     fin = np.isfinite(ref).all(axis=1)
     assert fin.sum() == m - 3
     _check(out[fin], ref[fin], "finite rows next to non-finite ones")
+
+
+@pytest.mark.parametrize("m", [256, 16384, 131072])
+@pytest.mark.parametrize("stash", [False, True])
+def test_overflow_into_negative_weight_row_is_not_absorbed(stash, m):
+    # The fast softplus form overflows to +inf for z >= 88.7.  Here hidden
+    # unit k of h1 overflows in a few rows and row k of W2 is strictly
+    # negative, so in the fast form every pre-activation of layer 2 of those
+    # rows is -inf, and softplus(-inf) = 0 would hide the overflow from any
+    # test of the layer-2 activations.  The exact value is far from 0:
+    # h1[k] = z = 100, z2 = 100 * (-1e-3) + (other terms) = O(1).  The kernel
+    # must detect the overflow (the -inf pre-activations are non-finite) and
+    # recompute those blocks exactly.
+    rng = np.random.default_rng(5)
+    k = 17
+    x = (rng.standard_normal((m, 128)) * 0.5).astype(np.float16)
+    rows = [1, 33, m - 2]
+    for r in rows:
+        x[r, k] = np.float16(100.0)
+    w1 = np.eye(128, dtype=np.float16)
+    w2 = (rng.standard_normal((128, 128)) / np.sqrt(128)).astype(np.float16)
+    w2[k, :] = np.float16(-1e-3)
+    w3 = (rng.standard_normal((128, 128)) / np.sqrt(128)).astype(np.float16)
+    ws = [w1, w2, w3]
+    xd, wd = _to_dev(x, ws)
+    res = ops.fwd(xd, wd, stash=stash)
+    out = (res[0] if stash else res).float().cpu().numpy()
+    sel = np.array(sorted(set(rows) | set(range(0, m, max(1, m // 2048)))))
+    ref = orc.forward(x[sel], ws)
+    _check(out[sel], ref, "overflow feeding a negative weight row")
+    # An absorbed overflow would leave h2 = 0 and out = 0 in those rows; the
+    # exact outputs are O(1), so the check above tells the two apart.
+    assert np.abs(orc.forward(x[rows], ws)).max(axis=1).min() > 0.5
 
 
 def test_zero_first_layer_closed_form():
