@@ -24,13 +24,7 @@ import torch
 import torch.nn as nn
 
 import _mlpmk  # noqa: F401  (registers the package as ``mlpmk``)
-from mlpmk.autograd import FusedMLPFunction, FusedMLPWNFunction, _split
-
-
-def _elem_dtype(x):
-    """Element type the kernels run in for input ``x``: bf16 for bf16 input,
-    else fp16 (the reference's modules cast to fp16, README.md:24-34)."""
-    return torch.bfloat16 if x.dtype == torch.bfloat16 else torch.float16
+from mlpmk.autograd import FusedMLPFunction, FusedMLPWNFunction, _split, fused_mlp, fused_mlp_wn  # noqa: F401
 
 
 def _dims(D, H, out_features, n_layers):
@@ -50,11 +44,12 @@ class FusedMLPSoftplus(nn.Module):
         )
 
     def forward(self, x):
-        # The kernels take fp16 or bf16: under autocast custom_fwd casts to fp16;
-        # otherwise a bf16 x runs the bf16 kernels and anything else is cast to
-        # fp16 (autograd carries the gradient back through the casts).
-        dt = _elem_dtype(x)
-        return FusedMLPFunction.apply(x.to(dt), *[w.to(dt) for w in self.weights])
+        # The kernels take fp16 or bf16 (mlpmk.autograd.kernel_dtype: the
+        # autocast dtype under autocast, else bf16 for bf16 x and fp16 for
+        # anything else; autograd carries the gradient back through the
+        # casts).  Without autograd (no_grad, inference_mode, or nothing
+        # requiring grad) this is one plain forward launch, no fp32 stash.
+        return fused_mlp(x, *self.weights)
 
     def extra_repr(self):
         return f"dims={self.dims}"
@@ -85,9 +80,8 @@ class FusedMLPSoftplusWN(nn.Module):
         return self.g_all[off : off + self.dims[layer + 1]]
 
     def forward(self, x):
-        if torch.is_autocast_enabled("cuda"):
-            return FusedMLPWNFunction.apply(x, self.v_all, self.g_all, self.dims)
-        return FusedMLPWNFunction.apply(x.to(_elem_dtype(x)), self.v_all, self.g_all, self.dims)
+        # Element type and stash rule as FusedMLPSoftplus.forward.
+        return fused_mlp_wn(x, self.v_all, self.g_all, self.dims)
 
     def extra_repr(self):
         return f"dims={self.dims}"

@@ -110,6 +110,25 @@ int mlpmk_bwd_recompute_supported(int num_layers, const int* dims);
 int mlpmk_fwd(int num_layers, const int* dims, int dtype, const void* x, const void* const* w, void* out,
               float* const* stash, int64_t M, void* stream);
 
+/* Forward kernels, as reported by mlpmk_fwd_launch_info. */
+enum {
+  MLPMK_KERNEL_NONE = -1,          /* M == 0: nothing is launched */
+  MLPMK_KERNEL_PERSISTENT = 0,     /* persistent grid, one 32*k-row block per wave at a time */
+  MLPMK_KERNEL_FEATURE_SPLIT = 1   /* small batches: the waves of a workgroup share each 32-row block */
+};
+
+/*
+ * The launch mlpmk_fwd makes for (num_layers, dims, dtype, M, stash != 0) on
+ * the current device, without launching: info[0] = kernel (MLPMK_KERNEL_*),
+ * info[1] = rows per batch block, info[2] = 64-lane waves per workgroup,
+ * info[3] = workgroups in the grid, info[4] = resident workgroups per CU.
+ * Needs the device (CU count, occupancy); launches nothing.  The library
+ * side of the reference's launch heuristic `_pick_config` (/root/reference/
+ * kernel.py:25-53, grid kernel.py:139-142), whose Python mirror kernel.py
+ * keeps; it answers from the same code path that mlpmk_fwd launches from.
+ */
+int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M, int stash, int* info);
+
 /*
  * Backward megakernel (one launch): data gradients with MFMA, weight gradients
  * as split-K partials reduced in LDS and then added with global fp32 atomics

@@ -24,10 +24,18 @@ import _mlpmk  # noqa: F401  (registers the package as ``mlpmk``)
 from mlpmk import ops as _ops
 
 # gfx950 launch policy of the inference forward (mlp-megakernel_amd/csrc/fwd.hip
-# and fwd_split.hip), mirrored here for _pick_config.
+# fwd_dispatch / launch_fwd_any and fwd_split.hip fwd_split_dispatch).  On a
+# GPU, _pick_config asks the library (mlpmk_fwd_launch_info, the same code
+# path that launches); this mirror answers without a device.
 _MI355X_CUS = 256
-_WAVES_PER_WG_WIDE = 12  # one-block-per-wave kernel, 3 waves per SIMD
-_WAVES_PER_WG_NARROW = 16
+# dims -> (max 32-row blocks per CU for the feature-split kernel, its waves,
+#          rows per block of the persistent kernel, its largest waves per workgroup)
+_POLICY = {
+    (128, 128, 128, 128): (1, 4, 32, 12),
+    (128, 128, 128, 128, 128, 128): (2, 4, 32, 12),
+    (32, 64, 64, 16): (2, 2, 64, 16),
+}
+_GENERIC_POLICY = (0, 0, 32, 8)  # runtime-width kernels: no split kernel, at most 8 waves
 
 
 def __getattr__(name):
@@ -36,36 +44,46 @@ def __getattr__(name):
     raise AttributeError(name)
 
 
+def _mirror_policy(M, dims, num_cus):
+    split_per_cu, split_waves, bm, max_waves = _POLICY.get(tuple(dims), _GENERIC_POLICY)
+    if -(-M // 32) <= split_per_cu * num_cus:
+        return 32, split_waves
+    blocks = -(-M // bm)
+    if max_waves > 4 and blocks <= 4 * num_cus:
+        return bm, 4
+    if max_waves > 8 and blocks <= 8 * num_cus:
+        return bm, 8
+    return bm, max_waves
+
+
 def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
     """gfx950 launch policy in the reference's tuple shape
-    ``(BM, BN3, BK1, BK2, BK3, warps)`` (kernel.py:25-53), as the library
-    applies it for the 3-layer network at this M.
+    ``(BM, BN3, BK1, BK2, BK3, warps)`` (kernel.py:25-53) for the 3-layer
+    network ``K1 -> N1 -> N2 -> N3`` at batch M.
 
-    BM = rows per block (32: one MFMA batch block; 64 for the narrow network's
-    one-block-per-wave kernel, which reads each weight fragment for two
-    blocks), BN3 = the whole output width (a workgroup computes every output
-    column), BK* = 16 (the K of v_mfma_f32_32x32x16_f16), warps = 64-lane waves
-    per workgroup:
-      * up to one 32-row block per CU (two for the narrow network): the
-        feature-split kernel, one wave per 32 output features (4 waves, 2 for
-        the narrow network) sharing each block;
-      * otherwise the persistent one-block-per-wave kernel with 4 waves per
-        workgroup up to 4 blocks per CU, 8 up to 8, then 12 (16 narrow).
-    ``num_cus`` defaults to ``NUM_SMS`` on a GPU and to MI355X's 256
-    otherwise.  ``fp32`` inputs are not supported by the main-branch surface
-    either (/root/reference/AGENTS.md:86-88).
+    BM = rows per MFMA batch block (32; 64 for the narrow network's
+    persistent kernel, which reads each weight fragment for two blocks),
+    BN3 = the whole output width (a workgroup computes every output column),
+    BK* = 16 (the K of v_mfma_f32_32x32x16_f16), warps = 64-lane waves per
+    workgroup:
+      * small batches (up to one 32-row block per CU for 3L-128, two for the
+        narrow network): the feature-split kernel, one wave per 32 output
+        features (4 waves; 2 for the narrow network) sharing each block;
+      * otherwise the persistent kernel with 4 waves per workgroup up to 4
+        blocks per CU, 8 up to 8, then 12 (16 narrow); runtime-width
+        networks (any other widths) at most 8.
+    With ``num_cus`` None and a GPU present the answer comes from the library
+    (``mlpmk_fwd_launch_info``); otherwise from the mirror above with
+    ``num_cus`` CUs (MI355X's 256 by default).  ``fp32`` inputs are not
+    supported by the main-branch surface either (/root/reference/AGENTS.md:86-88).
     """
     if fp32:
         raise TypeError("the fused forward takes fp16 inputs (main-branch surface is fp16 only)")
-    if num_cus is None:
-        num_cus = NUM_SMS if torch.cuda.is_available() else _MI355X_CUS  # noqa: F821 (module __getattr__)
-    narrow = max(K1, N1, N2, N3) <= 64
-    if -(-M // 32) <= (2 if narrow else 1) * num_cus:
-        return 32, N3, 16, 16, 16, 2 if narrow else 4
-    bm = 64 if narrow else 32
-    blocks = -(-M // bm)
-    warps = 4 if blocks <= 4 * num_cus else 8 if blocks <= 8 * num_cus else (
-        _WAVES_PER_WG_NARROW if narrow else _WAVES_PER_WG_WIDE)
+    dims = (K1, N1, N2, N3)
+    if num_cus is None and torch.cuda.is_available():
+        info = _ops.fwd_launch_info(dims, max(int(M), 1))
+        return info["rows_per_block"], N3, 16, 16, 16, info["waves"]
+    bm, warps = _mirror_policy(M, dims, _MI355X_CUS if num_cus is None else num_cus)
     return bm, N3, 16, 16, 16, warps
 
 

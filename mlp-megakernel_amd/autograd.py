@@ -14,8 +14,16 @@ Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
   backward (``ops.bwd_recompute_supported``) and ``x`` without grad, the
   forward stashes h_1 .. h_{L-2} only and the backward recomputes h_{L-1}
   (/root/reference/mlp_fused.md:451-452 lists this trade as future work).
-* AMP: ``custom_fwd(device_type="cuda", cast_inputs=torch.float16)`` and
-  ``custom_bwd`` as mlp_fused.md:168-172 describes.
+* AMP: ``custom_fwd`` / ``custom_bwd`` as mlp_fused.md:168-172 describes.
+  The reference casts to fp16 (``cast_inputs=torch.float16``); here the
+  tensors take the autocast dtype, so ``torch.autocast(dtype=torch.bfloat16)``
+  runs the bf16 kernels and fp16 autocast the fp16 ones (``kernel_dtype``).
+* inference: ``fused_mlp`` / ``fused_mlp_wn`` (and the modules) call the plain
+  forward, without the fp32 stash, whenever autograd will not need it -- grad
+  disabled (``torch.no_grad`` / ``inference_mode``) or nothing requiring grad.
+  Inside ``Function.forward`` grad mode is always off and
+  ``ctx.needs_input_grad`` reflects ``requires_grad`` only, so that choice is
+  made before ``apply``.
 
 Every launch goes through ``libmlpmk.so``; there is no PyTorch fallback.
 """
@@ -48,6 +56,21 @@ def _use_recompute(dims, m, need_dx):
     return ok and (RECOMPUTE == "always" or m >= RECOMPUTE_MIN_ROWS)
 
 
+def kernel_dtype(x):
+    """Element type the megakernels run in for input ``x``: the autocast dtype
+    when autocast is on (fp16 unless it is bf16), else bf16 for a bf16 ``x``
+    and fp16 for anything else (the reference's modules are fp16,
+    README.md:24-34)."""
+    if torch.is_autocast_enabled("cuda"):
+        return torch.bfloat16 if torch.get_autocast_dtype("cuda") == torch.bfloat16 else torch.float16
+    return torch.bfloat16 if x.dtype == torch.bfloat16 else torch.float16
+
+
+def _needs_graph(*tensors):
+    """True when autograd will run a backward through this call."""
+    return torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+
+
 def _as_row_broadcast(dout):
     """``dout`` with unit column stride, keeping a broadcast row (stride 0)
     as a broadcast: ``loss = out.sum()`` hands back a fully expanded scalar
@@ -63,15 +86,18 @@ def _as_row_broadcast(dout):
 class FusedMLPFunction(torch.autograd.Function):
     """``out = softplus(... softplus(x @ W1) ...) @ WL`` with the fused backward.
 
-    Inputs: ``x`` [M, D] and L weights [in, out], all fp16 or all bf16 (cast
-    to fp16 under autocast).  Returns ``out`` [M, OUT] of x's dtype.
+    Inputs: ``x`` [M, D] and L weights [in, out], cast to ``kernel_dtype(x)``
+    (autograd casts the gradients back).  Returns ``out`` [M, OUT] of that
+    dtype.  Always writes the stash when some input requires grad; use
+    ``fused_mlp`` to skip it when grad is disabled.
     """
 
     @staticmethod
-    @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float16)
+    @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, x, *weights):
-        x = x.contiguous()
-        weights = [w.contiguous() for w in weights]
+        dt = kernel_dtype(x)
+        x = x.to(dt).contiguous()
+        weights = [w.to(dt).contiguous() for w in weights]
         if any(ctx.needs_input_grad):
             dims = (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights)
             rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0])
@@ -108,9 +134,9 @@ class FusedMLPWNFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float16)
+    @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, x, v_all, g_all, dims):
-        x = x.contiguous()
+        x = x.to(kernel_dtype(x)).contiguous()
         dims = tuple(int(d) for d in dims)
         L = len(dims) - 1
         dev = x.device
@@ -160,10 +186,23 @@ def _split(flat, dims):
 
 
 def fused_mlp(x, *weights):
-    """Functional form of :class:`FusedMLPFunction`."""
-    return FusedMLPFunction.apply(x, *weights)
+    """Functional form of :class:`FusedMLPFunction`: the training forward
+    (with the fp32 stash) when autograd will need it, else one plain forward
+    launch."""
+    if _needs_graph(x, *weights):
+        return FusedMLPFunction.apply(x, *weights)
+    dt = kernel_dtype(x)
+    return ops.fwd(x.to(dt).contiguous(), [w.to(dt).contiguous() for w in weights])
 
 
 def fused_mlp_wn(x, v_all, g_all, dims):
-    """Functional form of :class:`FusedMLPWNFunction`."""
-    return FusedMLPWNFunction.apply(x, v_all, g_all, tuple(dims))
+    """Functional form of :class:`FusedMLPWNFunction` (same stash rule as
+    :func:`fused_mlp`)."""
+    dims = tuple(int(d) for d in dims)
+    if _needs_graph(x, v_all, g_all):
+        return FusedMLPWNFunction.apply(x, v_all, g_all, dims)
+    x = x.to(kernel_dtype(x)).contiguous()
+    w_all = torch.empty(sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1)), dtype=x.dtype, device=x.device)
+    inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=x.device)
+    ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
+    return ops.fwd(x, _split(w_all, dims))

@@ -13,7 +13,7 @@
 namespace mlpmk {
 
 bool fwd_supported_dims(int L, const int* dims);
-int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st);
+int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, LaunchInfo* info);
 bool bwd_supported_dims(int L, const int* dims);
 bool bwd_recompute_supported(int L, const int* dims);
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st);
@@ -170,7 +170,32 @@ int mlpmk_fwd(int num_layers, const int* dims, int dtype, const void* x, const v
   p.M = M;
   for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
   return fwd_dispatch(num_layers, dims, p, stash != nullptr, dtype == MLPMK_DTYPE_BF16,
-                      static_cast<hipStream_t>(stream));
+                      static_cast<hipStream_t>(stream), nullptr);
+}
+
+int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M, int stash, int* info) {
+  g_last_error[0] = 0;
+  int rc = check_dims(num_layers, dims);
+  if (rc) return rc;
+  if ((rc = check_elem_dtype(dtype))) return rc;
+  if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
+  if (!info) return fail(MLPMK_ERR_INVALID_ARG, "info is NULL");
+  if (!fwd_supported_dims(num_layers, dims))
+    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
+  if (M == 0) {  // mlpmk_fwd launches nothing
+    const int none[5] = {MLPMK_KERNEL_NONE, 0, 0, 0, 0};
+    memcpy(info, none, sizeof(none));
+    return MLPMK_OK;
+  }
+  FwdParams p = {};
+  p.M = M;
+  for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
+  LaunchInfo li = {};
+  rc = fwd_dispatch(num_layers, dims, p, stash != 0, dtype == MLPMK_DTYPE_BF16, nullptr, &li);
+  if (rc) return rc;
+  const int out[5] = {li.kernel, li.rows_per_block, li.waves, li.grid, li.wgs_per_cu};
+  memcpy(info, out, sizeof(out));
+  return MLPMK_OK;
 }
 
 static int bwd_common(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,

@@ -741,7 +741,7 @@ static bool dims_match(int L, const int* dims) {
 }
 
 template <class N, int NB, bool STASH, int NW, int D>
-static int launch_fwd(const FwdParams& p, hipStream_t st) {
+static int launch_fwd(const FwdParams& p, hipStream_t st, LaunchInfo* info) {
   constexpr int kMaxDev = 64;
   static int occ_cache[kMaxDev];  // 0 = unknown; benign race (idempotent value)
   int cus = 0;
@@ -762,6 +762,10 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
   const int64_t wgs = (nblk + NW - 1) / NW;
   const int64_t cap = (int64_t)cus * occ;
   const int grid = (int)(wgs < cap ? wgs : cap);
+  if (info) {
+    *info = LaunchInfo{MLPMK_KERNEL_PERSISTENT, (int)rows, NW, grid, occ};
+    return MLPMK_OK;
+  }
   (void)hipGetLastError();
   hipLaunchKernelGGL((fwd_kernel<N, NB, STASH, NW, D>), dim3(grid), dim3(NW * 64), 0, st, p);
   e = hipGetLastError();
@@ -781,18 +785,18 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
 // kernel runs 4-wave workgroups (one wave per SIMD), up to 8 blocks per CU
 // 8-wave workgroups; the persistent NW-wave kernel takes over beyond that.
 template <class N, int NB, int NW, int NBS, int NWS, int D>
-static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st) {
+static int launch_fwd_any(const FwdParams& p, bool stash, hipStream_t st, LaunchInfo* info) {
   int cus = 0;
   const int rc = current_device_cus(&cus);
   if (rc != MLPMK_OK) return rc;
   const int64_t nblk = (p.M + 32 * (stash ? NBS : NB) - 1) / (32 * (stash ? NBS : NB));
   if (stash) {
-    if (NWS > 4 && nblk <= 4 * (int64_t)cus) return launch_fwd<N, NBS, true, 4, D>(p, st);
-    return launch_fwd<N, NBS, true, NWS, D>(p, st);
+    if (NWS > 4 && nblk <= 4 * (int64_t)cus) return launch_fwd<N, NBS, true, 4, D>(p, st, info);
+    return launch_fwd<N, NBS, true, NWS, D>(p, st, info);
   }
-  if (NW > 4 && nblk <= 4 * (int64_t)cus) return launch_fwd<N, NB, false, 4, D>(p, st);
-  if (NW > 8 && nblk <= 8 * (int64_t)cus) return launch_fwd<N, NB, false, 8, D>(p, st);
-  return launch_fwd<N, NB, false, NW, D>(p, st);
+  if (NW > 4 && nblk <= 4 * (int64_t)cus) return launch_fwd<N, NB, false, 4, D>(p, st, info);
+  if (NW > 8 && nblk <= 8 * (int64_t)cus) return launch_fwd<N, NB, false, 8, D>(p, st, info);
+  return launch_fwd<N, NB, false, NW, D>(p, st, info);
 }
 
 // Runtime-width networks of 2..5 layers, compiled at width 128: any input
@@ -817,40 +821,41 @@ bool fwd_supported_dims(int L, const int* dims) {
          dims_match<NetNarrow>(L, dims) || fwd_generic_dims(L, dims);
 }
 
-int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus);
+int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus,
+                       LaunchInfo* info);
 
 // B: bf16 tensors (every shape is instantiated for both element formats).
 template <bool B>
-static int fwd_dispatch_t(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st) {
+static int fwd_dispatch_t(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, LaunchInfo* info) {
   if (dims_match<Net3L128>(L, dims))
-    return launch_fwd_any<typename ElemNet<B, Net3L128>::type, 1, 12, 1, 8, 1>(p, stash, st);
+    return launch_fwd_any<typename ElemNet<B, Net3L128>::type, 1, 12, 1, 8, 1>(p, stash, st, info);
   if (dims_match<Net5L128>(L, dims))
-    return launch_fwd_any<typename ElemNet<B, Net5L128>::type, 1, 12, 1, 8, 1>(p, stash, st);
+    return launch_fwd_any<typename ElemNet<B, Net5L128>::type, 1, 12, 1, 8, 1>(p, stash, st, info);
   if (dims_match<NetNarrow>(L, dims))
-    return launch_fwd_any<typename ElemNet<B, NetNarrow>::type, 2, 16, 1, 16, 1>(p, stash, st);
+    return launch_fwd_any<typename ElemNet<B, NetNarrow>::type, 2, 16, 1, 16, 1>(p, stash, st, info);
   if (fwd_generic_dims(L, dims)) {
     switch (L) {
       // At most 8 waves (4 for the 5-layer stash kernel): the runtime
       // strides cannot fold into immediate offsets, and the 12-wave kernels
       // (168 VGPRs) spill.
-      case 2: return launch_fwd_any<typename ElemNet<B, GNet2>::type, 1, 8, 1, 8, 1>(p, stash, st);
-      case 3: return launch_fwd_any<typename ElemNet<B, GNet3>::type, 1, 8, 1, 8, 1>(p, stash, st);
-      case 4: return launch_fwd_any<typename ElemNet<B, GNet4>::type, 1, 8, 1, 8, 1>(p, stash, st);
-      default: return launch_fwd_any<typename ElemNet<B, GNet5>::type, 1, 8, 1, 4, 1>(p, stash, st);
+      case 2: return launch_fwd_any<typename ElemNet<B, GNet2>::type, 1, 8, 1, 8, 1>(p, stash, st, info);
+      case 3: return launch_fwd_any<typename ElemNet<B, GNet3>::type, 1, 8, 1, 8, 1>(p, stash, st, info);
+      case 4: return launch_fwd_any<typename ElemNet<B, GNet4>::type, 1, 8, 1, 8, 1>(p, stash, st, info);
+      default: return launch_fwd_any<typename ElemNet<B, GNet5>::type, 1, 8, 1, 4, 1>(p, stash, st, info);
     }
   }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no forward kernel for these widths");
 }
 
-int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st) {
+int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, LaunchInfo* info) {
   int cus = 0;
   const int rc = current_device_cus(&cus);
   if (rc != MLPMK_OK) return rc;
   // Small batches run the feature-split kernel (fwd_split.hip) when it has one
   // for these widths and batch size.
-  const int rs = fwd_split_dispatch(L, dims, p, stash, bf, st, cus);
+  const int rs = fwd_split_dispatch(L, dims, p, stash, bf, st, cus, info);
   if (rs != MLPMK_ERR_UNSUPPORTED_SHAPE) return rs;
-  return bf ? fwd_dispatch_t<true>(L, dims, p, stash, st) : fwd_dispatch_t<false>(L, dims, p, stash, st);
+  return bf ? fwd_dispatch_t<true>(L, dims, p, stash, st, info) : fwd_dispatch_t<false>(L, dims, p, stash, st, info);
 }
 
 }  // namespace mlpmk

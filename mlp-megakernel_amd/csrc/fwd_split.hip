@@ -363,7 +363,7 @@ __global__ __launch_bounds__(Geo<N>::NWV * 64) void fwd_split_kernel(FwdParams p
 // ---------------------------------------------------------------------------
 
 template <class N, bool STASH>
-static int launch_split_t(const FwdParams& p, hipStream_t st) {
+static int launch_split_t(const FwdParams& p, hipStream_t st, LaunchInfo* info) {
   using G = fsplit::Geo<N>;
   constexpr int kMaxDev = 64;
   static int occ_cache[kMaxDev];  // 0 = unknown; benign race (idempotent value)
@@ -383,6 +383,10 @@ static int launch_split_t(const FwdParams& p, hipStream_t st) {
   const int64_t nblk = (p.M + 31) / 32;
   const int64_t cap = (int64_t)cus * occ;
   const int grid = (int)(nblk < cap ? nblk : cap);
+  if (info) {
+    *info = LaunchInfo{MLPMK_KERNEL_FEATURE_SPLIT, 32, G::NWV, grid, occ};
+    return MLPMK_OK;
+  }
   (void)hipGetLastError();
   hipLaunchKernelGGL((fsplit::fwd_split_kernel<N, STASH>), dim3(grid), dim3(G::NWV * 64), 0, st, p);
   e = hipGetLastError();
@@ -417,28 +421,30 @@ static bool split_dims_match(int L, const int* dims) {
 #endif
 
 template <class N>
-static int split_if_small(const FwdParams& p, bool stash, hipStream_t st, int cus, int per_cu) {
+static int split_if_small(const FwdParams& p, bool stash, hipStream_t st, int cus, int per_cu, LaunchInfo* info) {
   if ((p.M + 31) / 32 > (int64_t)per_cu * cus) return MLPMK_ERR_UNSUPPORTED_SHAPE;
-  return stash ? launch_split_t<N, true>(p, st) : launch_split_t<N, false>(p, st);
+  return stash ? launch_split_t<N, true>(p, st, info) : launch_split_t<N, false>(p, st, info);
 }
 
 // Launches the feature-split kernel when one exists for these widths and the
 // batch is small enough; otherwise returns MLPMK_ERR_UNSUPPORTED_SHAPE without
 // recording an error, and the caller runs fwd.hip's kernels.  B: bf16 tensors.
 template <bool B>
-static int fwd_split_dispatch_t(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus) {
+static int fwd_split_dispatch_t(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, int cus,
+                                LaunchInfo* info) {
   if (split_dims_match<SNet3L128>(L, dims))
-    return split_if_small<typename ElemNet<B, SNet3L128>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU_3L);
+    return split_if_small<typename ElemNet<B, SNet3L128>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU_3L, info);
   if (split_dims_match<SNet5L128>(L, dims))
-    return split_if_small<typename ElemNet<B, SNet5L128>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU);
+    return split_if_small<typename ElemNet<B, SNet5L128>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU, info);
   if (split_dims_match<SNetNarrow>(L, dims))
-    return split_if_small<typename ElemNet<B, SNetNarrow>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU);
+    return split_if_small<typename ElemNet<B, SNetNarrow>::type>(p, stash, st, cus, MLPMK_SPLIT_BLOCKS_PER_CU, info);
   return MLPMK_ERR_UNSUPPORTED_SHAPE;
 }
 
-int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus) {
-  return bf ? fwd_split_dispatch_t<true>(L, dims, p, stash, st, cus)
-            : fwd_split_dispatch_t<false>(L, dims, p, stash, st, cus);
+int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus,
+                       LaunchInfo* info) {
+  return bf ? fwd_split_dispatch_t<true>(L, dims, p, stash, st, cus, info)
+            : fwd_split_dispatch_t<false>(L, dims, p, stash, st, cus, info);
 }
 
 }  // namespace mlpmk

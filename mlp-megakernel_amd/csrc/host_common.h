@@ -21,4 +21,14 @@ int current_device_cus(int* cus);
 // current device; the caller caches it.
 int kernel_occupancy(const void* kernel, int threads, int* wgs_per_cu);
 
+// The launch a forward dispatcher makes.  Passed non-null, the dispatcher
+// fills it in and returns without launching (mlpmk_fwd_launch_info).
+struct LaunchInfo {
+  int kernel;          // MLPMK_KERNEL_PERSISTENT or MLPMK_KERNEL_FEATURE_SPLIT
+  int rows_per_block;  // rows of x per MFMA batch block
+  int waves;           // 64-lane waves per workgroup
+  int grid;            // workgroups
+  int wgs_per_cu;      // resident workgroups per CU (occupancy)
+};
+
 }  // namespace mlpmk

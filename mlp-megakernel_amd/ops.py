@@ -149,6 +149,25 @@ def fwd_into(x, weights, out, stash=None):
     return out
 
 
+KERNEL_NAMES = {-1: "none", 0: "persistent", 1: "feature_split"}
+
+
+def fwd_launch_info(dims, M, stash=False, dtype=torch.float16, device=None):
+    """The launch ``mlpmk_fwd`` makes for this shape on ``device`` (default:
+    the current one), from the library's own dispatch code, without
+    launching: ``{"kernel", "rows_per_block", "waves", "grid", "wgs_per_cu"}``
+    (``mlpmk_fwd_launch_info``)."""
+    lib = _lib.get()
+    pd, _k = _lib.int_array(list(dims))
+    info = (ctypes.c_int * 5)()
+    idx = torch.cuda.current_device() if device is None or device.index is None else device.index
+    with torch.cuda.device(idx):
+        rc = lib.mlpmk_fwd_launch_info(len(dims) - 1, pd, _elem_code(dtype), int(M), int(bool(stash)), info)
+    _check("mlpmk_fwd_launch_info", rc)
+    return {"kernel": KERNEL_NAMES[info[0]], "rows_per_block": info[1], "waves": info[2], "grid": info[3],
+            "wgs_per_cu": info[4]}
+
+
 def fwd(x, weights, stash=False, recompute=False):
     """Allocate ``out`` (and the fp32 stash when ``stash``) and run the forward.
 

@@ -6,7 +6,9 @@ forward, forward megakernel with stash, ``out.sum()``, backward megakernel
 with its partial-sum combine, weight-norm backward) and the inference
 launcher can be captured into one graph each.  Every replay here gets fresh
 inputs, eager work runs between replays, and each replay is checked against
-an eager copy of the model on the same inputs.
+an eager copy of the model on the same inputs and against the CPU oracle
+(outputs at atol = rtol = 1e-2; weight-norm gradients per entry within
+2e-2 |ref| + 2e-3 max|ref| and relative Frobenius 1e-2).
 
 With grids of 64 workgroups or more the backward reduces its partials in a
 fixed order, so eager and replayed gradients are bitwise equal; below that
@@ -14,11 +16,13 @@ fixed order, so eager and replayed gradients are bitwise equal; below that
 """
 import copy
 
+import numpy as np
 import pytest
 import torch
 
 import fused_mlp
 import kernel
+from oracle import mlp_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -34,6 +38,39 @@ def _eager_step(model, x):
     out = model(x)
     out.sum().backward()
     return out.detach().clone(), model.v_all.grad.clone(), model.g_all.grad.clone()
+
+
+def _oracle_wn_step(x, model):
+    """CPU oracle of one weight-norm training step (loss = out.sum()): the
+    forward on the fp16-rounded W = g v / ||v|| the kernels use, the
+    closed-form backward from the fp32 activations, the weight-norm chain
+    rule; returns out, dv_all, dg_all."""
+    dims = model.dims
+    xs = x.cpu().numpy()
+    w16, vs, gs = [], [], []
+    for i in range(len(dims) - 1):
+        v = model.v(i).detach().cpu().numpy()
+        g = model.g(i).detach().cpu().numpy()
+        w16.append(orc.wn_forward(v, g)[0].astype(np.float16))
+        vs.append(v)
+        gs.append(g)
+    out, hidden = orc.forward(xs, w16, return_hidden=True)
+    dws, _ = orc.backward(xs, w16, hidden, np.ones(dims[-1], np.float32), need_dx=False)
+    dv, dg = zip(*[orc.wn_backward(dws[i], vs[i], gs[i]) for i in range(len(vs))])
+    return out, np.concatenate([d.reshape(-1) for d in dv]), np.concatenate(dg)
+
+
+def _check_oracle(got, ref, what, grad):
+    got = got.detach().float().cpu().numpy().astype(np.float64)
+    ref = np.asarray(ref, np.float64)
+    if not grad:
+        ok, err, _ = orc.allclose_report(got, ref, 1e-2, 1e-2)
+        assert ok, f"{what}: max|err| {err}"
+        return
+    scale = np.abs(ref).max()
+    worst = np.max(np.abs(got - ref) - (2e-2 * np.abs(ref) + 2e-3 * scale))
+    frob = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert worst <= 0 and frob < 1e-2, f"{what}: worst excess {worst:.3g}, rel frob {frob:.3g}"
 
 
 def _same(got, ref, exact, what):
@@ -76,6 +113,10 @@ def test_whole_training_step_graph(m):
         assert torch.equal(got[0], ref[0]), f"replay {r}: out"
         _same(got[1], ref[1], exact, f"replay {r}: dv")
         _same(got[2], ref[2], exact, f"replay {r}: dg")
+        o_out, o_dv, o_dg = _oracle_wn_step(static_x, ref_model)
+        _check_oracle(got[0], o_out, f"replay {r}: out vs oracle", grad=False)
+        _check_oracle(got[1], o_dv, f"replay {r}: dv vs oracle", grad=True)
+        _check_oracle(got[2], o_dg, f"replay {r}: dg vs oracle", grad=True)
 
 
 def test_make_graphed_callables_training():
@@ -95,6 +136,10 @@ def test_make_graphed_callables_training():
         assert torch.equal(out.detach(), ref[0]), f"step {r}: out"
         assert torch.equal(model.v_all.grad, ref[1]), f"step {r}: dv"
         assert torch.equal(model.g_all.grad, ref[2]), f"step {r}: dg"
+        o_out, o_dv, o_dg = _oracle_wn_step(x, ref_model)
+        _check_oracle(out, o_out, f"step {r}: out vs oracle", grad=False)
+        _check_oracle(model.v_all.grad, o_dv, f"step {r}: dv vs oracle", grad=True)
+        _check_oracle(model.g_all.grad, o_dg, f"step {r}: dg vs oracle", grad=True)
 
 
 @pytest.mark.parametrize("m", [64, 4096, 65536])
@@ -113,3 +158,5 @@ def test_inference_launcher_graph(m):
         ref = kernel._fused_mlp_fwd(static_x.clone(), *ws)
         torch.cuda.synchronize()
         assert torch.equal(static_out, ref), f"replay {r}"
+        o_out = orc.forward(static_x.cpu().numpy(), [w.cpu().numpy() for w in ws])
+        _check_oracle(static_out, o_out, f"replay {r} vs oracle", grad=False)

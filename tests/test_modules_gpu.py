@@ -124,7 +124,7 @@ def test_module_inference_under_no_grad_and_dense_dout():
 
 
 def test_module_under_autocast_with_fp32_parameters():
-    # AMP: fp32 master weights, custom_fwd casts to fp16; grads come back fp32.
+    # AMP: fp32 master weights, fp16 autocast casts to fp16; grads come back fp32.
     torch.manual_seed(2)
     model = fused_mlp.FusedMLPSoftplus().cuda()
     x = torch.randn(1024, 128, device="cuda")
@@ -136,6 +136,92 @@ def test_module_under_autocast_with_fp32_parameters():
     for i, w in enumerate(model.weights):
         assert w.grad.dtype == torch.float32
         check_grad(w.grad.cpu().numpy(), ref_dws[i], f"AMP dW{i + 1}")
+
+
+class _RecordStash:
+    """Wraps ops.fwd (the autograd module's binding) and records the stash
+    argument of every forward launch."""
+
+    def __init__(self, monkeypatch):
+        import mlpmk.autograd as ag
+
+        self.calls = []
+        real = ops.fwd
+
+        def fwd(x, weights, stash=False, **kw):
+            self.calls.append(bool(stash))
+            return real(x, weights, stash=stash, **kw)
+
+        monkeypatch.setattr(ag.ops, "fwd", fwd)
+
+
+@pytest.mark.parametrize("wn", [False, True])
+@pytest.mark.parametrize("mode", ["no_grad", "inference_mode", "no_requires_grad"])
+def test_inference_writes_no_stash(monkeypatch, mode, wn):
+    # Module inference must launch the plain forward, not the training
+    # forward with its fp32 stash (0.5-1 GiB at 1M rows): under no_grad the
+    # parameters still require grad, so ctx.needs_input_grad inside
+    # Function.forward cannot tell.
+    torch.manual_seed(3)
+    cls = fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus
+    model = cls().cuda().half()
+    x = torch.randn(4096, 128, device="cuda").half()
+    ref = model(x).detach()  # training forward (parameters require grad)
+    rec = _RecordStash(monkeypatch)
+    if mode == "no_grad":
+        with torch.no_grad():
+            out = model(x)
+    elif mode == "inference_mode":
+        with torch.inference_mode():
+            out = model(x)
+    else:
+        for p_ in model.parameters():
+            p_.requires_grad_(False)
+        out = model(x)
+    assert rec.calls == [False], rec.calls
+    assert not out.requires_grad
+    assert torch.equal(out, ref)  # inference and training forwards agree bit for bit
+    model.zero_grad()
+    for p_ in model.parameters():
+        p_.requires_grad_(True)
+    rec.calls.clear()
+    model(x).sum().backward()
+    assert rec.calls == [True]
+
+
+@pytest.mark.parametrize("wn", [False, True])
+def test_module_under_bf16_autocast_runs_bf16_kernels(wn):
+    # torch.autocast(dtype=bfloat16): the bf16 kernels, not fp16 ones.
+    torch.manual_seed(4)
+    cls = fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus
+    model = cls().cuda()
+    x = torch.randn(2048, 128, device="cuda")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = model(x)
+        assert out.dtype == torch.bfloat16
+    out.float().sum().backward()
+    if wn:
+        ws = [w.detach() for w in _wn_weights(model)]
+    else:
+        ws = [w.detach() for w in model.weights]
+    xb = x.to(torch.bfloat16).float().cpu().numpy()
+    wb = [orc.to_bf16(w.float().cpu().numpy()) for w in ws]
+    ref = orc.forward(xb, wb, round_hidden=True, elem="bf16")
+    ok, err, _ = orc.allclose_report(out.detach().float().cpu().numpy(), ref, 3e-2, 3e-2)  # bf16 tolerance, test_bf16_gpu.py
+    assert ok, f"bf16 autocast out: {err}"
+    for p_ in model.parameters():
+        assert p_.grad is not None and p_.grad.dtype == torch.float32 and torch.isfinite(p_.grad).all()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        assert model(x).dtype == torch.bfloat16
+
+
+def _wn_weights(model):
+    """W_l = g v / ||v|| of a weight-norm module, fp32."""
+    ws = []
+    for i in range(len(model.dims) - 1):
+        v = model.v(i).float()
+        ws.append(model.g(i).float() * v / v.norm(dim=0, keepdim=True))
+    return ws
 
 
 def _torch_wn_ref(x16, v_all, g_all, dims):
