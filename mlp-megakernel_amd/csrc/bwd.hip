@@ -974,7 +974,16 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
   typedef typename ElemNet<B, GBNet2>::type G2;
   typedef typename ElemNet<B, GBNet3>::type G3;
   const int64_t we = weight_elems_of(L, dims);
-  if (bdims_match<BNet3L128>(L, dims)) return bwd_workspace_any<N3, 4>(M, dx, we, bytes);
+  if (bdims_match<BNet3L128>(L, dims)) {
+    int rc = bwd_workspace_any<N3, 4>(M, dx, we, bytes);
+    if (rc != MLPMK_OK || dx) return rc;
+    // Without dx the backward may also run in recompute mode (stash[1] NULL,
+    // decided per call), whose kernel has its own grid: size for the larger.
+    int64_t rcb = 0;
+    rc = partial_bytes<Recompute<N3>, 4, false>(M, we, &rcb);
+    if (rc == MLPMK_OK && rcb > *bytes) *bytes = rcb;
+    return rc;
+  }
   if (bdims_match<BNet5L128>(L, dims)) return bwd_split_workspace<N3, N2>(L, dims, M, dx, bytes);
   if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<NN, 4>(M, dx, we, bytes);
   if (bwd_generic_dims(L, dims)) {
@@ -998,8 +1007,7 @@ bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims
 // stash for h_2 (the forward then writes only h_1) the backward recomputes
 // h_2 from h_1 at the start of every round; no dx in that mode (the W_2
 // forward fragments take the LDS that dx's W_1 dgrad fragments would need).
-// Its grid equals the stashing no-dx kernel's (one 160 KiB workgroup per CU
-// against one 128 KiB one), so the workspace size is that kernel's.
+// The no-dx workspace size covers both kernels' grids (bwd_workspace_t).
 bool bwd_recompute_supported(int L, const int* dims) { return bdims_match<BNet3L128>(L, dims); }
 
 template <bool B>
