@@ -187,6 +187,33 @@ int mlpmk_bwd_ws(int num_layers, const int* dims, int dtype, const void* x, cons
                  const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
                  float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream);
 
+/* Size of the library-owned scratch array of mlpmk_bwd_noalloc (64 MiB per device). */
+#define MLPMK_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+/*
+ * mlpmk_bwd_ws without the workspace argument and without any allocation:
+ * the same kernels, with a library-owned device array of
+ * MLPMK_NOALLOC_SCRATCH_BYTES per device in place of the caller's workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree.
+ *   - Shapes whose workspace (mlpmk_bwd_workspace_size) exceeds
+ *     MLPMK_NOALLOC_SCRATCH_BYTES return MLPMK_ERR_UNSUPPORTED_SHAPE before
+ *     anything is launched: every 3-layer and 2-layer network at any M (the
+ *     partials take at most 48 MiB on MI355X), 4- and 5-layer networks up to
+ *     the M whose dz hand-over (M x 256 bytes) still fits (M = 65,536 for the
+ *     5-layer 128-wide network).
+ *   - Every call on a device shares that device's array, and calls that
+ *     overlap on one device (two streams) race; calls in one stream order are
+ *     safe.  The array keeps the last call's contents; nothing needs to start
+ *     at zero.
+ *   - The array's device address is looked up once per device, on the first
+ *     call on that device.
+ */
+int mlpmk_bwd_noalloc(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
+                      const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+                      float* const* dw, int64_t M, void* stream);
+
 /*
  * Bytes of workspace mlpmk_bwd_ws needs on the current device: one fp32 copy
  * of all dW blocks per workgroup of the backward grid, plus for the 5-layer

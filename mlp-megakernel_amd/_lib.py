@@ -34,6 +34,10 @@ SIGNATURES = {
         [c_int, P_INT, c_int, c_void_p, P_VOIDP, P_VOIDP, c_void_p, c_int64, c_void_p, P_VOIDP, c_void_p, c_int64,
          c_int64, c_void_p],
     ),
+    "mlpmk_bwd_noalloc": (
+        c_int,
+        [c_int, P_INT, c_int, c_void_p, P_VOIDP, P_VOIDP, c_void_p, c_int64, c_void_p, P_VOIDP, c_int64, c_void_p],
+    ),
     "mlpmk_bwd_workspace_size": (c_int, [c_int, P_INT, c_int, c_int64, c_int, ctypes.POINTER(c_int64)]),
     "mlpmk_wn_fwd": (c_int, [c_int, P_INT, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "mlpmk_wn_bwd": (

@@ -18,6 +18,7 @@ bool bwd_supported_dims(int L, const int* dims);
 bool bwd_recompute_supported(int L, const int* dims);
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st);
 int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, bool bf, int64_t* bytes);
+int scratch_workspace(void** ptr, int64_t* bytes);
 int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* v, const void* g, void* w_out,
                     float* inv_norm, hipStream_t st);
 int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const void* v, const void* g,
@@ -198,9 +199,12 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
   return MLPMK_OK;
 }
 
+// use_scratch: the workspace is the library's own scratch array
+// (mlpmk_bwd_noalloc), looked up after the arguments are validated.
 static int bwd_common(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
                       const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
-                      float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream) {
+                      float* const* dw, void* workspace, int64_t workspace_bytes, int64_t M, void* stream,
+                      bool use_scratch = false) {
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
   if ((rc = check_elem_dtype(dtype))) return rc;
@@ -248,11 +252,17 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
   p.dx = static_cast<_Float16*>(dx);
   p.M = M;
   for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
+  if (use_scratch && (rc = scratch_workspace(&workspace, &workspace_bytes))) return rc;
   if (workspace) {
     if ((rc = check_ptr(workspace, "workspace"))) return rc;
     int64_t need = 0;
     if ((rc = bwd_workspace_bytes(num_layers, dims, M, dx != nullptr, dtype == MLPMK_DTYPE_BF16, &need)))
       return rc;
+    if (use_scratch && need > workspace_bytes)
+      return fail(MLPMK_ERR_UNSUPPORTED_SHAPE,
+                  "M=%lld needs %lld bytes of workspace; mlpmk_bwd_noalloc's scratch holds %lld "
+                  "(MLPMK_NOALLOC_SCRATCH_BYTES): use mlpmk_bwd_ws with a larger workspace",
+                  (long long)M, (long long)need, (long long)workspace_bytes);
     if (workspace_bytes < need)
       return fail(MLPMK_ERR_INVALID_ARG, "workspace_bytes=%lld is below the %lld bytes needed",
                   (long long)workspace_bytes, (long long)need);
@@ -275,6 +285,14 @@ int mlpmk_bwd_ws(int num_layers, const int* dims, int dtype, const void* x, cons
   if (!workspace) return fail(MLPMK_ERR_INVALID_ARG, "workspace is NULL");
   return bwd_common(num_layers, dims, dtype, x, w, stash, dout, dout_row_stride, dx, dw, workspace,
                     workspace_bytes, M, stream);
+}
+
+int mlpmk_bwd_noalloc(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
+                      const float* const* stash, const void* dout, int64_t dout_row_stride, void* dx,
+                      float* const* dw, int64_t M, void* stream) {
+  g_last_error[0] = 0;
+  return bwd_common(num_layers, dims, dtype, x, w, stash, dout, dout_row_stride, dx, dw, nullptr, 0, M, stream,
+                    true);
 }
 
 int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t M, int with_dx, int64_t* bytes) {

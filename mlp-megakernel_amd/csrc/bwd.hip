@@ -45,6 +45,8 @@
 // one 64-byte window, the two half-waves (features f and f+8) land 128 bytes
 // apart, and the 16-byte fragment reads of 16 lanes (16 consecutive features,
 // same 8 rows) fall on 16 distinct chunks -- all bank-conflict free.
+#include <atomic>
+
 #include "device_common.h"
 #include "host_common.h"
 #include "params.h"
@@ -999,6 +1001,42 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
 
 int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, bool bf, int64_t* bytes) {
   return bf ? bwd_workspace_t<true>(L, dims, M, dx, bytes) : bwd_workspace_t<false>(L, dims, M, dx, bytes);
+}
+
+// Library-owned workspace of mlpmk_bwd_noalloc, for callers that cannot
+// allocate device memory (code under graph capture, serving loops, harnesses
+// that forbid hipMalloc): the same kernels as mlpmk_bwd_ws, with this array
+// in place of the caller's workspace.  Each device holds its own copy, at its
+// own address, until the process ends.  Every call on a device shares it and
+// leaves its contents behind; nothing in it needs to start at zero (every
+// partial-sum block and the dz hand-over are written in full before they
+// are read), and calls that overlap on one device (two streams) race.
+static __device__ __align__(256) char scratch[MLPMK_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` on the current device.  In host code the
+// array's name is only a stand-in for the symbol: the address comes from
+// hipGetSymbolAddress, looked up once per device (on the device's first
+// mlpmk_bwd_noalloc call, with that device current) and kept.
+int scratch_workspace(void** ptr, int64_t* bytes) {
+  constexpr int kMaxDev = 64;
+  static std::atomic<void*> addr[kMaxDev];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDev) return fail(MLPMK_ERR_NO_DEVICE, "device %d: at most %d devices", dev, kMaxDev);
+  void* a = addr[dev].load(std::memory_order_acquire);
+  if (!a) {
+    int cus = 0;
+    int rc = current_device_cus(&cus);  // a gfx950 device, or no code object to look in
+    if (rc != MLPMK_OK) return rc;
+    e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!a) return fail(MLPMK_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    addr[dev].store(a, std::memory_order_release);  // same value from every racing thread
+  }
+  *ptr = a;
+  *bytes = MLPMK_NOALLOC_SCRATCH_BYTES;
+  return MLPMK_OK;
 }
 
 bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims); }
