@@ -1,15 +1,26 @@
-"""Benchmark of the gfx950 fused softplus-MLP forward megakernel.
+"""Benchmark of the gfx950 fused softplus-MLP megakernels.
 
-Default workload (throughput point): 3-layer
+Headline (throughput point): the 3-layer
 D=H=OUT=128 fp16 forward at M = 1,048,576 rows, seeded synthetic inputs
 (x ~ N(0,1), W_l ~ N(0, 1/in)) resident in HBM before timing.  A "step" is one
 launch over the whole batch.  Two input/output buffer pairs alternate so the
-1 GiB working set cannot sit in the 256 MB Infinity Cache.
+1 GiB working set cannot sit in the 256 MB Infinity Cache.  ``value`` and
+``roofline`` come from the K timed launches (HIP events around them, after a
+0.1 s clock ramp and W warm-up launches); ``sustained`` repeats the
+measurement over >= 0.5 s of back-to-back launches.
 
-Prints ONE JSON line (the driver's contract) with the headline throughput,
-the roofline fraction of the forward kernel, and the CPU baseline (the numpy
-oracle on the host cores, bounded sample).  ``--config`` / ``--m`` select
-other BASELINE configs, ``--sweep`` adds the latency sweep M = 64..4096.
+Besides the headline the default run times every other BASELINE config (extra
+keys, each with the buffers it touches rotated past the Infinity Cache or
+labelled cache-resident): the 5-layer and narrow forwards, M = 65,536, the
+M = 64..4096 latency sweep (event timing, one-launch and 20-launch graph
+replays, and the replay floor of a one-workgroup kernel), and the
+weight-norm training step at M = 4096 / 16384 / 131072.  ``cpu_baseline`` is
+the reference's eager PyTorch path (kernel.py:163-171) in fp32 on the host
+cores; the numpy oracle's time is reported beside it.
+
+Prints ONE JSON line (the driver's contract).  ``--config`` / ``--m`` move the
+headline to another config, ``--no-extra`` skips the extra configs (for
+profiler runs), ``--train`` adds the longer training experiments.
 """
 import argparse
 import contextlib
@@ -152,7 +163,30 @@ def cpu_threads():
         return os.cpu_count() or 1
 
 
-def cpu_baseline(orc, dims, uniform, budget_s=10.0, chunk=65536):
+def cpu_model_name():
+    """The host CPU's model name (/proc/cpuinfo), as lscpu reports it."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def host_threads():
+    """Host threads for the CPU legs: the CPUs this process may run on, capped
+    by OMP_NUM_THREADS when set (the GPU box sets it to its CPU share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    return max(n, 1)
+
+
+def cpu_oracle_numpy(orc, dims, uniform, budget_s=5.0, chunk=65536):
     """The numpy oracle's forward (fp32, BLAS matmuls) on host cores over a
     bounded sample: repeated `chunk`-row batches until `budget_s` has elapsed."""
     x, ws = orc.make_inputs(dims, chunk, seed=7, x_dist="uniform" if uniform else "normal")
@@ -177,33 +211,133 @@ def cpu_baseline(orc, dims, uniform, budget_s=10.0, chunk=65536):
     }
 
 
-def torch_eager_cpu(torch, dims, uniform, budget_s=5.0, chunk=65536):
-    """The reference's eager math (kernel.py:168-171) in PyTorch on the CPU, fp32."""
-    g = torch.Generator().manual_seed(11)
-    x = (torch.rand((chunk, dims[0]), generator=g) * 2 - 1) if uniform else torch.randn((chunk, dims[0]), generator=g)
-    ws = [torch.randn((dims[i], dims[i + 1]), generator=g) / dims[i] ** 0.5 for i in range(len(dims) - 1)]
-    F = torch.nn.functional
+def cpu_eager_baseline(torch, dims, uniform, budget_s=10.0, chunk=65536):
+    """The reference's eager path on the host: ``Model.forward``
+    (kernel.py:163-171, softplus(x @ w1) -> softplus(. @ w2) -> . @ w3) in
+    PyTorch fp32 on the CPU, over repeated `chunk`-row batches of the
+    workload's shape until `budget_s` has elapsed."""
+    import kernel
 
-    def run():
-        a = x
-        for i, w in enumerate(ws):
-            a = a @ w
-            if i < len(ws) - 1:
-                a = F.softplus(a)
-        return a
+    threads = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g = torch.Generator().manual_seed(11)
+        x = (torch.rand((chunk, dims[0]), generator=g) * 2 - 1) if uniform else torch.randn((chunk, dims[0]), generator=g)
+        ws = [torch.randn((dims[i], dims[i + 1]), generator=g) / dims[i] ** 0.5 for i in range(len(dims) - 1)]
+        F = torch.nn.functional
+        model = kernel.Model()
 
-    run()
-    rows, reps, t0 = 0, 0, time.perf_counter()
-    while True:
-        run()
-        rows += chunk
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s and reps >= 2:
-            break
-    return {"value": rows / el, "unit": "rows/s", "threads": torch.get_num_threads(), "sample": f"{reps} x {chunk} rows fp32"}
+        def run():
+            if len(ws) == 3:
+                return model(x, *ws)
+            a = x  # the same chain for other depths
+            for i, w in enumerate(ws):
+                a = a @ w
+                if i < len(ws) - 1:
+                    a = F.softplus(a)
+            return a
+
+        with torch.no_grad():
+            run()
+            rows, reps, t0 = 0, 0, time.perf_counter()
+            while True:
+                run()
+                rows += chunk
+                reps += 1
+                el = time.perf_counter() - t0
+                if el >= budget_s and reps >= 2:
+                    break
+    finally:
+        torch.set_num_threads(prev)
+    return {
+        "value": rows / el,
+        "unit": "rows/s",
+        "cores": threads,
+        "kind": "reference",
+        "cpu": cpu_model_name(),
+        "sample": f"the reference's eager Model.forward (kernel.py:163-171) in PyTorch fp32 on {threads} host "
+        f"threads, {reps} x {chunk} rows of the same widths in {el:.1f} s",
+    }
 
 
+def fwd_bench(torch, ops, dims, m, uniform, steps=200, warmup=20, dtype=None):
+    """Forward launches of one config, buffers rotated so that the inputs and
+    outputs they touch exceed the 256 MB Infinity Cache (>= 512 MB in
+    total, at least two pairs): ms per launch (HIP events around `steps`
+    launches after a 0.1 s clock ramp), rows/s, roofline fraction."""
+    dtype = dtype or torch.float16
+    per_pair = m * (dims[0] + dims[-1]) * 2
+    pairs = max(2, -(-(512 << 20) // per_pair))
+    xs, ws = [], None
+    for k in range(pairs):
+        x, w = make_device_inputs(torch, dims, m, seed=k, uniform=uniform)
+        xs.append(x.to(dtype))
+        ws = ws or [t.to(dtype) for t in w]
+    outs = [torch.empty((m, dims[-1]), device="cuda", dtype=dtype) for _ in range(pairs)]
+
+    def step(i):
+        ops.fwd_into(xs[i % pairs], ws, outs[i % pairs])
+
+    with gc_paused():
+        ramp_clock(torch, step)
+        ms = time_launches(torch, step, steps, warmup)
+    nbytes, nflops = algorithmic(dims, m)
+    ai = nflops / nbytes
+    hbm_bound = HBM_PEAK_GBS * ai / 1e3 < MFMA_F16_PEAK_TFLOPS
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = nflops / (ms * 1e-3) / 1e12
+    info = ops.fwd_launch_info(dims, m)
+    del xs, outs
+    return {
+        "ms_per_step": round(ms, 5),
+        "rows_per_s": round(m / (ms * 1e-3), 1),
+        "achieved_gbs": round(gbs, 1),
+        "tflops": round(tflops, 1),
+        "bound": "hbm" if hbm_bound else "mfma",
+        "roofline_frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "buffers": f"{pairs} rotating x/out pairs, {pairs * per_pair / 2**20:.0f} MiB",
+        "launch": info,
+    }
+
+
+def latency_sweep(torch, ops, dims, sizes=(64, 128, 256, 512, 1024, 2048, 4096)):
+    """BASELINE configs[1]'s latency sweep: per M, HIP-event time of 200
+    back-to-back launches (host dispatch included), the median of one-launch
+    graph replays (/root/reference/profile.py:50-80), and 20-launch graph
+    replays (launch latency shared); plus the replay floor of a one-workgroup
+    kernel (a 16-byte copy) under the same two replay methods.  Buffers are
+    L2/MALL-resident at these sizes (at most 2 MiB): the figures are
+    launch-latency-bound, not bandwidth measurements."""
+    res = {}
+    for m in sizes:
+        x, ws = make_device_inputs(torch, dims, m, seed=0, uniform=False)
+        o = torch.empty((m, dims[-1]), device="cuda", dtype=torch.float16)
+        fn = lambda i: ops.fwd_into(x, ws, o)  # noqa: E731
+        with gc_paused():
+            ev = time_launches(torch, fn, 200, 20)
+            g1 = time_graph(torch, fn)
+            g20 = time_graph(torch, fn, iters=50, per_graph=20)
+        res[str(m)] = {"event_ms": round(ev, 5), "graph1_ms": round(g1, 5), "graph20_ms_per_launch": round(g20, 5),
+                       "rows_per_s": round(m / (min(ev, g1, g20) * 1e-3), 1),
+                       "kernel": ops.fwd_launch_info(dims, m)["kernel"]}
+    src = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    fn = lambda i: ops.copy_bytes(src, dst)  # noqa: E731
+    with gc_paused():
+        res["floor_one_workgroup_kernel"] = {"graph1_ms": round(time_graph(torch, fn), 5),
+                                             "graph20_ms_per_launch": round(time_graph(torch, fn, iters=50, per_graph=20), 5)}
+    res["note"] = "cache-resident (<= 2 MiB per M): launch-latency-bound sizes"
+    return res
+
+
+def sustained(torch, step, ms_hint, seconds=0.6):
+    """ms per launch over >= `seconds` of back-to-back launches (one HIP-event
+    pair around all of them), right after the burst measurement."""
+    n = max(int(seconds / (ms_hint * 1e-3)), 100)
+    with gc_paused():
+        ms = time_launches(torch, step, n, 0)
+    return ms, n
 
 
 def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, dtype=None):
@@ -231,33 +365,40 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
     model = fused_mlp.FusedMLPSoftplusWN(n_layers=n_layers).cuda()
     dims = tuple(model.dims)
     rc = mag._use_recompute(dims, m, False)
-    x = torch.randn(m, 128, device="cuda").to(dtype)  # bf16 x runs the bf16 kernels
+    # Steps rotate over nx inputs (up to 256 MB of x, at most 8 buffers) so
+    # that x is not re-read from the Infinity Cache; the stash a step's
+    # forward writes is read back by the same step's backward, as in training.
+    nx = min(8, max(1, -(-(256 << 20) // (m * 256))))
+    xs = [torch.randn(m, 128, device="cuda").to(dtype) for _ in range(nx)]  # bf16 x runs the bf16 kernels
 
-    def step(_):
+    def step(i):
         model.v_all.grad = None
         model.g_all.grad = None
-        model(x).sum().backward()
+        model(xs[i % nx]).sum().backward()
 
     with gc_paused():
         ramp_clock(torch, step, seconds=0.2)
         ms = time_launches(torch, step, steps, warmup)
 
-    # The same step captured whole into one HIP graph (the library allocates
-    # nothing and records no memset); a replay costs launch latency plus the
-    # kernels, no Python or autograd dispatch.
+    # The same step captured whole into one HIP graph per input (the library
+    # allocates nothing and records no memset); a replay costs launch latency
+    # plus the kernels, no Python or autograd dispatch.
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for i in range(3):
             step(i)
     torch.cuda.current_stream().wait_stream(side)
-    model.v_all.grad = None
-    model.g_all.grad = None
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        model(x).sum().backward()
+    graphs = []
+    for k in range(nx):
+        model.v_all.grad = None
+        model.g_all.grad = None
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            model(xs[k]).sum().backward()
+        graphs.append(g)
     with gc_paused():
-        gms = time_launches(torch, lambda i: graph.replay(), steps, warmup)
+        gms = time_launches(torch, lambda i: graphs[i % nx].replay(), steps, warmup)
     # per row: x + out + stash written in the forward; dout, stash, x read
     # back (no dx).  Flops: forward 2*sum(in*out), dgrad of layers 1.., wgrad
     # (+ the recomputed layer).
@@ -271,8 +412,10 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
         "tflops": round(flop * m / (ms * 1e-3) / 1e12, 2),
         "graph_ms_per_step": round(gms, 5),
         "graph_rows_per_s": m / (gms * 1e-3),
+        "graph_roofline_frac": round(nbytes * m / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd" if n_layers == 3 else
                     "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..2, then 1..0) + wn_bwd",
+        "x_buffers": nx,
         "recompute_h_last": rc,
         "dtype": str(dtype).replace("torch.", ""),
     }
@@ -361,10 +504,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", choices=sorted(CONFIG_DIMS), default="3l128")
     ap.add_argument("--m", type=int, default=None)
-    ap.add_argument("--sweep", action="store_true", help="add the M=64..4096 latency sweep")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="headline only: skip the other BASELINE configs, the sweep and the training step")
     ap.add_argument("--train", action="store_true",
-                    help="add the training step (3L + weight norm, loss = out.sum()) at M = 4096, 16384, 131072, "
-                         "and the 5-layer one at M = 65536, 131072")
+                    help="add the longer training experiments (5-layer step, bf16, stash vs recompute, "
+                         "the reference's PyTorch-op backward)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     args = ap.parse_args()
@@ -411,25 +555,34 @@ def main():
         1e-2,
     )
 
-    # --- timed region -------------------------------------------------------
+    # --- timed region: the K launches of the contract ----------------------
     with gc_paused():
         ramp_clock(torch, step)
         ms = time_launches(torch, step, args.steps, args.warmup)
+    # the same launches sustained for >= 0.5 s, right after
+    sus_ms, sus_n = sustained(torch, step, ms)
     nbytes, nflops = algorithmic(dims, m)
     achieved_gbs = nbytes / (ms * 1e-3) / 1e9
     tflops = nflops / (ms * 1e-3) / 1e12
     ai = nflops / nbytes
     roof_tflops = min(MFMA_F16_PEAK_TFLOPS, HBM_PEAK_GBS * ai / 1e3)
     bound = "hbm" if HBM_PEAK_GBS * ai / 1e3 < MFMA_F16_PEAK_TFLOPS else "mfma"
+
+    def frac_of(t_ms):
+        if bound == "hbm":
+            return nbytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+        return nflops / (t_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS
+
     if bound == "hbm":
         roofline = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved_gbs / HBM_PEAK_GBS, 4)}
+                    "frac": round(frac_of(ms), 4)}
     else:
         roofline = {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+                    "frac": round(frac_of(ms), 4)}
     roofline["traffic"] = load_traffic(workload)
     roofline["kernel"] = "mlpmk::fwd_kernel"
     roofline["algorithmic_bytes_per_launch"] = nbytes
+    roofline["timed_over"] = f"the {args.steps} timed launches (HIP events); 'sustained' has the >= 0.5 s figure"
 
     # The same workload with bf16 tensors (the bf16 instantiation of the
     # kernel; a secondary figure, the metric stays the fp16 one).
@@ -441,10 +594,12 @@ def main():
         bf16_ms = time_launches(torch, lambda i: ops.fwd_into(xb[i & 1], wb, ob[i & 1]), args.steps, args.warmup)
     del xb, wb, ob
 
-    # achievable-HBM reference: the library's 16-byte copy over 512 MiB
+    # achievable-HBM reference: the library's 16-byte copy over 512 MiB with
+    # the forward's cache policy (default loads, non-temporal stores)
     src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     with gc_paused():
+        ramp_clock(torch, lambda i: ops.copy_bytes(src, dst), 0.05)
         cms = time_launches(torch, lambda i: ops.copy_bytes(src, dst), 20, 5)
     copy_gbs = 2 * src.numel() / (cms * 1e-3) / 1e9
     del src, dst
@@ -464,35 +619,31 @@ def main():
         "data": "synthetic (seeded N(0,1) x, N(0,1/in) fp16 weights, resident in HBM)",
         "config": {"workload": workload, "dims": list(dims), "M": m, "parallelism": "none (1 GPU)"},
         "roofline": roofline,
+        "sustained": {"ms_per_step": round(sus_ms, 5), "launches": sus_n, "seconds": round(sus_ms * sus_n / 1e3, 3),
+                      "roofline_frac": round(frac_of(sus_ms), 4)},
         "tflops": round(tflops, 2),
         "roofline_tflops": round(roof_tflops, 1),
         "frac_of_min_mfma_hbm_roofline": round(tflops / roof_tflops, 4),
         "copy_kernel_gbs": round(copy_gbs, 1),
+        "copy_kernel": "512 MiB, 16-byte default loads + non-temporal stores (the forward's policy)",
         "bf16_ms_per_step": round(bf16_ms, 5),
         "parity": {"ok": ok, "max_abs_err": maxerr, "atol": 1e-2, "rtol": 1e-2, "rows_checked": 4096},
         "device": torch.cuda.get_device_properties(0).name,
+        "launch": ops.fwd_launch_info(dims, m),
     }
 
-    if args.sweep:
-        # BASELINE configs 2 and 3: the M = 64..4096 latency sweep and the
-        # M = 65,536 throughput point (3-layer), M = 65,536 (5-layer).
-        sweep_ms = (64, 128, 256, 512, 1024, 2048, 4096, 65536) if args.config == "3l128" else (65536,)
-        sweep = {}
-        for ms_m in sweep_ms:
-            xx, ww = make_device_inputs(torch, dims, ms_m, seed=0, uniform=uniform)
-            oo = torch.empty((ms_m, dims[-1]), device="cuda", dtype=torch.float16)
-            with gc_paused():
-                ev = time_launches(torch, lambda i: ops.fwd_into(xx, ww, oo), 200, 20)
-                gr = time_graph(torch, lambda i: ops.fwd_into(xx, ww, oo))
-                gr20 = time_graph(torch, lambda i: ops.fwd_into(xx, ww, oo), iters=50, per_graph=20)
-            best = min(ev, gr, gr20)
-            sweep[str(ms_m)] = {"event_ms": round(ev, 5), "graph_ms": round(gr, 5),
-                                "graph20_ms_per_launch": round(gr20, 5),
-                                "rows_per_s": round(ms_m / (best * 1e-3), 1)}
-        result["latency_sweep"] = sweep
+    if not args.no_extra:
+        # The other BASELINE configs, each timed here too.
+        result["configs"] = {
+            "3l128 M=65536": fwd_bench(torch, ops, CONFIG_DIMS["3l128"], 65536, False),
+            "5l128 M=65536": fwd_bench(torch, ops, CONFIG_DIMS["5l128"], 65536, False),
+            "5l128 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["5l128"], 1048576, False),
+            "narrow M=4194304": fwd_bench(torch, ops, CONFIG_DIMS["narrow"], 4194304, True),
+        }
+        result["latency_sweep"] = latency_sweep(torch, ops, CONFIG_DIMS["3l128"])
+        result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
 
     if args.train:
-        result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
         result["training_5l"] = {str(mt): train_step_bench(torch, mt, n_layers=5) for mt in (65536, 131072)}
         result["training_bf16"] = {str(mt): train_step_bench(torch, mt, steps=20, warmup=5, dtype=torch.bfloat16)
                                    for mt in (16384, 131072)}
@@ -503,8 +654,8 @@ def main():
                                                   for mt in (4096, 32768, 131072, 1048576)}
 
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(orc, dims, uniform, budget_s=args.cpu_budget)
-        result["cpu_eager_torch_fp32"] = torch_eager_cpu(torch, dims, uniform, budget_s=args.cpu_budget / 2)
+        result["cpu_baseline"] = cpu_eager_baseline(torch, dims, uniform, budget_s=args.cpu_budget)
+        result["cpu_oracle_numpy"] = cpu_oracle_numpy(orc, dims, uniform, budget_s=args.cpu_budget / 2)
     else:
         result["cpu_baseline"] = None
 

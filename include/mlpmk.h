@@ -251,10 +251,12 @@ int mlpmk_wn_bwd(int num_layers, const int* dims, int param_dtype, const float* 
                  const void* g, const float* inv_norm, void* dv, void* dg, void* stream);
 
 /*
- * Diagnostic: a plain streaming copy of `bytes` bytes (multiple of 16) with the
- * same 128-bit load/store width as the megakernels.  Used only to calibrate
- * hardware byte counters (FETCH_SIZE / WRITE_SIZE) against a known size.  No
- * counterpart in the reference.
+ * Diagnostic: a streaming copy of `bytes` bytes (multiple of 16) with the same
+ * 128-bit load/store width and cache policy as the forward megakernel's x and
+ * out traffic (default loads, non-temporal stores).  Used to calibrate
+ * hardware byte counters (FETCH_SIZE / WRITE_SIZE) against a known size and
+ * as the benchmark's achievable-HBM reference.  No counterpart in the
+ * reference.
  */
 int mlpmk_copy(const void* src, void* dst, int64_t bytes, void* stream);
 

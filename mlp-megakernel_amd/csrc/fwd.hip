@@ -20,8 +20,10 @@
 //    W_L by ln(2), hidden layers chain with no scaling at all (ln2 and log2e
 //    cancel between W^T h' and the next exp2), so the epilogue is exp2, add,
 //    log2 per element in fp32 and one pack per pair (see sp2); overflow is
-//    detected one layer later by a class test of one accumulator per row.
-//    The stash stores natural-unit h = ln2 * h' in fp32.
+//    detected one layer later by a class test of one accumulator per row
+//    (networks of up to 3 layers) or by a running maximum of the packed
+//    activations (deeper ones).  The stash stores natural-unit h = ln2 * h'
+//    in fp32.
 //  * Each layer is software-pipelined by 32-feature output block: the MFMA
 //    chain of block mb+1 is issued ahead of block mb's activation, so the
 //    matrix core and the VALU work concurrently within one wave.
@@ -383,25 +385,32 @@ __device__ __forceinline__ void chain(f32x16 (&acc)[NB], Frags<KSM>& f, const T 
 // Halving (and doubling every later accumulator, kIn) keeps the whole range;
 // both are exact power-of-two scalings.
 //
-// Overflow detection by propagation: every accumulator of a row in layer
-// l >= 1 sums that row's whole input vector, and a product with an infinite
-// or NaN operand is infinite or NaN whatever the weight (inf * 0 = NaN), so
-// one non-finite input makes every accumulator of the row non-finite.  A
-// finite input row keeps the fp32 accumulators finite (at most 128 products
-// of fp16 magnitudes, far below the fp32 range).  Testing one accumulator
-// per row and layer -- element 0 of output block 0, which every lane holds
-// for its row -- therefore detects every overflow and NaN of the layer
-// below: one class test per lane and layer instead of folding every packed
-// activation into a running maximum (33 v_pk_maximum3_f16 per 32-row block
-// of the 3-layer network).  Layer 0's inputs are the caller's x, and a
-// non-finite x also triggers the exact pass, which reproduces it.
+// Overflow detection by propagation (networks of up to 3 layers): every
+// accumulator of a row in layer l >= 1 sums that row's whole input vector,
+// and a product with an infinite or NaN operand is infinite or NaN whatever
+// the weight (inf * 0 = NaN), so one non-finite input makes every
+// accumulator of the row non-finite.  A finite input row keeps the fp32
+// accumulators finite (at most 128 products of fp16 magnitudes, far below
+// the fp32 range).  Testing one accumulator per row and layer -- element 0 of
+// output block 0, which every lane holds for its row -- therefore detects
+// every overflow and NaN of the layer below: one class test per lane and
+// layer instead of folding every packed activation into a running maximum
+// (33 v_pk_maximum3_f16 per 32-row block of the 3-layer network; 3L-128 at
+// 1M rows 129.4 -> 126.2 us, narrow at 4M 120.1 -> 116.6 us).  Layer 0's
+// inputs are the caller's x, and a non-finite x also triggers the exact
+// pass, which reproduces it.  The 4- and 5-layer kernels, bound by the
+// matrix core rather than by VALU issue, keep the running maximum `m`
+// (sp2_track): without it the scheduler spilled in their hot loop.
+template <class N>
+constexpr bool kPropagate = N::L <= 3;
+
 template <class N, int l, int NB, bool STASH, bool STAGE, bool EXACT, int KSM>
 __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[NB], int mb,
-                                         f16x8 (&nxt)[KSM][NB], bool& bad, int lane) {
+                                         f16x8 (&nxt)[KSM][NB], bool& bad, f16x2& m, int lane) {
   constexpr int Nout = N::d[l + 1];
   constexpr bool LAST = (l == N::L - 1);
   const int n = lane & 31, g = lane >> 5;
-  if constexpr (!EXACT && l > 0) {
+  if constexpr (!EXACT && kPropagate<N> && l > 0) {
     if (mb == 0) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) bad = bad || !__builtin_isfinite(acc[nb][0]);
@@ -462,10 +471,16 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       }
       f16x8 lo = pack8<N::bf>(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7]);
       f16x8 hi = pack8<N::bf>(q[8], q[9], q[10], q[11], q[12], q[13], q[14], q[15]);
-      // Ordering anchor (no instruction): the stash kernels keep more values
-      // live per step, and without an anchor the scheduler interleaved
-      // consecutive epilogues far enough to spill.
-      if constexpr (STASH) asm volatile("" : "+v"(lo), "+v"(hi));
+      if constexpr (!EXACT && !kPropagate<N>) m = sp2_track<!STASH>(m, lo, hi);
+      // Ordering anchor (no instruction) where the running maximum is gone:
+      // keeps the packed activations of consecutive epilogues in program
+      // order, as the maximum's dependence chain did.  Without either, the
+      // scheduler interleaved consecutive epilogues far enough that the
+      // stash kernels spilled (and the 5-layer inference kernel waited on its
+      // fragment reads: 209 -> 312 us at 1M rows).  The exact pass spills
+      // with it; the narrow network's two-block kernel (NB = 2) is faster
+      // without it (116.6 vs 120.7 us at 4M rows).
+      if constexpr (!EXACT && kPropagate<N> && NB == 1) asm volatile("" : "+v"(lo), "+v"(hi));
       if constexpr (STASH && N::gen) {
         // Runtime hidden width HW (a multiple of 16): feature groups past it are dropped.
         const rsrc_t sr = io.stash[l];
@@ -534,7 +549,8 @@ struct Chain {
   f16x8 b0[KSM][NB], b1[KSM][NB];  // hidden activations, ping-pong between layers
   f32x16 acc[2][NB];             // accumulators of the current and the next step
   Frags<KSM> fr;                 // fragments of the next chain to issue
-  bool bad;                      // some row's accumulator of layer >= 1 was not finite
+  bool bad;                      // some row's accumulator of layer >= 1 was not finite (kPropagate)
+  f16x2 ovf;                     // running maximum of the block's packed sp2 values (!kPropagate)
   f16x8 rf;                      // register-resident fragment (LdsPlan::reg_frags)
 
   // Layer l reads x (l = 0), b0 (odd l) or b1 (even l >= 2) and writes b0
@@ -585,7 +601,7 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
     MLPMK_SCHED_FENCE();
     load_block_x<N, NB>(c.xa, p, next * ROWS, lane);
   }
-  epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.bad, lane);
+  epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.bad, c.ovf, lane);
   if constexpr (l == N::L - 1 && STAGE) {
     if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
   }
@@ -599,8 +615,8 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
 // One row block: the whole layer chain, stores, and the x refill for block
 // `next`.  On entry c.xa holds the block's x rows and c.fr the fragments of
 // step 0; on exit they hold the same for block `next`.  Returns (wave-
-// uniform) whether some row of the fast form met a non-finite accumulator in
-// a layer >= 1: an overflowed or NaN activation below it (see epilogue).
+// uniform) whether the fast form overflowed or met a NaN somewhere in the
+// block (see epilogue).
 template <class N, int NB, bool STASH, bool STAGE, bool EXACT, int KSM, int RF>
 __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
                                           int lane_off, i32x4* stage, int64_t b, int64_t next, int lane) {
@@ -610,10 +626,13 @@ __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>&
   io.stage = stage;
   const FragBase<N, RF> fb(lds_b, lane_off);
   c.bad = false;
+  c.ovf = f16x2{};
   chain<N, T1, RF, 0, N::ks(0), NB>(c.acc[0], c.fr, c.xa, fb, c.rf);
   load_frags<N, T1, KSM, RF, N::ks(0)>(c.fr, fb, c.rf);
   step<N, 0, NB, STASH, STAGE, EXACT, KSM, RF>(p, io, c, fb, next, lane);
-  return !EXACT && __builtin_amdgcn_ballot_w64(c.bad) != 0;
+  if constexpr (EXACT) return false;
+  else if constexpr (kPropagate<N>) return __builtin_amdgcn_ballot_w64(c.bad) != 0;
+  else return sp2_overflowed<N::bf>(c.ovf);
 }
 
 // Block b with the fast softplus form, then -- only if one of its wave's rows

@@ -223,13 +223,15 @@ int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const vo
 }
 
 // ---------------------------------------------------------------------------
-// Calibration copy: 16-byte loads/stores, grid-stride, same access width as the
-// megakernels.  Used only to scale FETCH_SIZE / WRITE_SIZE counters.
+// Calibration copy: 16-byte loads/stores, grid-stride, the access width and
+// cache policy of the forward megakernel's x and out traffic (default loads,
+// non-temporal stores).  Used to scale FETCH_SIZE / WRITE_SIZE counters and as
+// the achievable-HBM reference of the benchmark.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void copy_kernel(const f32x4* __restrict__ src, f32x4* __restrict__ dst,
                                                    int64_t n16) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
-    dst[i] = src[i];
+    __builtin_nontemporal_store(src[i], &dst[i]);
 }
 
 int copy_dispatch(const void* src, void* dst, int64_t bytes, hipStream_t st) {
