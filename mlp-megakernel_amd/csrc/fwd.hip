@@ -186,6 +186,97 @@ __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
   }
 }
 
+// stage_weights in two phases -- every weight load, then (after the caller
+// has issued other loads) every LDS write -- for the persistent kernels,
+// which request each wave's first x rows in between.  The LDS writes then
+// wait for the weight loads only, not for the 24 MB of first x blocks that
+// the whole chip requests at kernel start (3L-128 at 1M rows: the
+// workgroup barrier after staging passed at ~7 us with the x rows requested
+// first, since the weight loads queued behind them).  Same values as
+// stage_weights.
+template <class N, int NT, int RF>
+struct SplitStaging {
+  static constexpr int TOTAL = StageTasks<N>::total();
+  static constexpr bool kTasks = TOTAL >= NT && !N::gen;
+  static constexpr int TPT = kTasks ? (TOTAL + NT - 1) / NT : 1;
+  // Column gathers (too few tasks for every thread): per layer, this thread's
+  // items item = threadIdx.x + k * NT, k < kSlots(l).
+  static constexpr int kSlots(int l) { return (N::mbs(l) * N::ks(l) * 64 + NT - 1) / NT; }
+  static constexpr int kSlotOff(int l) {
+    int o = 0;
+    for (int i = 0; i < l; ++i) o += kSlots(i);
+    return o;
+  }
+  static constexpr int kGather = kTasks ? 1 : kSlotOff(N::L);
+  static_assert(!N::gen, "runtime-width networks stage in one phase");
+  f16x8 r[TPT][8];   // task rows (kTasks)
+  f16x8 g[kGather];  // raw gathered fragment lanes, unscaled (!kTasks)
+
+  __device__ __forceinline__ void load(const FwdParams& p) {
+    if constexpr (kTasks) {
+#pragma unroll
+      for (int k = 0; k < TPT; ++k) {
+        const int t = threadIdx.x + k * NT;
+        if (TOTAL % NT == 0 || t < TOTAL) stage_load_any<N, 0>(p, r[k], t);
+      }
+    } else {
+      load_layers<0>(p);
+    }
+  }
+  __device__ __forceinline__ void store(f16x8* lds) {
+    if constexpr (kTasks) {
+#pragma unroll
+      for (int k = 0; k < TPT; ++k) {
+        const int t = threadIdx.x + k * NT;
+        if (TOTAL % NT == 0 || t < TOTAL) stage_store_any<N, 0, RF>(lds, r[k], t);
+      }
+    } else {
+      store_layers<0>(lds);
+    }
+  }
+
+ private:
+  // The lanes weight_fragment() gathers, before its scaling.
+  template <int l>
+  __device__ __forceinline__ void load_layers(const FwdParams& p) {
+    if constexpr (l < N::L) {
+      constexpr int KS = N::ks(l), Nout = N::d[l + 1], items = N::mbs(l) * KS * 64;
+#pragma unroll
+      for (int k = 0; k < kSlots(l); ++k) {
+        const int item = threadIdx.x + k * NT;
+        f16x8 v = {};
+        const int f = item >> 6, lane = item & 63;
+        const int mb = f / KS, st = f % KS, of = outfeat(mb, lane & 31);
+        if (item < items && of < Nout) {
+          const f16* src = p.w[l] + (int64_t)(16 * st + 8 * (lane >> 5)) * Nout + of;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = src[(int64_t)j * Nout];
+        }
+        g[kSlotOff(l) + k] = v;
+      }
+      load_layers<l + 1>(p);
+    }
+  }
+  template <int l>
+  __device__ __forceinline__ void store_layers(f16x8* lds) {
+    if constexpr (l < N::L) {
+      constexpr int items = N::mbs(l) * N::ks(l) * 64;
+#pragma unroll
+      for (int k = 0; k < kSlots(l); ++k) {
+        const int item = threadIdx.x + k * NT;
+        const int f = item >> 6, lane = item & 63;
+        if (item < items && N::frag_off(l) + f >= RF) {
+          f16x8 v;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = scaled_weight<N::bf>(g[kSlotOff(l) + k][j], wscale<N>(l));
+          lds[(N::frag_off(l) + f - RF) * 64 + lane] = v;
+        }
+      }
+      store_layers<l + 1>(lds);
+    }
+  }
+};
+
 // Per-block view of the row-major tensors: buffer resources clipped to the
 // block's valid rows, so loads of tail rows read zeros and their stores drop.
 struct BlockIO {
@@ -684,21 +775,28 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   const int64_t G = gridDim.x;
   // Wave w's first block is the workgroup's w-th (static); later blocks are
   // claimed from the counter, which starts past the first NW.  The persistent
-  // kernels (more than 8 waves) request the first block's x rows before the
-  // weight staging (5L-128 at 1M rows: 315 -> 203 us in separate-process
-  // runs; 3L-128 unchanged); the 4- and 8-wave kernels of smaller batches
-  // request them after it (M = 65536: 11.7 / 19.3 us against 12.8 / 21.7 us
-  // with the early request, 3L / 5L).  Past the end a block's resource is
-  // empty: reads zeros.
+  // kernels (more than 8 waves) request the first block's x rows between the
+  // weight loads and the weight LDS writes of the staging (SplitStaging;
+  // requesting them after the staging: 5L-128 at 1M rows 315 us against
+  // 203 us); the 4- and 8-wave kernels of smaller batches request them
+  // after it (M = 65536: 11.7 / 19.3 us against 12.8 / 21.7 us with the
+  // early request, 3L / 5L).  Past the end a block's resource is empty:
+  // reads zeros.
   static_assert(D == 1, "one block of x rows in flight per wave");
   constexpr bool kEarlyX = NW > 8;
   Chain<N, NB, KSM> c;
   const int64_t b0 = (int64_t)blockIdx.x + (int64_t)wid * G;
-  if constexpr (kEarlyX) load_block_x<N, NB>(c.xa, p, b0 * ROWS, lane);
   if constexpr (CLAIM) {
     if (threadIdx.x == 0) *claim_ctr = NW;
   }
-  stage_weights<N, NW * 64, RF>(p, lds);
+  if constexpr (kEarlyX) {
+    SplitStaging<N, NW * 64, RF> sw;
+    sw.load(p);
+    load_block_x<N, NB>(c.xa, p, b0 * ROWS, lane);
+    sw.store(lds);
+  } else {
+    stage_weights<N, NW * 64, RF>(p, lds);
+  }
   __syncthreads();
 
   i32x4* stage = stage_tiles + (STAGE ? wid * TC : 0);
