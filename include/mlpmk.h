@@ -251,6 +251,21 @@ int mlpmk_wn_bwd(int num_layers, const int* dims, int param_dtype, const float* 
                  const void* g, const float* inv_norm, void* dv, void* dg, void* stream);
 
 /*
+ * The elementwise step of the reference's large-M backward fallback, its fused
+ * `sigmoid_h_mul` kernel (/root/reference/mlp_fused.md:114-146):
+ *   dz[i] = dh[i] * (1 - exp(-h[i])),  i < n
+ * h is the fp32 activation stash, dh the data gradient of the layer above
+ * (dh_dtype fp32, fp16 or bf16).  dz32 receives dz in fp32 (for the fp32
+ * weight-gradient GEMM); dz16, if not NULL, the same values rounded to
+ * dz16_dtype (fp16 or bf16, for the next data-gradient GEMM).  The library
+ * GEMMs around it (rocBLAS / hipBLASLt through torch) complete the fallback
+ * backward in mlpmk.fallback; the fused backward megakernel (mlpmk_bwd_ws) is
+ * the default path at every M.
+ */
+int mlpmk_sigmoid_h_mul(const float* h, const void* dh, int dh_dtype, float* dz32, void* dz16, int dz16_dtype,
+                        int64_t n, void* stream);
+
+/*
  * Diagnostic: a streaming copy of `bytes` bytes (multiple of 16) with the same
  * 128-bit load/store width and cache policy as the forward megakernel's x and
  * out traffic (default loads, non-temporal stores).  Used to calibrate

@@ -45,6 +45,7 @@ SIGNATURES = {
         [c_int, P_INT, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
     "mlpmk_copy": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "mlpmk_sigmoid_h_mul": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64, c_void_p]),
 }
 
 STATUS = {

@@ -42,11 +42,32 @@ from . import ops
 RECOMPUTE = "auto"
 RECOMPUTE_MIN_ROWS = 1 << 17
 
+# Backward implementation: "fused" (the backward megakernel, every M) or
+# "fallback" (the reference's large-M path of library GEMMs and the fused
+# sigmoid_h_mul kernel, mlp_fused.md:114-146; mlpmk.fallback).  The fallback
+# reads every activation from the stash, so it turns recomputation off.
+BACKWARD = "fused"
+
 _rc_shapes = {}
 
 
+def _backward_impl():
+    if BACKWARD not in ("fused", "fallback"):
+        raise ValueError(f"BACKWARD must be 'fused' or 'fallback', got {BACKWARD!r}")
+    return BACKWARD
+
+
+def _run_bwd(x, weights, hs, dout, dws, dx):
+    if _backward_impl() == "fallback":
+        from . import fallback
+
+        fallback.bwd(x, weights, hs, dout, dws, dx)
+    else:
+        ops.bwd(x, weights, hs, dout, dws, dx)
+
+
 def _use_recompute(dims, m, need_dx):
-    if need_dx or RECOMPUTE == "never":
+    if need_dx or RECOMPUTE == "never" or _backward_impl() == "fallback":
         return False
     if RECOMPUTE not in ("auto", "always"):
         raise ValueError(f"RECOMPUTE must be 'auto', 'always' or 'never', got {RECOMPUTE!r}")
@@ -120,7 +141,7 @@ class FusedMLPFunction(torch.autograd.Function):
         dout = _as_row_broadcast(dout.to(x.dtype))
         dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        ops.bwd(x, weights, hs, dout, dws, dx)
+        _run_bwd(x, weights, hs, dout, dws, dx)
         return (dx, *[d if need else None for d, need in zip(dws, ctx.needs_input_grad[1:])])
 
 
@@ -166,7 +187,7 @@ class FusedMLPWNFunction(torch.autograd.Function):
         dout = _as_row_broadcast(dout.to(x.dtype))
         dw_all = torch.zeros(w_all.numel(), dtype=torch.float32, device=x.device)
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        ops.bwd(x, weights, hs, dout, _split(dw_all, dims), dx)
+        _run_bwd(x, weights, hs, dout, _split(dw_all, dims), dx)
         dv = dg = None
         if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
             dv = torch.empty_like(v_all)

@@ -24,6 +24,8 @@ int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* 
 int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const void* v, const void* g,
                     const float* inv_norm, void* dv, void* dg, hipStream_t st);
 int copy_dispatch(const void* src, void* dst, int64_t bytes, hipStream_t st);
+int sigmoid_h_mul_dispatch(const float* h, const void* dh, int dh_dtype, float* dz32, void* dz16, int dz16_dtype,
+                           int64_t n, hipStream_t st);
 
 static thread_local char g_last_error[512];
 
@@ -341,6 +343,21 @@ int mlpmk_wn_bwd(int num_layers, const int* dims, int param_dtype, const float* 
     return rc;
   return wn_bwd_dispatch(num_layers, dims, param_dtype, dw, v, g, inv_norm, dv, dg,
                          static_cast<hipStream_t>(stream));
+}
+
+int mlpmk_sigmoid_h_mul(const float* h, const void* dh, int dh_dtype, float* dz32, void* dz16, int dz16_dtype,
+                        int64_t n, void* stream) {
+  g_last_error[0] = 0;
+  if (n < 0) return fail(MLPMK_ERR_INVALID_ARG, "n=%lld is negative", (long long)n);
+  if (dh_dtype != MLPMK_DTYPE_F32 && dh_dtype != MLPMK_DTYPE_F16 && dh_dtype != MLPMK_DTYPE_BF16)
+    return fail(MLPMK_ERR_INVALID_ARG, "dh_dtype=%d (0 = fp32, 1 = fp16, 2 = bf16)", dh_dtype);
+  if (dz16 && dz16_dtype != MLPMK_DTYPE_F16 && dz16_dtype != MLPMK_DTYPE_BF16)
+    return fail(MLPMK_ERR_INVALID_ARG, "dz16_dtype=%d (1 = fp16, 2 = bf16)", dz16_dtype);
+  if (n == 0) return MLPMK_OK;
+  int rc;
+  if ((rc = check_ptr(h, "h")) || (rc = check_ptr(dh, "dh")) || (rc = check_ptr(dz32, "dz32"))) return rc;
+  if (dz16 && (rc = check_ptr(dz16, "dz16"))) return rc;
+  return sigmoid_h_mul_dispatch(h, dh, dh_dtype, dz32, dz16, dz16_dtype, n, static_cast<hipStream_t>(stream));
 }
 
 int mlpmk_copy(const void* src, void* dst, int64_t bytes, void* stream) {

@@ -477,8 +477,8 @@ struct BwdWave {
           float v[16];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            v[j] = acc[j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[B][2 * mb][j] * kLog2e));
-            v[8 + j] = acc[8 + j] * (1.0f - __builtin_amdgcn_exp2f(-hbuf[B][2 * mb + 1][j] * kLog2e));
+            v[j] = acc[j] * sig_from_h(hbuf[B][2 * mb][j]);
+            v[8 + j] = acc[8 + j] * sig_from_h(hbuf[B][2 * mb + 1][j]);
           }
           const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
           const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);

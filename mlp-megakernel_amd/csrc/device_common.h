@@ -124,6 +124,19 @@ __device__ __forceinline__ float sp2(float u) {
 // Replaces an overflowed sp2 by u (u >= 128); every other value is kept as is.
 __device__ __forceinline__ float sp2_fix(float u, float s) { return u >= 128.0f ? u : s; }
 
+// sigma(z) = 1 - exp(-h) from the post-activation h = softplus(z) >= 0 (the
+// softplus derivative as the stash contract states it, mlp_fused.md:57-61),
+// evaluated as -expm1(-h): 1 - 2^(-h log2 e) for h >= 1/32, where the
+// cancellation costs ~2^-23 / sigma < 4e-6 relative at most, and the series
+// h (1 - h/2 (1 - h/3 (1 - h/4))) below, whose truncation error is below
+// h^5 / 120 (< 8e-9 relative at h = 1/32).  The plain 1 - exp(-h) has no
+// correct digit left for saturated units (h < ~1e-7, z < ~-16).
+__device__ __forceinline__ float sig_from_h(float h) {
+  const float big = 1.0f - __builtin_amdgcn_exp2f(-h * kLog2e);
+  const float small = h * (1.0f - 0.5f * h * (1.0f - (1.0f / 3.0f) * h * (1.0f - 0.25f * h)));
+  return h < 0.03125f ? small : big;
+}
+
 template <bool BF = false>
 __device__ __forceinline__ f16x2 cvt2(float a, float b) {
   if constexpr (BF) {

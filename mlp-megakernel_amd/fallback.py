@@ -1,0 +1,76 @@
+"""The reference's large-M backward fallback, on MI355X.
+
+/root/reference/mlp_fused.md:114-146: above an M threshold the reference
+leaves its fused Triton backward (whose fp32 weight-gradient atomics contend)
+for library GEMMs plus one fused elementwise kernel, ``sigmoid_h_mul``
+(``dz = (1 - exp(-h)) * dh``), with the weight-gradient GEMM of each layer
+issued right after that layer's data-gradient GEMM ("interleaved", so that
+h_l and dz_l are still in L2):
+
+    dh2 = grad @ W3.T  ->  dw3 = h2.T @ grad
+    dz2 = sigmoid(h2) * dh2  ->  dh1 = dz2 @ W2.T
+    dw2 = h1.T @ dz2 ...
+
+Here the GEMMs are rocBLAS / hipBLASLt calls through torch (data gradients in
+the 16-bit element type with fp32 accumulation, weight gradients in fp32 from
+the fp32 stash: sums over many rows would overflow fp16) and the elementwise
+step is this library's ``mlpmk_sigmoid_h_mul`` HIP kernel, which writes dz in
+fp32 for the weight-gradient GEMM and in the 16-bit type for the next
+data-gradient GEMM from one read of h and dh.
+
+The fused backward megakernel (``ops.bwd``) replaces this at every M on
+MI355X -- it needs no atomics in its workspace form and was measured 4.6-21x
+faster at M = 4K..1M -- so autograd uses it unless ``autograd.BACKWARD`` is
+set to ``"fallback"``; this path is kept as the reference's alternative and as
+a comparator.  Same arguments and results as ``ops.bwd``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .ops import _check, _elem_code, _launch
+
+
+def sigmoid_h_mul(h, dh, dz16_dtype=None):
+    """``dz = dh * (1 - exp(-h))`` (``mlpmk_sigmoid_h_mul``): ``h`` fp32, ``dh``
+    fp32 / fp16 / bf16, same shape, contiguous, on one GPU.  Returns the fp32
+    ``dz`` and, when ``dz16_dtype`` is given, ``dz`` in that 16-bit type."""
+    if h.dtype != torch.float32 or h.shape != dh.shape:
+        raise ValueError("h must be fp32 and shaped like dh")
+    if not (h.is_contiguous() and dh.is_contiguous()) or h.device != dh.device or h.device.type != "cuda":
+        raise ValueError("h and dh must be contiguous tensors on one GPU")
+    dh_code = _lib.DTYPE_F32 if dh.dtype == torch.float32 else _elem_code(dh.dtype, "dh")
+    dz32 = torch.empty_like(h)
+    dz16 = torch.empty_like(h, dtype=dz16_dtype) if dz16_dtype is not None else None
+    dz16_code = _elem_code(dz16_dtype, "dz16") if dz16_dtype is not None else _lib.DTYPE_F16
+    lib = _lib.get()
+    rc = _launch(h.device, lib.mlpmk_sigmoid_h_mul, h.data_ptr(), dh.data_ptr(), dh_code, dz32.data_ptr(),
+                 dz16.data_ptr() if dz16 is not None else None, dz16_code, h.numel())
+    _check("mlpmk_sigmoid_h_mul", rc)
+    return (dz32, dz16) if dz16_dtype is not None else dz32
+
+
+def bwd(x, weights, hs, dout, dws, dx=None):
+    """Gradients of ``out = MLP(x)`` from the fp32 stash ``hs`` = [h1 ..
+    h_{L-1}]: ``dws[l] += h_l^T dz_l`` (``h_0 = x``) and, if ``dx`` is given,
+    ``dx = dz_0 W_0^T``, in the interleaved order of mlp_fused.md:139-145.
+    ``dout`` may be a broadcast row (stride 0), as ``loss = out.sum()``
+    gives."""
+    L = len(weights)
+    if len(hs) != L - 1 or any(h is None for h in hs):
+        raise ValueError("the fallback backward reads every hidden activation from the stash (no recompute)")
+    dt = x.dtype
+    dz16 = dout.to(dt).contiguous() if dout.stride(0) != 0 else dout[:1].to(dt).expand_as(dout).contiguous()
+    dz32 = dz16.float()
+    for l in range(L - 1, -1, -1):
+        need_dh = l > 0 or dx is not None
+        if need_dh:
+            dh = dz16 @ weights[l].t().contiguous()  # data gradient: 16-bit GEMM, fp32 accumulation
+        a = hs[l - 1] if l > 0 else x.float()
+        dws[l].add_(a.t() @ dz32)  # weight gradient: fp32 GEMM, right after (interleaved)
+        if l > 0:
+            dz32, dz16 = sigmoid_h_mul(hs[l - 1], dh.contiguous(), dz16_dtype=dt)
+        elif dx is not None:
+            dx.copy_(dh)
+    return dws, dx

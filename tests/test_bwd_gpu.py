@@ -216,3 +216,58 @@ def test_workspace_too_small_is_rejected():
                           4096, torch.cuda.current_stream().cuda_stream)
     assert rc == 1 and b"workspace_bytes" in lib.mlpmk_last_error()
     assert all(d.abs().max().item() == 0 for d in dws)  # nothing launched
+
+
+@pytest.mark.parametrize("m", [4096, 131072])
+def test_saturated_units_weight_gradients(m):
+    # Columns of W1 drive their pre-activation to a constant z in -10 .. -20
+    # (x[:, 0] = 1 and the column is z at row 0, 0 elsewhere), and three
+    # columns of W2 drive theirs to ~-12 .. -25 (all weights -0.2 against
+    # h1 ~ 0.7).  Their units saturate: h = softplus(z) ~ e^z, the derivative
+    # sigma = 1 - e^-h ~ h is evaluated as -expm1(-h) in the kernel (the plain
+    # 1 - exp(-h) has no correct digit below h ~ 1e-7), and dz = dh * sigma
+    # is tiny.  Down to z ~ -12 every dW entry of those columns must meet
+    # rtol 2e-2 against the oracle, with an atol scaled by the column's own
+    # magnitude; below, dz is an fp16 subnormal (the wgrad MFMA operand, as
+    # the reference's tl.dot operands are INPUT_DTYPE), and each entry must
+    # stay within that rounding: |err| <= 2e-2 |ref| + 2^-24 * sum_r |a[r, i]|.
+    dims = (128, 128, 128, 128)
+    x, ws = orc.make_inputs(dims, m, seed=31)
+    x[:, 0] = np.float16(1.0)
+    zs = [-10.0, -11.0, -12.0, -14.0, -16.0, -18.0, -20.0]
+    cols1 = list(range(3, 3 + len(zs)))
+    for c, z in zip(cols1, zs):
+        ws[0][:, c] = 0
+        ws[0][0, c] = np.float16(z)
+    cols2 = [40, 41, 42]
+    for c in cols2:
+        ws[1][:, c] = np.float16(-0.2)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dout = torch.ones((1, 128), dtype=torch.float16, device="cuda").expand(m, 128)
+    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+    ops.bwd(xd, wd, hs, dout, dws, None)
+    _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    rdws, _ = orc.backward(x, ws, ref_h, np.ones((m, 128), np.float32), need_dx=False)
+    acts = [x.astype(np.float64), ref_h[0].astype(np.float64)]
+    z2 = (ref_h[0].astype(np.float16).astype(np.float64) @ ws[1][:, cols2].astype(np.float64))
+    assert z2.max() < -10.0, z2.max()
+    for layer, cols, zcol in ((0, cols1, zs), (1, cols2, [None] * len(cols2))):
+        got = dws[layer].cpu().numpy().astype(np.float64)
+        ref = rdws[layer].astype(np.float64)
+        asum = np.abs(acts[layer]).sum(axis=0)  # sum_r |a[r, i]| per input feature i
+        for c, z in zip(cols, zcol):
+            g, r = got[:, c], ref[:, c]
+            assert np.abs(r).max() > 0, (layer, c)
+            if z is not None and z >= -12.0:
+                bound = 2e-2 * np.abs(r) + 2e-3 * np.abs(r).max()
+                what = f"dW{layer + 1}[:, {c}] (z = {z}) per entry at rtol 2e-2"
+            else:
+                bound = 2e-2 * np.abs(r) + 2.0 ** -24 * asum
+                what = f"dW{layer + 1}[:, {c}] (z = {z}) within the fp16-dz rounding bound"
+            excess = np.abs(g - r) - bound
+            assert excess.max() <= 0, f"{what}: worst excess {excess.max():.3g}, max|ref| {np.abs(r).max():.3g}"
+    # and the matrix as a whole, as everywhere else
+    for i in range(3):
+        check_dw(dws[i].cpu().numpy(), rdws[i], f"saturated net dW{i + 1}")
