@@ -21,15 +21,18 @@
 //    is directly the next layer's B operand.
 //  * wgrad reduces over rows, so it needs rows in the MFMA K dimension while
 //    the dgrad layout holds one row per lane.  Every layer, each wave writes
-//    its rows of a_l and dz_l (fp16) into LDS exchange tiles laid out
-//    [feature][row]; after a workgroup barrier each wave reads 16-byte A/B
-//    fragments (8 rows of one feature per lane) for the 32x32 tiles of dW_l
-//    it owns and accumulates them over all R rows -- the split-K partial sums
-//    of the R rows are reduced in the MFMA accumulators across the waves'
-//    contributions through LDS.
+//    its 32 rows of a_l and dz_l (fp16) into LDS exchange tiles laid out
+//    [row][feature], one 16-byte write per lane and K-step straight from the
+//    row-per-lane registers.  After a workgroup barrier each wave reads the
+//    A/B fragments of the 32x32 dW_l tiles it owns with ds_read_b64_tr_b16,
+//    which transposes 4x4 blocks of 16-bit elements on the way out of LDS, so
+//    a lane receives 8 rows of one feature, and accumulates them over all R
+//    rows of the round in MFMA accumulators.
 //  * The owned dW tiles stay in registers (AGPRs) across all rounds of the
-//    workgroup; at the end each wave adds them to the fp32 dW in global memory
-//    with hardware float atomics (one add per element per workgroup).
+//    workgroup.  At the end each wave either adds them to the fp32 dW with
+//    hardware float atomics (small grids) or writes them to its workgroup's
+//    slot of a partial-sum workspace, which bwd_combine_kernel then reduces
+//    in a fixed order (no atomics, bitwise-reproducible).
 //
 // Segment mode (SEG) runs the upper layers of a deeper network on their own:
 // layer 0 of the segment then takes its activation from the fp32 stash of
@@ -40,11 +43,10 @@
 // four dgrad weight blocks and the exchange tiles do not fit the 160 KiB LDS
 // of one workgroup together.
 //
-// The exchange tiles are XOR-swizzled, element (f, r) at f*R + (r ^ 8*(f & 15)):
-// the 2-byte writes of one half-wave (32 consecutive rows of one feature) hit
-// one 64-byte window, the two half-waves (features f and f+8) land 128 bytes
-// apart, and the 16-byte fragment reads of 16 lanes (16 consecutive features,
-// same 8 rows) fall on 16 distinct chunks -- all bank-conflict free.
+// The exchange tiles are swizzled by whole 8-feature chunks (Bwd::swz): the
+// 16-byte writes of 8 consecutive rows land in 8 distinct chunk slots and the
+// four rows of one transposed read fall in four distinct 16-feature windows,
+// so both directions are free of bank conflicts.
 #include <atomic>
 
 #include "device_common.h"
