@@ -340,6 +340,56 @@ def sustained(torch, step, ms_hint, seconds=0.6):
     return ms, n
 
 
+def timeline_leg(torch, step, m, rows_per_block=32):
+    """Per-XCD view of one persistent launch, from a library built with
+    per-wave timestamps (``make timeline`` -> libmlpmk_timeline.so, loaded
+    through MLPMK_LIBRARY): after ~0.3 s of back-to-back launches, one more
+    launch is recorded.  Per XCD: mean shader clock over the waves' spans
+    (s_memtime cycles / s_memrealtime ticks), when its first and last wave
+    finished and how long the weight staging took, relative to the first
+    wave's start."""
+    import ctypes
+
+    from mlpmk import _lib
+    lib = _lib.get()
+    if not hasattr(lib, "mlpmk_fwd_timeline"):
+        raise SystemExit("bench.py --timeline: the loaded library has no timestamps; build `make -C "
+                         "mlp-megakernel_amd/csrc timeline` and set MLPMK_LIBRARY=mlp-megakernel_amd/libmlpmk_timeline.so")
+    words = 4096 * 8
+    buf = np.zeros(words, np.uint64)
+    fn = lib.mlpmk_fwd_timeline
+    fn.restype, fn.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
+    with gc_paused():
+        ramp_clock(torch, step, 0.3)
+        if fn(buf.ctypes.data, buf.nbytes) != 0:  # clears the records
+            raise SystemExit("mlpmk_fwd_timeline failed")
+        step(0)
+        torch.cuda.synchronize()
+    if fn(buf.ctypes.data, buf.nbytes) != 0:
+        raise SystemExit("mlpmk_fwd_timeline failed")
+    r = buf.reshape(-1, 8)
+    r = r[r[:, 7] == 1].astype(np.float64)
+    t0 = r[:, 0].min()
+    start, staged, end, cyc = r[:, 0] - t0, r[:, 1] - t0, r[:, 2] - t0, r[:, 3]
+    xcc = r[:, 4].astype(int)
+    mhz = 100.0 * cyc / np.maximum(r[:, 2] - r[:, 0], 1)
+    out = {"waves": int(len(r)), "blocks": int(r[:, 6].sum()), "rows": m,
+           "kernel_us": round(end.max() / 100.0, 2), "xcd": {}}
+    for x in sorted(set(xcc)):
+        k = xcc == x
+        out["xcd"][str(x)] = {
+            "waves": int(k.sum()),
+            "blocks": int(r[k, 6].sum()),
+            "mhz": round(float(mhz[k].mean()), 0),
+            "staging_us": round(float((staged[k] - start[k]).mean()) / 100.0, 2),
+            "first_finish_us": round(float(end[k].min()) / 100.0, 2),
+            "last_finish_us": round(float(end[k].max()) / 100.0, 2),
+        }
+    out["mhz_mean"] = round(float(mhz.mean()), 0)
+    out["finish_spread_us"] = round(float(end.max() - end.min()) / 100.0, 2)
+    return out
+
+
 def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, dtype=None):
     """One training step of BASELINE config 5 through the drop-in module:
     weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
@@ -511,6 +561,11 @@ def main():
                          "the reference's PyTorch-op backward)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--quick", action="store_true",
+                    help="counter-collection runs: parity gate, warm-up and the timed launches only (no clock ramp, "
+                         "sustained run, bf16 figure or copy reference)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-XCD clock and finish times of one launch (needs libmlpmk_timeline.so via MLPMK_LIBRARY)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -557,10 +612,11 @@ def main():
 
     # --- timed region: the K launches of the contract ----------------------
     with gc_paused():
-        ramp_clock(torch, step)
+        if not args.quick:
+            ramp_clock(torch, step)
         ms = time_launches(torch, step, args.steps, args.warmup)
     # the same launches sustained for >= 0.5 s, right after
-    sus_ms, sus_n = sustained(torch, step, ms)
+    sus_ms, sus_n = sustained(torch, step, ms) if not args.quick else (float("nan"), 0)
     nbytes, nflops = algorithmic(dims, m)
     achieved_gbs = nbytes / (ms * 1e-3) / 1e9
     tflops = nflops / (ms * 1e-3) / 1e12
@@ -584,25 +640,38 @@ def main():
     roofline["algorithmic_bytes_per_launch"] = nbytes
     roofline["timed_over"] = f"the {args.steps} timed launches (HIP events); 'sustained' has the >= 0.5 s figure"
 
-    # The same workload with bf16 tensors (the bf16 instantiation of the
-    # kernel; a secondary figure, the metric stays the fp16 one).
-    xb = [x.to(torch.bfloat16) for x in xs]
-    wb = [w.to(torch.bfloat16) for w in ws]
-    ob = [torch.empty_like(o, dtype=torch.bfloat16) for o in outs]
-    with gc_paused():
-        ramp_clock(torch, lambda i: ops.fwd_into(xb[i & 1], wb, ob[i & 1]))
-        bf16_ms = time_launches(torch, lambda i: ops.fwd_into(xb[i & 1], wb, ob[i & 1]), args.steps, args.warmup)
-    del xb, wb, ob
+    bf16_ms = copy_gbs = float("nan")
+    if args.quick:
+        # counter runs: a few copies of known size to calibrate FETCH_SIZE /
+        # WRITE_SIZE against (no timing)
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            ops.copy_bytes(src, dst)
+        torch.cuda.synchronize()
+        del src, dst
+    else:
+        # The same workload with bf16 tensors (the bf16 instantiation of the
+        # kernel; a secondary figure, the metric stays the fp16 one).
+        xb = [x.to(torch.bfloat16) for x in xs]
+        wb = [w.to(torch.bfloat16) for w in ws]
+        ob = [torch.empty_like(o, dtype=torch.bfloat16) for o in outs]
+        with gc_paused():
+            ramp_clock(torch, lambda i: ops.fwd_into(xb[i & 1], wb, ob[i & 1]))
+            bf16_ms = time_launches(torch, lambda i: ops.fwd_into(xb[i & 1], wb, ob[i & 1]), args.steps, args.warmup)
+        del xb, wb, ob
 
-    # achievable-HBM reference: the library's 16-byte copy over 512 MiB with
-    # the forward's cache policy (default loads, non-temporal stores)
-    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
-    with gc_paused():
-        ramp_clock(torch, lambda i: ops.copy_bytes(src, dst), 0.05)
-        cms = time_launches(torch, lambda i: ops.copy_bytes(src, dst), 20, 5)
-    copy_gbs = 2 * src.numel() / (cms * 1e-3) / 1e9
-    del src, dst
+        # achievable-HBM reference: the library's 16-byte copy over 512 MiB
+        # with the forward's cache policy (default loads, non-temporal
+        # stores); 512 MiB each way so that the source cannot stay in the
+        # 256 MB Infinity Cache between launches
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        with gc_paused():
+            ramp_clock(torch, lambda i: ops.copy_bytes(src, dst), 0.05)
+            cms = time_launches(torch, lambda i: ops.copy_bytes(src, dst), 20, 5)
+        copy_gbs = 2 * src.numel() / (cms * 1e-3) / 1e9
+        del src, dst
 
     result = {
         "metric": METRIC,
@@ -619,18 +688,24 @@ def main():
         "data": "synthetic (seeded N(0,1) x, N(0,1/in) fp16 weights, resident in HBM)",
         "config": {"workload": workload, "dims": list(dims), "M": m, "parallelism": "none (1 GPU)"},
         "roofline": roofline,
-        "sustained": {"ms_per_step": round(sus_ms, 5), "launches": sus_n, "seconds": round(sus_ms * sus_n / 1e3, 3),
-                      "roofline_frac": round(frac_of(sus_ms), 4)},
+        "sustained": None if args.quick else {
+            "ms_per_step": round(sus_ms, 5), "launches": sus_n, "seconds": round(sus_ms * sus_n / 1e3, 3),
+            "roofline_frac": round(frac_of(sus_ms), 4)},
         "tflops": round(tflops, 2),
         "roofline_tflops": round(roof_tflops, 1),
         "frac_of_min_mfma_hbm_roofline": round(tflops / roof_tflops, 4),
-        "copy_kernel_gbs": round(copy_gbs, 1),
-        "copy_kernel": "512 MiB, 16-byte default loads + non-temporal stores (the forward's policy)",
-        "bf16_ms_per_step": round(bf16_ms, 5),
+        "copy_kernel_gbs": None if args.quick else round(copy_gbs, 1),
+        "copy_kernel": "512 MiB each way, 16-byte default loads + non-temporal stores (the forward's policy), "
+                       "3 workgroups of 256 threads per CU (the fastest grid-stride shape measured)",
+        "bf16_ms_per_step": None if args.quick else round(bf16_ms, 5),
         "parity": {"ok": ok, "max_abs_err": maxerr, "atol": 1e-2, "rtol": 1e-2, "rows_checked": 4096},
         "device": torch.cuda.get_device_properties(0).name,
         "launch": ops.fwd_launch_info(dims, m),
     }
+    if os.environ.get("MLPMK_LIBRARY"):
+        result["library"] = os.path.basename(os.environ["MLPMK_LIBRARY"])
+    if args.timeline:
+        result["timeline"] = timeline_leg(torch, step, m)
 
     if not args.no_extra:
         # The other BASELINE configs, each timed here too.

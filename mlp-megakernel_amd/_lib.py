@@ -3,13 +3,17 @@
 The library is loaded lazily on first use so that importing the package works
 on machines without the built library; any call then raises ``OSError``
 naming the missing file.  There is no fallback implementation.
+
+``MLPMK_LIBRARY`` (environment) names another build of the same ABI to load
+instead, e.g. ``libmlpmk_sp2.so`` (``make forms``: the forward built with
+another softplus evaluation, for measurement).
 """
 import ctypes
 import os
 import threading
 
 LIB_NAME = "libmlpmk.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+LIB_PATH = os.environ.get("MLPMK_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 c_int, c_int64, c_void_p, c_char_p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_char_p
 P_INT = ctypes.POINTER(c_int)

@@ -226,7 +226,10 @@ int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const vo
 // Calibration copy: 16-byte loads/stores, grid-stride, the access width and
 // cache policy of the forward megakernel's x and out traffic (default loads,
 // non-temporal stores).  Used to scale FETCH_SIZE / WRITE_SIZE counters and as
-// the achievable-HBM reference of the benchmark.
+// the achievable-HBM reference of the benchmark.  Grid: 3 workgroups of 256
+// threads per CU, the fastest of the grid-stride and per-workgroup-chunk
+// copies measured on MI355X at 512 MiB each way (6.13 TB/s; 8 per CU: 5.15,
+// 1 per CU with 1024 threads: 6.02, 8 KiB chunks per workgroup: 6.08).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void copy_kernel(const f32x4* __restrict__ src, f32x4* __restrict__ dst,
                                                    int64_t n16) {
@@ -240,7 +243,7 @@ int copy_dispatch(const void* src, void* dst, int64_t bytes, hipStream_t st) {
   if (rc) return rc;
   const int64_t n16 = bytes / 16;
   int64_t grid = (n16 + 255) / 256;
-  if (grid > (int64_t)cus * 8) grid = (int64_t)cus * 8;
+  if (grid > (int64_t)cus * 3) grid = (int64_t)cus * 3;
   (void)hipGetLastError();
   hipLaunchKernelGGL(copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const f32x4*)src, (f32x4*)dst, n16);
   hipError_t e = hipGetLastError();
