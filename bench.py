@@ -47,10 +47,11 @@ CONFIG_DIMS = {
 DEFAULT_M = {"3l128": 1048576, "5l128": 1048576, "narrow": 4194304}
 
 
-def algorithmic(dims, m):
-    """(bytes, flops) of one forward launch: x + out rows once, weights once."""
-    wbytes = 2 * sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
-    rbytes = 2 * (dims[0] + dims[-1])
+def algorithmic(dims, m, esize=2):
+    """(bytes, flops) of one forward launch: x + out rows once, weights once
+    (``esize`` bytes per element: 2 for fp16/bf16 tensors, 4 for fp32)."""
+    wbytes = esize * sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
+    rbytes = esize * (dims[0] + dims[-1])
     flops = 2 * sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))
     return rbytes * m + wbytes, flops * m
 
@@ -267,7 +268,8 @@ def fwd_bench(torch, ops, dims, m, uniform, steps=200, warmup=20, dtype=None):
     total, at least two pairs): ms per launch (HIP events around `steps`
     launches after a 0.1 s clock ramp), rows/s, roofline fraction."""
     dtype = dtype or torch.float16
-    per_pair = m * (dims[0] + dims[-1]) * 2
+    esize = torch.empty((), dtype=dtype).element_size()
+    per_pair = m * (dims[0] + dims[-1]) * esize
     pairs = max(2, -(-(512 << 20) // per_pair))
     xs, ws = [], None
     for k in range(pairs):
@@ -282,14 +284,15 @@ def fwd_bench(torch, ops, dims, m, uniform, steps=200, warmup=20, dtype=None):
     with gc_paused():
         ramp_clock(torch, step)
         ms = time_launches(torch, step, steps, warmup)
-    nbytes, nflops = algorithmic(dims, m)
+    nbytes, nflops = algorithmic(dims, m, esize)
     ai = nflops / nbytes
     hbm_bound = HBM_PEAK_GBS * ai / 1e3 < MFMA_F16_PEAK_TFLOPS
     gbs = nbytes / (ms * 1e-3) / 1e9
     tflops = nflops / (ms * 1e-3) / 1e12
-    info = ops.fwd_launch_info(dims, m)
+    info = ops.fwd_launch_info(dims, m, dtype=dtype)
     del xs, outs
     return {
+        "dtype": str(dtype).replace("torch.", ""),
         "ms_per_step": round(ms, 5),
         "rows_per_s": round(m / (ms * 1e-3), 1),
         "achieved_gbs": round(gbs, 1),
@@ -714,6 +717,8 @@ def main():
             "5l128 M=65536": fwd_bench(torch, ops, CONFIG_DIMS["5l128"], 65536, False),
             "5l128 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["5l128"], 1048576, False),
             "narrow M=4194304": fwd_bench(torch, ops, CONFIG_DIMS["narrow"], 4194304, True),
+            # fp32 tensors (fp16 MFMA operands, fp32 rows: twice the bytes)
+            "3l128 fp32 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["3l128"], 1048576, False, dtype=torch.float32),
         }
         result["latency_sweep"] = latency_sweep(torch, ops, CONFIG_DIMS["3l128"])
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}

@@ -41,10 +41,11 @@ typedef enum mlpmk_status {
   MLPMK_ERR_NO_DEVICE = 5          /* no usable gfx950 device */
 } mlpmk_status;
 
-/* Element types.  The megakernels (mlpmk_fwd, mlpmk_bwd*) take fp16 or bf16
- * tensors (x, w, out, dout, dx all of that type; fp32 accumulation, fp32
- * stash and weight gradients either way; fp32 tensors are rejected with
- * MLPMK_ERR_UNSUPPORTED_SHAPE).  The weight-norm parameters may be fp32,
+/* Element types.  The forward (mlpmk_fwd) takes fp16, bf16 or fp32 tensors
+ * (x, w and out all of that type); the backward (mlpmk_bwd*) fp16 or bf16
+ * tensors (x, w, dout, dx; fp32 ones are rejected with
+ * MLPMK_ERR_UNSUPPORTED_SHAPE).  Accumulation, the stash and the weight
+ * gradients are fp32 either way.  The weight-norm parameters may be fp32,
  * fp16 or bf16.  The reference's kernels take their element type as the
  * INPUT_DTYPE constexpr (/root/reference/mlp_fused.md:159-166). */
 enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1, MLPMK_DTYPE_BF16 = 2 };
@@ -96,9 +97,13 @@ int mlpmk_bwd_recompute_supported(int num_layers, const int* dims);
  * and its training-forward variant that stores the hidden activations
  * (/root/reference/mlp_fused.md:52-61, fp32 storage README.md:30).
  *
- *   dtype  MLPMK_DTYPE_F16 or MLPMK_DTYPE_BF16: element type of x, w and out
- *          (bf16: bf16 MFMA operands, hidden activations rounded to bf16
- *          between layers, as the reference's casts to INPUT_DTYPE do)
+ *   dtype  MLPMK_DTYPE_F16, MLPMK_DTYPE_BF16 or MLPMK_DTYPE_F32: element
+ *          type of x, w and out (bf16: bf16 MFMA operands, hidden
+ *          activations rounded to bf16 between layers, as the reference's
+ *          casts to INPUT_DTYPE do; fp32: x, the scaled weights and the
+ *          hidden activations rounded to fp16 MFMA operands -- the 10-bit
+ *          mantissa of the reference's TF32 tl.dot operands, with fp16's
+ *          exponent range -- and out written in fp32 from the accumulators)
  *   x      [M, dims[0]]            dtype, device
  *   w[l]   [dims[l], dims[l+1]]    dtype, device, l = 0 .. num_layers-1
  *   out    [M, dims[num_layers]]   dtype, device (written)
@@ -138,7 +143,8 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
  * function (/root/reference/mlp_fused.md:88-112, README.md:32) -- the file that
  * held it (fused_mlp.py, README.md:18) is not in the reference snapshot.
  *
- *   dtype            as in mlpmk_fwd: element type of x, w, dout and dx
+ *   dtype            MLPMK_DTYPE_F16 or MLPMK_DTYPE_BF16: element type of x,
+ *                    w, dout and dx
  *   x                [M, dims[0]] dtype
  *   w[l]             as in mlpmk_fwd
  *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd;

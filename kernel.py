@@ -2,8 +2,9 @@
 
 Same public surface as /root/reference/kernel.py:
   * ``_fused_mlp_fwd(x, w1, w2, w3) -> out``  (kernel.py:130-156): contiguous
-    copies of the inputs, a fresh fp16 ``[M, N3]`` output, one asynchronous
-    launch on the current stream, no synchronisation.
+    copies of the inputs, a fresh ``[M, N3]`` output of x's dtype (fp16, bf16
+    or fp32, as the reference passes fp32 on, kernel.py:138), one
+    asynchronous launch on the current stream, no synchronisation.
   * ``_pick_config(M, K1, N1, N2, N3, fp32=False)`` (kernel.py:25-53): the
     launch policy, here the gfx950 one.
   * ``Model`` (eager reference, kernel.py:163-171) and ``ModelNew`` (fused,
@@ -36,6 +37,10 @@ _POLICY = {
     (32, 64, 64, 16): (2, 2, 64, 16),
 }
 _GENERIC_POLICY = (0, 0, 32, 8)  # runtime-width kernels: no split kernel, at most 8 waves
+# fp32 tensors (fwd_f32.hip): the persistent kernel only, 32-row blocks, at
+# most this many waves (4 where 8 would spill: the 3-layer runtime-width kernel).
+_POLICY_F32 = {(128, 128, 128, 128): 8, (32, 64, 64, 16): 8, (128, 128, 128, 128, 128, 128): 8}
+_GENERIC_WAVES_F32 = {2: 8, 3: 4, 4: 8, 5: 4}
 
 
 def __getattr__(name):
@@ -44,7 +49,12 @@ def __getattr__(name):
     raise AttributeError(name)
 
 
-def _mirror_policy(M, dims, num_cus):
+def _mirror_policy(M, dims, num_cus, fp32=False):
+    if fp32:
+        max_waves = _POLICY_F32.get(tuple(dims)) or _GENERIC_WAVES_F32[len(dims) - 1]
+        if max_waves > 4 and -(-M // 32) <= 4 * num_cus:
+            return 32, 4
+        return 32, max_waves
     split_per_cu, split_waves, bm, max_waves = _POLICY.get(tuple(dims), _GENERIC_POLICY)
     if -(-M // 32) <= split_per_cu * num_cus:
         return 32, split_waves
@@ -74,16 +84,16 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
         networks (any other widths) at most 8.
     With ``num_cus`` None and a GPU present the answer comes from the library
     (``mlpmk_fwd_launch_info``); otherwise from the mirror above with
-    ``num_cus`` CUs (MI355X's 256 by default).  ``fp32`` inputs are not
-    supported by the main-branch surface either (/root/reference/AGENTS.md:86-88).
+    ``num_cus`` CUs (MI355X's 256 by default).  ``fp32`` inputs (fp32 x, W
+    and out; fp16 MFMA operands) always take the persistent kernel, with at
+    most 8 waves per workgroup (4 up to 4 blocks per CU, and for the 3-layer
+    runtime-width kernel).
     """
-    if fp32:
-        raise TypeError("the fused forward takes fp16 inputs (main-branch surface is fp16 only)")
     dims = (K1, N1, N2, N3)
     if num_cus is None and torch.cuda.is_available():
-        info = _ops.fwd_launch_info(dims, max(int(M), 1))
+        info = _ops.fwd_launch_info(dims, max(int(M), 1), dtype=torch.float32 if fp32 else torch.float16)
         return info["rows_per_block"], N3, 16, 16, 16, info["waves"]
-    bm, warps = _mirror_policy(M, dims, _MI355X_CUS if num_cus is None else num_cus)
+    bm, warps = _mirror_policy(M, dims, _MI355X_CUS if num_cus is None else num_cus, fp32=fp32)
     return bm, N3, 16, 16, 16, warps
 
 

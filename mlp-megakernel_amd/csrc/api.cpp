@@ -13,7 +13,7 @@
 namespace mlpmk {
 
 bool fwd_supported_dims(int L, const int* dims);
-int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, LaunchInfo* info);
+int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, int dtype, hipStream_t st, LaunchInfo* info);
 bool bwd_supported_dims(int L, const int* dims);
 bool bwd_recompute_supported(int L, const int* dims);
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st);
@@ -87,6 +87,13 @@ static int check_elem_dtype(int dtype) {
   return fail(MLPMK_ERR_INVALID_ARG, "dtype=%d (1 = fp16, 2 = bf16)", dtype);
 }
 
+// Element format of the forward's x, W and out: fp32 tensors are taken too
+// (fp16 MFMA operands, fp32 output rows).
+static int check_fwd_dtype(int dtype) {
+  if (dtype == MLPMK_DTYPE_F16 || dtype == MLPMK_DTYPE_BF16 || dtype == MLPMK_DTYPE_F32) return MLPMK_OK;
+  return fail(MLPMK_ERR_INVALID_ARG, "dtype=%d (0 = fp32, 1 = fp16, 2 = bf16)", dtype);
+}
+
 static int check_dims(int L, const int* dims) {
   if (!dims) return fail(MLPMK_ERR_INVALID_ARG, "dims is NULL");
   if (L < 2 || L > kMaxLayersHost)
@@ -144,7 +151,7 @@ int mlpmk_fwd(int num_layers, const int* dims, int dtype, const void* x, const v
   g_last_error[0] = 0;
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
-  if ((rc = check_elem_dtype(dtype))) return rc;
+  if ((rc = check_fwd_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   if (!w) return fail(MLPMK_ERR_INVALID_ARG, "w is NULL");
   if (!fwd_supported_dims(num_layers, dims))
@@ -172,15 +179,14 @@ int mlpmk_fwd(int num_layers, const int* dims, int dtype, const void* x, const v
   p.out = static_cast<_Float16*>(out);
   p.M = M;
   for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
-  return fwd_dispatch(num_layers, dims, p, stash != nullptr, dtype == MLPMK_DTYPE_BF16,
-                      static_cast<hipStream_t>(stream), nullptr);
+  return fwd_dispatch(num_layers, dims, p, stash != nullptr, dtype, static_cast<hipStream_t>(stream), nullptr);
 }
 
 int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M, int stash, int* info) {
   g_last_error[0] = 0;
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
-  if ((rc = check_elem_dtype(dtype))) return rc;
+  if ((rc = check_fwd_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   if (!info) return fail(MLPMK_ERR_INVALID_ARG, "info is NULL");
   if (!fwd_supported_dims(num_layers, dims))
@@ -194,7 +200,7 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
   p.M = M;
   for (int l = 0; l <= num_layers; ++l) p.dims[l] = dims[l];
   LaunchInfo li = {};
-  rc = fwd_dispatch(num_layers, dims, p, stash != 0, dtype == MLPMK_DTYPE_BF16, nullptr, &li);
+  rc = fwd_dispatch(num_layers, dims, p, stash != 0, dtype, nullptr, &li);
   if (rc) return rc;
   const int out[5] = {li.kernel, li.rows_per_block, li.waves, li.grid, li.wgs_per_cu};
   memcpy(info, out, sizeof(out));

@@ -74,6 +74,17 @@ def _elem_code(dtype, name="x"):
     return code
 
 
+def _fwd_code(dtype, name="x"):
+    """Element type of the forward's x, weights and out: fp16, bf16, or fp32
+    (fp32 tensors run with fp16 MFMA operands and write fp32 rows)."""
+    if dtype == torch.float32:
+        return _lib.DTYPE_F32
+    code = _ELEM.get(dtype)
+    if code is None:
+        raise TypeError(f"{name} must be float32, float16 or bfloat16, got {dtype}")
+    return code
+
+
 def _require(t, name, dtype, device):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
@@ -110,15 +121,17 @@ def _launch(device, fn, *args):
 def fwd_into(x, weights, out, stash=None):
     """Run the forward megakernel writing ``out`` (and ``stash`` if given).
 
-    ``x`` [M, D] fp16 or bf16, ``weights`` list of [in, out] and ``out``
-    [M, OUT] of x's dtype, ``stash`` list of L-1 fp32 [M, H_l] tensors (an entry may be None:
-    that activation is not written) or None.  All contiguous on one CUDA
-    (HIP) device.
+    ``x`` [M, D] fp16, bf16 or fp32, ``weights`` list of [in, out] and
+    ``out`` [M, OUT] of x's dtype, ``stash`` list of L-1 fp32 [M, H_l] tensors
+    (an entry may be None: that activation is not written) or None.  All
+    contiguous on one CUDA (HIP) device.  fp32 tensors run with fp16 MFMA
+    operands (the 10-bit mantissa of TF32, fp16's exponent range) and fp32
+    accumulation, softplus and output rows.
     """
     dev = x.device
     if dev.type != "cuda":
         raise ValueError(f"x must be on a GPU device, got {dev}")
-    code = _elem_code(x.dtype)
+    code = _fwd_code(x.dtype)
     _require(x, "x", x.dtype, dev)
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
@@ -162,7 +175,7 @@ def fwd_launch_info(dims, M, stash=False, dtype=torch.float16, device=None):
     info = (ctypes.c_int * 5)()
     idx = torch.cuda.current_device() if device is None or device.index is None else device.index
     with torch.cuda.device(idx):
-        rc = lib.mlpmk_fwd_launch_info(len(dims) - 1, pd, _elem_code(dtype), int(M), int(bool(stash)), info)
+        rc = lib.mlpmk_fwd_launch_info(len(dims) - 1, pd, _fwd_code(dtype), int(M), int(bool(stash)), info)
     _check("mlpmk_fwd_launch_info", rc)
     return {"kernel": KERNEL_NAMES[info[0]], "rows_per_block": info[1], "waves": info[2], "grid": info[3],
             "wgs_per_cu": info[4]}

@@ -78,10 +78,9 @@ def test_fwd_validation_codes():
     assert _fwd(d, stash=(A, A + 4)) == MISALIGNED
     assert b"stash[1]" in lib.mlpmk_last_error()
     assert lib.mlpmk_fwd(3, None, 1, A, None, A, None, 1, None) == INVALID
-    # element types: fp16 (1) and bf16 (2); fp32 (0) has no megakernel, others are invalid
-    assert _fwd(d, dtype=0) == UNSUPPORTED
-    assert b"fp32" in lib.mlpmk_last_error()
+    # element types: fp16 (1), bf16 (2) and fp32 (0, fp16 MFMA operands); others are invalid
     assert _fwd(d, dtype=7) == INVALID
+    assert _fwd(d, dtype=0, m=0) == OK
     assert _fwd(d, dtype=2, m=0) == OK
     # M == 0 succeeds without touching a device (x/out may even be NULL)
     assert _fwd(d, x=None, out=None, m=0) == OK
@@ -92,6 +91,7 @@ def test_fwd_validation_codes():
         assert lib.mlpmk_last_error() != b""
         assert _fwd(d, stash=(A, None)) in (NODEV, HIPERR)
         assert _fwd(d, dtype=2) in (NODEV, HIPERR)
+        assert _fwd(d, dtype=0) in (NODEV, HIPERR)
 
 
 def test_bwd_validation_codes():
@@ -207,8 +207,12 @@ def test_drop_in_modules_import_without_gpu():
     assert cfg(40000, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 4)
     assert cfg(4194304, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 16)
     assert cfg(4096, 128, 128, 128, 128, num_cus=8) == (32, 128, 16, 16, 16, 12)
-    with pytest.raises(TypeError):
-        kernel._pick_config(4096, 128, 128, 128, 128, fp32=True)
+    # fp32 tensors: the persistent kernel only, 4 waves up to 4 blocks per CU,
+    # then 8 (4 for the 3-layer runtime-width kernel)
+    assert cfg(4096, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 4)
+    assert cfg(1048576, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 8)
+    assert cfg(4194304, 32, 64, 64, 16, fp32=True) == (32, 16, 16, 16, 16, 8)
+    assert cfg(1048576, 64, 64, 64, 64, fp32=True) == (32, 64, 16, 16, 16, 4)
     assert callable(kernel._fused_mlp_fwd) and kernel.Model and kernel.ModelNew
 
 

@@ -92,17 +92,20 @@ def test_launcher_runs_on_the_current_stream_without_sync():
     assert ok, err
 
 
+@pytest.mark.parametrize("fp32", [False, True])
 @pytest.mark.parametrize("dims", [(128,) * 4, (32, 64, 64, 16), (64, 64, 64, 64), (128, 128, 128, 10), (64, 128, 32, 16)])
-def test_pick_config_mirror_matches_the_library_launch(dims):
+def test_pick_config_mirror_matches_the_library_launch(dims, fp32):
     # The Python mirror of the launch policy (used without a device) against
     # the library's own answer from the code path that launches
-    # (mlpmk_fwd_launch_info), at the sizes where the policy switches.
+    # (mlpmk_fwd_launch_info), at the sizes where the policy switches; fp16
+    # and fp32 tensors.
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    dt = torch.float32 if fp32 else torch.float16
     for m in (1, 64, 32 * cus, 32 * cus + 1, 64 * cus, 64 * cus + 1, 128 * cus, 128 * cus + 1, 256 * cus,
               256 * cus + 1, 512 * cus + 1, 1048576):
-        info = ops.fwd_launch_info(dims, m)
-        assert kernel._mirror_policy(m, dims, cus) == (info["rows_per_block"], info["waves"]), (dims, m, info)
-        assert kernel._pick_config(m, *dims)[::5] == (info["rows_per_block"], info["waves"])
+        info = ops.fwd_launch_info(dims, m, dtype=dt)
+        assert kernel._mirror_policy(m, dims, cus, fp32=fp32) == (info["rows_per_block"], info["waves"]), (dims, m, info)
+        assert kernel._pick_config(m, *dims, fp32=fp32)[::5] == (info["rows_per_block"], info["waves"])
         nblk = -(-m // info["rows_per_block"])
         per_wg = 1 if info["kernel"] == "feature_split" else info["waves"]
         assert info["grid"] == min(-(-nblk // per_wg), cus * info["wgs_per_cu"]), (dims, m, info)
