@@ -54,8 +54,9 @@ constexpr int kStreamStore = 2;
 // The fp32 activation stash (two 16-byte pieces of each of 32 rows per
 // instruction pair, 1 KiB per row for the 3-layer network) keeps the default
 // policy so that L2 merges the pieces of a line: with nt the 3-layer training
-// forward at M = 131072 took 87 us instead of 35 us.  (The fp16 output rows
-// written the same way by the 5-layer network are slightly faster with nt.)
+// forward at M = 131072 took 87 us instead of 35 us.  Output rows wider than
+// 64 bytes written the same way (no LDS staging tile) keep it too
+// (kDirectOutStore in fwd_kernel.h).
 constexpr int kStashStore = 0;
 template <class T, int AUX = 0>
 __device__ __forceinline__ T buf_load16(rsrc_t r, uint32_t byte_off) {
