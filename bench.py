@@ -43,8 +43,10 @@ CONFIG_DIMS = {
     "3l128": (128, 128, 128, 128),
     "5l128": (128, 128, 128, 128, 128, 128),
     "narrow": (32, 64, 64, 16),
+    # hidden width 256 (streamed-weight kernel; not a BASELINE config)
+    "3l256": (128, 256, 256, 128),
 }
-DEFAULT_M = {"3l128": 1048576, "5l128": 1048576, "narrow": 4194304}
+DEFAULT_M = {"3l128": 1048576, "5l128": 1048576, "narrow": 4194304, "3l256": 1048576}
 
 
 def algorithmic(dims, m, esize=2):
@@ -719,6 +721,8 @@ def main():
             "narrow M=4194304": fwd_bench(torch, ops, CONFIG_DIMS["narrow"], 4194304, True),
             # fp32 tensors (fp16 MFMA operands, fp32 rows: twice the bytes)
             "3l128 fp32 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["3l128"], 1048576, False, dtype=torch.float32),
+            # hidden width 256: weights streamed through LDS (fwd_wide.hip)
+            "3l256 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["3l256"], 1048576, False),
         }
         result["latency_sweep"] = latency_sweep(torch, ops, CONFIG_DIMS["3l128"])
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}

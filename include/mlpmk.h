@@ -66,12 +66,16 @@ const char* mlpmk_last_error(void);
  * of 16 in [16, 128] and whose output width is in [1, 128] (runtime-width
  * kernels, compiled at width 128 with the true widths as launch parameters;
  * the reference's kernel takes tile-multiple K1, N1, N2 and masks N3,
- * /root/reference/kernel.py:60-63,86-87).
+ * /root/reference/kernel.py:60-63,86-87), and -- for fp16 and bf16 tensors --
+ * the same with widths up to 256 (input and hidden multiples of 16 in
+ * [16, 256], output in [1, 256]; a streamed-weight kernel: the weights do
+ * not fit one workgroup's LDS).
  */
 int mlpmk_fwd_supported(int num_layers, const int* dims);
 
 /* 1 if the backward kernel exists for (num_layers, dims), else 0.  Host only.
- * The same shapes as mlpmk_fwd_supported. */
+ * The shapes of mlpmk_fwd_supported with every width at most 128 (wider
+ * networks train through the library-GEMM fallback, mlpmk_sigmoid_h_mul). */
 int mlpmk_bwd_supported(int num_layers, const int* dims);
 
 /*

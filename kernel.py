@@ -50,6 +50,8 @@ def __getattr__(name):
 
 
 def _mirror_policy(M, dims, num_cus, fp32=False):
+    if max(dims) > 128:  # streamed-weight kernel (fwd_wide.hip): 8 waves, 32-row blocks, any M
+        return 32, 8
     if fp32:
         max_waves = _POLICY_F32.get(tuple(dims)) or _GENERIC_WAVES_F32[len(dims) - 1]
         if max_waves > 4 and -(-M // 32) <= 4 * num_cus:
@@ -82,6 +84,8 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
       * otherwise the persistent kernel with 4 waves per workgroup up to 4
         blocks per CU, 8 up to 8, then 12 (16 narrow); runtime-width
         networks (any other widths) at most 8.
+    Widths above 128 (up to 256) take the streamed-weight kernel at every M
+    (8 waves, one 32-row block each per round).
     With ``num_cus`` None and a GPU present the answer comes from the library
     (``mlpmk_fwd_launch_info``); otherwise from the mirror above with
     ``num_cus`` CUs (MI355X's 256 by default).  ``fp32`` inputs (fp32 x, W

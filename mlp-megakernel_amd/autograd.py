@@ -57,8 +57,21 @@ def _backward_impl():
     return BACKWARD
 
 
+_bwd_shapes = {}
+
+
+def _fused_bwd_supported(dims):
+    ok = _bwd_shapes.get(dims)
+    if ok is None:
+        ok = _bwd_shapes[dims] = ops.bwd_supported(list(dims))
+    return ok
+
+
 def _run_bwd(x, weights, hs, dout, dws, dx):
-    if _backward_impl() == "fallback":
+    # Shapes without a fused backward (widths above 128) take the fallback:
+    # the reference's own route for shapes its fused kernel does not cover.
+    dims = tuple([int(x.shape[1])] + [int(w.shape[1]) for w in weights])
+    if _backward_impl() == "fallback" or not _fused_bwd_supported(dims):
         from . import fallback
 
         fallback.bwd(x, weights, hs, dout, dws, dx)
@@ -67,7 +80,7 @@ def _run_bwd(x, weights, hs, dout, dws, dx):
 
 
 def _use_recompute(dims, m, need_dx):
-    if need_dx or RECOMPUTE == "never" or _backward_impl() == "fallback":
+    if need_dx or RECOMPUTE == "never" or _backward_impl() == "fallback" or not _fused_bwd_supported(tuple(dims)):
         return False
     if RECOMPUTE not in ("auto", "always"):
         raise ValueError(f"RECOMPUTE must be 'auto', 'always' or 'never', got {RECOMPUTE!r}")

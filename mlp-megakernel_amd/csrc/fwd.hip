@@ -33,9 +33,13 @@ bool fwd_generic_dims(int L, const int* dims) {
   return dims[L] >= 1 && dims[L] <= 128;
 }
 
+bool fwd_wide_dims(int L, const int* dims);
+int fwd_wide_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st,
+                      LaunchInfo* info);
+
 bool fwd_supported_dims(int L, const int* dims) {
   return dims_match<Net3L128>(L, dims) || dims_match<Net5L128>(L, dims) ||
-         dims_match<NetNarrow>(L, dims) || fwd_generic_dims(L, dims);
+         dims_match<NetNarrow>(L, dims) || fwd_generic_dims(L, dims) || fwd_wide_dims(L, dims);
 }
 
 int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus,
@@ -71,6 +75,8 @@ int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, int dty
                  LaunchInfo* info) {
   if (dtype == MLPMK_DTYPE_F32) return fwd_dispatch_f32(L, dims, p, stash, st, info);
   const bool bf = dtype == MLPMK_DTYPE_BF16;
+  // Widths above 128 (up to 256): the streamed-weight kernel (fwd_wide.hip).
+  if (fwd_wide_dims(L, dims)) return fwd_wide_dispatch(L, dims, p, stash, bf, st, info);
   int cus = 0;
   const int rc = current_device_cus(&cus);
   if (rc != MLPMK_OK) return rc;

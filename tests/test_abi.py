@@ -43,19 +43,24 @@ def test_version_and_status_strings():
 
 
 @pytest.mark.parametrize(
-    "dims,ok",
-    [((128, 128, 128, 128), True), ((128,) * 6, True), ((32, 64, 64, 16), True),
+    "dims,ok,bwd_ok",
+    [((128, 128, 128, 128), True, True), ((128,) * 6, True, True), ((32, 64, 64, 16), True, True),
      # runtime-width kernels: 2..5 layers, input/hidden multiples of 16 up to
      # 128, any output width up to 128
-     ((128, 64, 128, 128), True), ((32, 128, 3), True), ((16, 48, 80, 112, 7), True), ((128,) * 5, True),
-     ((64, 128, 128, 1), True),
-     ((128, 128), False), ((100, 128, 128, 128), False), ((128, 136, 128, 128), False),
-     ((128, 256, 128), False), ((128, 128, 129), False), ((128,) * 7, False)],
+     ((128, 64, 128, 128), True, True), ((32, 128, 3), True, True), ((16, 48, 80, 112, 7), True, True),
+     ((128,) * 5, True, True), ((64, 128, 128, 1), True, True),
+     # streamed-weight forward: widths up to 256 (multiples of 16, any output
+     # width up to 256); their backward is the library-GEMM fallback, not the
+     # fused kernel
+     ((128, 256, 128), True, False), ((128, 256, 256, 128), True, False), ((256, 64, 200), True, False),
+     ((128, 128, 129), True, False), ((16, 256, 256, 256, 256, 256), True, False),
+     ((128, 128), False, False), ((100, 128, 128, 128), False, False), ((128, 136, 128, 128), False, False),
+     ((128, 272, 128), False, False), ((128, 128, 257), False, False), ((128, 248, 128), False, False),
+     ((128,) * 7, False, False)],
 )
-def test_forward_support_table(dims, ok):
+def test_forward_support_table(dims, ok, bwd_ok):
     assert ops.fwd_supported(list(dims)) is ok
-    # the backward covers the same shapes
-    assert ops.bwd_supported(list(dims)) is ok
+    assert ops.bwd_supported(list(dims)) is bwd_ok
 
 
 def _fwd(dims, x=A, w=(A, A, A), out=A, stash=None, m=256, dtype=1):

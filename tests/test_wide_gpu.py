@@ -1,0 +1,187 @@
+"""Hidden widths above 128 (up to 256): the streamed-weight forward
+(``fwd_wide.hip``) against the CPU oracle, and training of the drop-in modules
+at H = 256 through the library-GEMM fallback backward.
+
+The reference's kernel compiles for any hidden width (constexpr tile loops,
+/root/reference/kernel.py:60-123; its modules take H, README.md:62,68) and
+lists larger H as the next step (mlp_fused.md:453-454).  Tolerances as for
+the 128-wide kernels: outputs at atol = rtol = 1e-2 against the fp32 oracle
+(kernel.py:110,117 round the hidden activations to fp16 as the kernels do);
+weight gradients per entry within 2e-2 |ref| + 2e-3 max|ref| and relative
+Frobenius 1e-2.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import fused_mlp
+import kernel
+from mlpmk import ops
+from oracle import mlp_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+SHAPES = [
+    ((128, 256, 256, 128), 4096),
+    ((128, 256, 256, 128), 131072),
+    ((128, 256, 256, 128), 257),       # ragged: one full round plus one row
+    ((256, 256, 256, 256), 8192),
+    ((128, 256, 128), 3000),           # 2 layers
+    ((64, 256, 192, 100), 5001),       # runtime widths, output not a multiple of 8
+    ((16, 144, 48, 3), 777),           # one hidden width above 128, tiny output
+    ((128, 128, 129), 1024),           # only the output above 128
+    ((256, 64, 200), 999),             # input above 128
+    ((128, 256, 256, 256, 256, 128), 4096),  # 5 layers
+    ((96, 208, 160, 256, 50), 2048),   # 4 layers
+]
+
+
+def _check(got, ref, what):
+    ok, err, _ = orc.allclose_report(np.asarray(got, np.float64), ref, TOL, TOL)
+    assert ok, f"{what}: max|err| {err}"
+
+
+@pytest.mark.parametrize("dims,m", SHAPES)
+def test_wide_forward_matches_oracle(dims, m):
+    x, ws = orc.make_inputs(dims, m, seed=len(dims) * 100 + m % 97)
+    out = ops.fwd(torch.from_numpy(x).cuda(), [torch.from_numpy(w).cuda() for w in ws])
+    assert tuple(out.shape) == (m, dims[-1]) and out.dtype == torch.float16
+    _check(out.float().cpu().numpy(), orc.forward(x, ws, round_hidden=True), f"{dims} M={m}")
+    info = ops.fwd_launch_info(dims, m)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert info == {"kernel": "persistent", "rows_per_block": 32, "waves": 8,
+                    "grid": min(-(-m // 256), cus), "wgs_per_cu": 1}
+    assert kernel._mirror_policy(m, dims, cus) == (32, 8)
+
+
+def test_wide_forward_at_one_million_rows_sampled():
+    dims, m = (128, 256, 256, 128), 1 << 20
+    x, ws = orc.make_inputs(dims, m, seed=7)
+    out = ops.fwd(torch.from_numpy(x).cuda(), [torch.from_numpy(w).cuda() for w in ws])
+    idx = np.random.default_rng(0).choice(m, 8192, replace=False)
+    idx[:4] = [0, 255, 256, m - 1]  # round edges
+    _check(out.float().cpu().numpy()[idx], orc.forward(x[idx], ws, round_hidden=True), "1M sampled")
+
+
+def test_wide_forward_bf16():
+    dims, m = (128, 256, 256, 128), 4096
+    x, ws = orc.make_inputs(dims, m, seed=9, elem="bf16")
+    xb = torch.from_numpy(x).cuda().bfloat16()
+    wb = [torch.from_numpy(w).cuda().bfloat16() for w in ws]
+    out = ops.fwd(xb, wb)
+    assert out.dtype == torch.bfloat16
+    ok, err, _ = orc.allclose_report(out.float().cpu().numpy(), orc.forward(x, ws, round_hidden=True, elem="bf16"),
+                                     3e-2, 3e-2)
+    assert ok, err
+
+
+@pytest.mark.parametrize("dims,m", [((128, 256, 256, 128), 4096), ((64, 256, 192, 100), 777)])
+def test_wide_stash_matches_oracle_hidden(dims, m):
+    x, ws = orc.make_inputs(dims, m, seed=13)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    out, hs = ops.fwd(xd, wd, stash=True)
+    ref, hidden = orc.forward(x, ws, round_hidden=True, return_hidden=True)
+    _check(out.float().cpu().numpy(), ref, "out")
+    for i, (h, r) in enumerate(zip(hs, hidden)):
+        _check(h.cpu().numpy(), r, f"h{i + 1}")
+    assert torch.equal(ops.fwd(xd, wd), out)  # inference and training forward agree bit for bit
+
+
+def test_wide_forward_large_preactivations_and_nonfinite_rows():
+    # z past 88.7 (2^u overflows fp32): softplus(z) = z, as the reference's
+    # threshold gives; a row holding inf or NaN makes only its own outputs
+    # non-finite, although the kernel pads widths with zero weights.
+    dims, m = (128, 256, 256, 128), 2048
+    x, ws = orc.make_inputs(dims, m, seed=17)
+    big = np.arange(m) % 61 == 0
+    x[big] = (x[big].astype(np.float32) * 300.0).astype(np.float16)
+    x[5, 3] = np.inf
+    x[700, 0] = np.nan
+    out = ops.fwd(torch.from_numpy(x).cuda(), [torch.from_numpy(w).cuda() for w in ws]).float().cpu().numpy()
+    ref = orc.forward(x, ws, round_hidden=True)
+    bad = np.zeros(m, bool)
+    bad[[5, 700]] = True
+    assert not np.isfinite(out[bad]).all(axis=1).any()
+    assert np.isfinite(out[~bad]).all()
+    assert np.abs(ref[big & ~bad]).max() > 100.0
+    row_scale = np.abs(ref).max(axis=1, keepdims=True)
+    err = np.abs(out[~bad] - ref[~bad])
+    assert np.all(err <= TOL + TOL * np.abs(ref[~bad]) + TOL * row_scale[~bad] * big[~bad][:, None]), float(err.max())
+
+
+def test_wide_launcher_matches_model():
+    dims, m = (128, 256, 256, 64), 4096
+    x, ws = orc.make_inputs(dims, m, seed=19)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    out = kernel._fused_mlp_fwd(xd, *wd)
+    eager = kernel.Model()(xd.float(), *[w.float() for w in wd])
+    _check(out.float().cpu().numpy(), eager.cpu().numpy(), "vs eager Model")
+    assert kernel._pick_config(m, *dims)[::5] == (32, 8)
+
+
+def _torch_ref(x16, ws16):
+    x = x16.detach().cpu().double().requires_grad_(True)
+    ws = [w.detach().cpu().double().requires_grad_(True) for w in ws16]
+    a = x
+    for i, w in enumerate(ws):
+        a = a @ w
+        if i < len(ws) - 1:
+            a = F.softplus(a)
+    a.sum().backward()
+    return a.detach().numpy(), x.grad.numpy(), [w.grad.numpy() for w in ws]
+
+
+def _check_grad(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max()
+    worst = np.max(np.abs(got - ref) - (2e-2 * np.abs(ref) + 2e-3 * scale))
+    frob = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert worst <= 0 and frob < 1e-2, f"{what}: worst excess {worst:.3g}, rel frob {frob:.3g}"
+
+
+@pytest.mark.parametrize("H,n_layers", [(256, 3), (192, 5)])
+def test_module_with_wide_hidden_trains(H, n_layers):
+    torch.manual_seed(3)
+    model = fused_mlp.FusedMLPSoftplus(D=128, H=H, out_features=128, n_layers=n_layers).cuda().half()
+    x = torch.randn(4096, 128, device="cuda").half().requires_grad_(True)
+    out = model(x)
+    out.sum().backward()
+    ref_out, ref_dx, ref_dws = _torch_ref(x, list(model.weights))
+    _check(out.detach().float().cpu().numpy(), ref_out, "out")
+    for i, w in enumerate(model.weights):
+        _check_grad(w.grad.float().cpu().numpy(), ref_dws[i], f"dW{i + 1}")
+    _check(x.grad.float().cpu().numpy(), ref_dx, "dx")
+
+
+def test_weight_norm_module_with_wide_hidden_trains():
+    torch.manual_seed(4)
+    model = fused_mlp.FusedMLPSoftplusWN(D=128, H=256, out_features=128).cuda()
+    x = torch.randn(2048, 128, device="cuda").half()
+    with torch.no_grad():
+        out_inf = model(x)
+    out = model(x)
+    assert torch.equal(out.detach(), out_inf)
+    out.sum().backward()
+    assert torch.isfinite(model.v_all.grad).all() and torch.isfinite(model.g_all.grad).all()
+    # against the oracle of one weight-norm training step
+    dims = model.dims
+    xs = x.cpu().numpy()
+    w16, vs, gs = [], [], []
+    for i in range(len(dims) - 1):
+        v = model.v(i).detach().cpu().numpy()
+        g = model.g(i).detach().cpu().numpy()
+        w16.append(orc.wn_forward(v, g)[0].astype(np.float16))
+        vs.append(v)
+        gs.append(g)
+    ref, hidden = orc.forward(xs, w16, return_hidden=True, round_hidden=True)
+    _check(out.detach().float().cpu().numpy(), ref, "wn out")
+    dws, _ = orc.backward(xs, w16, hidden, np.ones(dims[-1], np.float32), need_dx=False)
+    dv, dg = zip(*[orc.wn_backward(dws[i], vs[i], gs[i]) for i in range(len(vs))])
+    _check_grad(model.v_all.grad.cpu().numpy(), np.concatenate([d.reshape(-1) for d in dv]), "dv")
+    _check_grad(model.g_all.grad.cpu().numpy(), np.concatenate(dg), "dg")
