@@ -88,8 +88,9 @@ int mlpmk_bwd_supported(int num_layers, const int* dims);
  * stash) for one more layer of MFMA and softplus work.  The reference lists
  * this trade as future work ("skip saving H in forward, recompute from X +
  * weights in backward", /root/reference/mlp_fused.md:451-452).  Supported:
- * the 3-layer 128-wide network, without dx (the recomputed layer's weight
- * fragments take the LDS that the dx layer's would need).
+ * the 3-layer and 5-layer 128-wide networks, with or without dx (the
+ * recomputing kernel reads W_{L-2}'s forward operands transposed out of the
+ * dgrad copy it stages anyway; 5 layers: mlpmk_bwd_ws / _noalloc).
  */
 int mlpmk_bwd_recompute_supported(int num_layers, const int* dims);
 
@@ -155,7 +156,6 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
  *                    stash[num_layers-2] may be NULL where
  *                    mlpmk_bwd_recompute_supported says so: the kernel then
  *                    recomputes h_{num_layers-1} from h_{num_layers-2}
- *                    (dx must be NULL in that mode)
  *   dout             dL/dout, dtype, row l at dout + l * dout_row_stride
  *                    elements; dout_row_stride = 0 broadcasts one row
  *                    (the expanded ones of loss = out.sum()), otherwise a

@@ -80,7 +80,8 @@ def _run_bwd(x, weights, hs, dout, dws, dx):
 
 
 def _use_recompute(dims, m, need_dx):
-    if need_dx or RECOMPUTE == "never" or _backward_impl() == "fallback" or not _fused_bwd_supported(tuple(dims)):
+    del need_dx  # the recomputing backward also writes dx
+    if RECOMPUTE == "never" or _backward_impl() == "fallback" or not _fused_bwd_supported(tuple(dims)):
         return False
     if RECOMPUTE not in ("auto", "always"):
         raise ValueError(f"RECOMPUTE must be 'auto', 'always' or 'never', got {RECOMPUTE!r}")

@@ -246,10 +246,8 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
   for (int l = 0; l < num_layers - 1; ++l) {
     char name[16];
     snprintf(name, sizeof(name), "stash[%d]", l);
-    if (!stash[l] && l == num_layers - 2 && num_layers > 2 && bwd_recompute_supported(num_layers, dims)) {
-      if (dx) return fail(MLPMK_ERR_INVALID_ARG, "%s is NULL (recompute mode), which computes no dx", name);
+    if (!stash[l] && l == num_layers - 2 && num_layers > 2 && bwd_recompute_supported(num_layers, dims))
       continue;  // the kernel recomputes h_{L-1}
-    }
     if ((rc = check_ptr(stash[l], name))) return rc;
     p.stash[l] = stash[l];
   }

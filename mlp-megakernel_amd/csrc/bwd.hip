@@ -111,10 +111,10 @@ struct BwdGeom {
   }
   // Recompute mode (N::rc): a_{L-1} = h_{L-1} is not read from the stash but
   // recomputed at the start of every round from h_{L-2} with W_{L-2}, whose
-  // forward A fragments take rc_frags() KiB of LDS.
+  // forward A fragments are read transposed out of its staged dgrad
+  // fragments (no LDS of their own).
   static constexpr bool RC = N::rc;
-  static constexpr int rc_frags() { return RC ? N::mbs(L - 2) * N::ks(L - 2) : 0; }
-  static constexpr int lds_bytes() { return (ndfrag() + rc_frags()) * 1024 + (fa() + fz()) * R * 2; }
+  static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
   // Per-layer prefetch: every stash layer (and x) gets its own register
   // buffer, reloaded for the next round right after its last use, so each
   // load has a whole round to arrive instead of one wgrad.  Measured at
@@ -135,7 +135,7 @@ struct BwdGeom {
     for (int i = 1; i < L; ++i)
       if (N::d[i] % 32 != 0) return false;  // hidden widths in whole 32-feature blocks
     if (DX && N::d[0] % 32 != 0) return false;
-    if (RC && (L != 3 || DX || SEG || N::gen)) return false;  // recompute: the 3-layer network, no dx
+    if (RC && (L != 3 || N::gen)) return false;  // recompute: 3-layer (segment) kernels of 128-wide networks
     return N::valid() && R >= 128 && lds_bytes() <= 163840;
   }
 };
@@ -209,35 +209,6 @@ __device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* l
   }
 }
 
-// Recompute mode: the forward A fragments of W_{L-2} (hidden to hidden, so
-// unscaled, as the forward stages them): fragment (mb, s), lane (i, g) holds
-// W[16s + 8g + j][outfeat(mb, i)].  Thread t loads the 8 x 8 tile at rows
-// 8kb.., columns 8cb.. with 16-byte row loads and transposes it in registers:
-// column q of the tile is lane (i, g)'s 16 bytes of fragment (mb, s), with
-// s = kb / 2, g = kb % 2, mb = cb / 4 and i = 16 (cb/2 % 2) + 8 (q/4) + 4 (cb % 2) + q % 4.
-template <class N, int NT>
-__device__ __forceinline__ void stage_rc_weights(const BwdParams& p, f16x8* lds) {
-  constexpr int l = N::L - 2;
-  constexpr int Nout = N::d[l + 1], KS = N::ks(l), CB = N::mbs(l) * 4, TASKS = (N::d[l] / 8) * CB;
-  static_assert(N::d[l + 1] % 32 == 0, "whole 32-feature blocks");
-  for (int t = threadIdx.x; t < TASKS; t += NT) {
-    const int kb = t / CB, cb = t % CB;
-    const f16* src = p.w[l] + (int64_t)(8 * kb) * Nout + 8 * cb;
-    f16x8 r[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = *reinterpret_cast<const f16x8*>(src + (int64_t)j * Nout);
-    const int s = kb >> 1, g = kb & 1, mb = cb >> 2;
-    const int ibase = 16 * ((cb >> 1) & 1) + 4 * (cb & 1);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      f16x8 v;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = r[j][q];
-      lds[(mb * KS + s) * 64 + 32 * g + ibase + 8 * (q >> 2) + (q & 3)] = v;
-    }
-  }
-}
-
 // Recompute mode for a network type: the backward recomputes h_{L-1} instead
 // of reading it (the forward then stashes only h_1 .. h_{L-2}).
 template <class Base>
@@ -257,7 +228,7 @@ struct BwdWave {
   static constexpr int FA = Gm::fa(), FZ = Gm::fz();  // features per exchange-tile row
 
   const BwdParams& p;
-  const f16x8* wfr;  // staged dgrad fragments (followed by the recompute fragments in RC mode)
+  const f16x8* wfr;  // staged dgrad fragments
   f16* ta;           // exchange tile: a_l, [row][feature] (FA features per row)
   f16* tz;           // exchange tile: dz_l, [row][feature] (FZ features per row)
   int lane, n, g, wid;
@@ -567,8 +538,33 @@ struct BwdWave {
     for (int s = 0; s < KSI; ++s)
       bop[s] = pack8<N::bf>(hbuf[0][s][0] * sc, hbuf[0][s][1] * sc, hbuf[0][s][2] * sc, hbuf[0][s][3] * sc,
                      hbuf[0][s][4] * sc, hbuf[0][s][5] * sc, hbuf[0][s][6] * sc, hbuf[0][s][7] * sc);
-    const int fbase = (Gm::ndfrag() * 64 + lane) * 16;
+    // Forward A fragment (output block mbo over W_l's columns, K-step so
+    // over its rows): lane (i, g) needs W_l[16 so + 8g + j][outfeat(mbo, i)],
+    // j = 0..7.  W_l is staged for dgrad with 16 contiguous bytes of a row per
+    // lane (fragment (mb_d, s_d), lane (i_d, g_d): W_l[outfeat(mb_d, i_d)]
+    // [16 s_d + 8 g_d + 0..7]), so 4 consecutive columns of one row are 8
+    // contiguous bytes there, and two ds_read_b64_tr_b16 per fragment gather
+    // the transpose.  Addressing lane u = a + 4e of a 16-lane group q serves
+    // result lanes 4a .. 4a+3 with row 16 so + 8 (q >> 1) + 4k + e (read k)
+    // and columns outfeat(mbo, 16 (q & 1) + 4a) + 0..3 = 32 mbo + 16 (q & 1) +
+    // 8 (a & 1) + 4 (a >> 1) + 0..3.  That row sits in dgrad block mb_d =
+    // so >> 1 at lane i_d = 16 (so & 1) + h(r) (h inverts outfeat within 16
+    // rows), the columns in K-step s_d = 2 mbo + (q & 1), half g_d = a & 1,
+    // bytes 8 (a >> 1) ..: a lane-dependent byte offset lk[k] plus a
+    // compile-time one per (mbo, so).
+    constexpr int KSD = Gm::dks(l);  // K-steps of W_l's dgrad fragments (its columns)
+    int lk[2];
+    {
+      const int q = lane >> 4, u = lane & 15, a = u & 3, e = u >> 2;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int r = 8 * (q >> 1) + 4 * k + e;
+        const int h = 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
+        lk[k] = Gm::dfrag_off(l) * 1024 + (q & 1) * 1024 + (32 * (a & 1) + h) * 16 + 8 * (a >> 1);
+      }
+    }
     const char* wb = reinterpret_cast<const char*>(wfr);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
     // Software pipeline over the 32-feature blocks: block mb's MFMA chain
     // shares a scheduling region with block mb - 1's activations, and the
     // fences keep the compiler from hoisting later blocks' fragment reads
@@ -578,10 +574,19 @@ struct BwdWave {
 #pragma unroll
     for (int mb = 0; mb <= MBO; ++mb) {
       if (mb < MBO) {
-        const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSI * 1024));
+        const char* b0 = wb + opaque(lk[0]);
+        const char* b1 = wb + opaque(lk[1]);
         f32x16 a = {};
 #pragma unroll
-        for (int s = 0; s < KSI; ++s) a = mfma32x32x16<N::bf>(frag[s * 64], bop[s], a);
+        for (int s = 0; s < KSI; ++s) {
+          const int off = (s >> 1) * KSD * 1024 + 2 * mb * 1024 + 256 * (s & 1);  // a constant after unrolling
+          const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)const_cast<char*>(b0 + off));
+          const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)const_cast<char*>(b1 + off));
+          a = mfma32x32x16<N::bf>(__builtin_bit_cast(f16x8, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7)),
+                                  bop[s], a);
+        }
         acc[mb & 1] = a;
       }
       if (mb > 0) {
@@ -706,7 +711,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   using Gm = BwdGeom<N, NW, DX, SEG>;
   static_assert(Gm::valid(), "unsupported backward shape");
   constexpr int R = Gm::R;
-  __shared__ f16x8 wfr[(Gm::ndfrag() + Gm::rc_frags()) * 64];
+  __shared__ f16x8 wfr[Gm::ndfrag() * 64];
   __shared__ f16 ta[Gm::fa() * R];
   __shared__ f16 tz[Gm::fz() * R];
   const int lane = threadIdx.x & 63;
@@ -731,7 +736,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
     wv.template load_h<N::L - 1>(wv.row0);
   }
   stage_dgrad_weights<N, Gm, NW * 64>(p, wfr);
-  if constexpr (Gm::RC) stage_rc_weights<N, NW * 64>(p, wfr + Gm::ndfrag() * 64);
   __syncthreads();
   for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
     wv.round();
@@ -978,17 +982,25 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
   typedef typename ElemNet<B, GBNet2>::type G2;
   typedef typename ElemNet<B, GBNet3>::type G3;
   const int64_t we = weight_elems_of(L, dims);
+  // The 128-wide 3- and 5-layer backward may also run in recompute mode
+  // (the last stash entry NULL, decided per call), whose kernel has its own
+  // grid: size for the larger of the two.
   if (bdims_match<BNet3L128>(L, dims)) {
     int rc = bwd_workspace_any<N3, 4>(M, dx, we, bytes);
-    if (rc != MLPMK_OK || dx) return rc;
-    // Without dx the backward may also run in recompute mode (stash[1] NULL,
-    // decided per call), whose kernel has its own grid: size for the larger.
+    if (rc != MLPMK_OK) return rc;
     int64_t rcb = 0;
-    rc = partial_bytes<Recompute<N3>, 4, false>(M, we, &rcb);
+    rc = dx ? partial_bytes<Recompute<N3>, 4, true>(M, we, &rcb) : partial_bytes<Recompute<N3>, 4, false>(M, we, &rcb);
     if (rc == MLPMK_OK && rcb > *bytes) *bytes = rcb;
     return rc;
   }
-  if (bdims_match<BNet5L128>(L, dims)) return bwd_split_workspace<N3, N2>(L, dims, M, dx, bytes);
+  if (bdims_match<BNet5L128>(L, dims)) {
+    int rc = bwd_split_workspace<N3, N2>(L, dims, M, dx, bytes);
+    if (rc != MLPMK_OK) return rc;
+    int64_t rcb = 0;
+    rc = bwd_split_workspace<Recompute<N3>, N2>(L, dims, M, dx, &rcb);
+    if (rc == MLPMK_OK && rcb > *bytes) *bytes = rcb;
+    return rc;
+  }
   if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<NN, 4>(M, dx, we, bytes);
   if (bwd_generic_dims(L, dims)) {
     switch (L) {
@@ -1043,12 +1055,14 @@ int scratch_workspace(void** ptr, int64_t* bytes) {
 
 bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims); }
 
-// The 3-layer 128-wide network also runs in recompute mode: with a NULL
-// stash for h_2 (the forward then writes only h_1) the backward recomputes
-// h_2 from h_1 at the start of every round; no dx in that mode (the W_2
-// forward fragments take the LDS that dx's W_1 dgrad fragments would need).
-// The no-dx workspace size covers both kernels' grids (bwd_workspace_t).
-bool bwd_recompute_supported(int L, const int* dims) { return bdims_match<BNet3L128>(L, dims); }
+// The 3- and 5-layer 128-wide networks also run in recompute mode: with a
+// NULL stash entry for h_{L-1} (the forward then does not write it) the
+// backward recomputes it from h_{L-2} at the start of every round (for 5
+// layers in the launch of layers 4..2), with or without dx.  The workspace
+// size covers both kernels' grids (bwd_workspace_t).
+bool bwd_recompute_supported(int L, const int* dims) {
+  return bdims_match<BNet3L128>(L, dims) || bdims_match<BNet5L128>(L, dims);
+}
 
 template <bool B>
 static int bwd_dispatch_t(int L, const int* dims, const BwdParams& p, hipStream_t st) {
@@ -1057,11 +1071,9 @@ static int bwd_dispatch_t(int L, const int* dims, const BwdParams& p, hipStream_
   typedef typename ElemNet<B, BNetNarrow>::type NN;
   typedef typename ElemNet<B, GBNet2>::type G2;
   typedef typename ElemNet<B, GBNet3>::type G3;
-  if (bdims_match<BNet3L128>(L, dims) && !p.stash[1]) {
-    if (p.dx) return fail(MLPMK_ERR_INVALID_ARG, "recomputing h_2 (stash[1] == NULL) has no dx");
-    return launch_bwd<Recompute<N3>, 4, false>(p, st);
-  }
+  if (bdims_match<BNet3L128>(L, dims) && !p.stash[1]) return launch_bwd_any<Recompute<N3>, 4>(p, st);
   if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<N3, 4>(p, st);
+  if (bdims_match<BNet5L128>(L, dims) && !p.stash[3]) return launch_bwd_split<Recompute<N3>, N2>(p, L, st);
   if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<N3, N2>(p, L, st);
   if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<NN, 4>(p, st);
   if (bwd_generic_dims(L, dims)) {

@@ -233,7 +233,7 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     workgroups go through a workspace from torch's allocator and a second
     kernel (``mlpmk_bwd_ws``); otherwise every workgroup adds its partials
     with fp32 atomics (``mlpmk_bwd``).  A None last stash entry selects the
-    recomputing backward (``bwd_recompute_supported``; no dx).
+    recomputing backward (``bwd_recompute_supported``; with or without dx).
     """
     dev = x.device
     code = _elem_code(x.dtype)

@@ -1,10 +1,11 @@
-"""Recomputing backward of the 3-layer 128-wide network: the training forward
-writes only h_1, and the backward recomputes h_2 = softplus(h_1 W_2) for every
-block of rows from h_1 and W_2 instead of reading a stashed h_2 -- the
-activation recomputation the reference lists as future work
-(/root/reference/mlp_fused.md:451-452).  Parity against the CPU oracle with the
-weight-gradient tolerance of test_bwd_gpu.py, and against the stashing
-backward on the same inputs.
+"""Recomputing backward of the 3- and 5-layer 128-wide networks: the training
+forward does not write the last hidden activation h_{L-1}, and the backward
+recomputes it, softplus(h_{L-2} W_{L-2}), for every block of rows instead of
+reading it from the stash -- the activation recomputation the reference lists
+as future work (/root/reference/mlp_fused.md:451-452) -- with or without dx.
+Parity against the CPU oracle with the weight-gradient tolerance of
+test_bwd_gpu.py (dx at 1e-2 / 1e-2), and against the stashing backward on the
+same inputs.
 """
 import numpy as np
 import pytest
@@ -38,7 +39,9 @@ def _train(x, ws, dout_mode, recompute, workspace=True, seed=0):
 
 def test_support_and_stash_layout():
     assert ops.bwd_recompute_supported(D3)
-    assert not ops.bwd_recompute_supported([128] * 6)
+    assert ops.bwd_recompute_supported([128] * 6)
+    for dims in ([128] * 5, [32, 64, 64, 16], [64, 64, 64, 64], [128, 256, 256, 128]):
+        assert not ops.bwd_recompute_supported(dims), dims
     x, ws = orc.make_inputs(D3, 3000, seed=1)
     xd = torch.from_numpy(x).cuda()
     wd = [torch.from_numpy(w).cuda() for w in ws]
@@ -129,14 +132,72 @@ def test_recompute_operands_beyond_fp16():
         assert _rel(dws_rc[i], dws_st[i]) < 2e-3, f"dW{i + 1}: {_rel(dws_rc[i], dws_st[i]):.3g}"
 
 
-def test_recompute_rejects_dx():
-    x = torch.randn((256, 128), device="cuda").half()
-    wd = [(torch.randn((128, 128), device="cuda") / 128 ** 0.5).half() for _ in range(3)]
-    _, hs = ops.fwd(x, wd, stash=True, recompute=True)
-    dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
-    dout = torch.ones((256, 128), dtype=torch.float16, device="cuda")
-    with pytest.raises(ops.MlpmkError, match="dx"):
-        ops.bwd(x, wd, hs, dout, dws, torch.empty_like(x))
+def _train_dx(dims, x, ws, dout_np, recompute):
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    out, hs = ops.fwd(xd, wd, stash=True, recompute=recompute)
+    dout = torch.from_numpy(dout_np).cuda()
+    dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(len(dims) - 1)]
+    dx = torch.empty_like(xd)
+    ops.bwd(xd, wd, hs, dout, dws, dx)
+    torch.cuda.synchronize()
+    return out, hs, [d.cpu().numpy() for d in dws], dx.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dims", [D3, [128] * 6])
+@pytest.mark.parametrize("m", [100, 4096, 65536])
+def test_recompute_backward_with_dx(dims, m):
+    x, ws = orc.make_inputs(dims, m, seed=m % 37)
+    dout_np = np.random.default_rng(m).standard_normal((m, dims[-1])).astype(np.float16)
+    out_rc, hs_rc, dws_rc, dx_rc = _train_dx(dims, x, ws, dout_np, recompute=True)
+    out_st, hs_st, dws_st, dx_st = _train_dx(dims, x, ws, dout_np, recompute=False)
+    assert hs_rc[-1] is None and torch.equal(out_rc, out_st)
+    _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    rdws, rdx = orc.backward(x, ws, ref_h, dout_np.astype(np.float32), need_dx=True)
+    for i in range(len(dims) - 1):
+        check_dw(dws_rc[i], rdws[i], f"recompute dW{i + 1} M={m}")
+        assert _rel(dws_rc[i], dws_st[i]) < 2e-3, f"dW{i + 1} M={m}: recompute vs stash"
+    ok, err, _ = orc.allclose_report(dx_rc, rdx, 1e-2, 1e-2)
+    assert ok, f"dx M={m}: {err}"
+    assert _rel(dx_rc, dx_st) < 2e-3
+
+
+@pytest.mark.parametrize("m", [100, 5000, 131072])
+def test_five_layer_forward_without_h4_writes_the_same_bits(m):
+    g = torch.Generator(device="cuda").manual_seed(m)
+    x = torch.randn((m, 128), generator=g, device="cuda").half()
+    wd = [(torch.randn((128, 128), generator=g, device="cuda") / 128 ** 0.5).half() for _ in range(5)]
+    out_full, hs_full = ops.fwd(x, wd, stash=True)
+    out_rc, hs_rc = ops.fwd(x, wd, stash=True, recompute=True)
+    assert hs_rc[3] is None and torch.equal(out_full, out_rc)
+    for a, b in zip(hs_full[:3], hs_rc[:3]):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("m", [4096, 131072])
+@pytest.mark.parametrize("dout_mode", ["ones", "dense"])
+def test_five_layer_recompute_backward_matches_oracle_and_stash(m, dout_mode):
+    dims = [128] * 6
+    x, ws = orc.make_inputs(dims, m, seed=m % 53)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    if dout_mode == "ones":
+        dout_np = np.ones((m, 128), np.float16)
+        dout = torch.ones((1, 128), dtype=torch.float16, device="cuda").expand(m, 128)
+    else:
+        dout_np = np.random.default_rng(m + 1).standard_normal((m, 128)).astype(np.float16)
+        dout = torch.from_numpy(dout_np).cuda()
+    res = {}
+    for rc in (True, False):
+        _, hs = ops.fwd(xd, wd, stash=True, recompute=rc)
+        dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(5)]
+        ops.bwd(xd, wd, hs, dout, dws, None)
+        res[rc] = [d.cpu().numpy() for d in dws]
+    _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    rdws, _ = orc.backward(x, ws, ref_h, dout_np.astype(np.float32), need_dx=False)
+    for i in range(5):
+        check_dw(res[True][i], rdws[i], f"5L recompute dW{i + 1} M={m} {dout_mode}")
+        assert _rel(res[True][i], res[False][i]) < 2e-3, f"5L dW{i + 1} M={m}: recompute vs stash"
 
 
 @pytest.mark.parametrize("wn", [False, True])
@@ -152,8 +213,9 @@ def test_modules_recompute_policy(wn):
     model = cls().cuda()
     x = torch.randn(5000, 128, device="cuda").half()
     assert mag._use_recompute(tuple(model.dims), 1 << 20, False)
-    assert not mag._use_recompute(tuple(model.dims), 1 << 20, True)
-    assert not mag._use_recompute((128,) * 6, 1 << 20, False)
+    assert mag._use_recompute(tuple(model.dims), 1 << 20, True)  # dx too
+    assert mag._use_recompute((128,) * 6, 1 << 20, False)
+    assert not mag._use_recompute((128,) * 5, 1 << 20, False)  # 4 layers: no recomputing kernel
     grads = {}
     policy = mag.RECOMPUTE
     try:
@@ -161,11 +223,34 @@ def test_modules_recompute_policy(wn):
             mag.RECOMPUTE = pol
             for p in model.parameters():
                 p.grad = None
-            model(x).float().sum().backward()
+            xg = x.clone().requires_grad_(True)
+            model(xg).float().sum().backward()  # dx wanted too
             grads[pol] = [p.grad.detach().float().cpu().numpy() for p in model.parameters()]
-        xg = x.clone().requires_grad_(True)
-        model(xg).float().sum().backward()  # dx wanted: the stash path
-        assert xg.grad is not None and torch.isfinite(xg.grad).all()
+            grads[pol].append(xg.grad.float().cpu().numpy())
+    finally:
+        mag.RECOMPUTE = policy
+    for a, b in zip(grads["always"], grads["never"]):
+        assert _rel(a, b) < 2e-3
+
+
+def test_five_layer_module_recompute_policy():
+    import fused_mlp5
+    from mlpmk import autograd as mag
+
+    torch.manual_seed(1)
+    model = fused_mlp5.FusedMLP5Softplus().cuda().half()
+    x = torch.randn(4096, 128, device="cuda").half()
+    grads = {}
+    policy = mag.RECOMPUTE
+    try:
+        for pol in ("never", "always"):
+            mag.RECOMPUTE = pol
+            for p in model.parameters():
+                p.grad = None
+            xg = x.clone().requires_grad_(True)
+            model(xg).float().sum().backward()
+            grads[pol] = [p.grad.detach().float().cpu().numpy() for p in model.parameters()]
+            grads[pol].append(xg.grad.float().cpu().numpy())
     finally:
         mag.RECOMPUTE = policy
     for a, b in zip(grads["always"], grads["never"]):
