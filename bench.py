@@ -734,6 +734,10 @@ def main():
         result["training_stash_vs_recompute"] = {
             str(mt): {pol: train_step_bench(torch, mt, steps=20, warmup=5, recompute=pol) for pol in ("never", "always")}
             for mt in (131072, 1048576)}
+        result["training_stash_vs_recompute_5l"] = {
+            str(mt): {pol: train_step_bench(torch, mt, steps=20, warmup=5, n_layers=5, recompute=pol)
+                      for pol in ("never", "always")}
+            for mt in (131072, 1048576)}
         result["backward_vs_pytorch_fallback"] = {str(mt): backward_comparison(torch, ops, mt)
                                                   for mt in (4096, 32768, 131072, 1048576)}
 
