@@ -33,6 +33,12 @@
 //    hardware float atomics (small grids) or writes them to its workgroup's
 //    slot of a partial-sum workspace, which bwd_combine_kernel then reduces
 //    in a fixed order (no atomics, bitwise-reproducible).
+//  * dz through LDS (3-layer and smaller networks, DZL): the dgrad reads its
+//    B operands from the exchange tile the wave wrote and writes dz_{l-1}
+//    into a second tile, so no dz stays in registers between layers, and the
+//    registers that frees let every layer's rows of the next round be
+//    requested as soon as this round has consumed them: HBM always has the
+//    next rows in flight.
 //
 // Segment mode (SEG) runs the upper layers of a deeper network on their own:
 // layer 0 of the segment then takes its activation from the fp32 stash of
@@ -114,15 +120,21 @@ struct BwdGeom {
   // forward A fragments are read transposed out of its staged dgrad
   // fragments (no LDS of their own).
   static constexpr bool RC = N::rc;
-  static constexpr int lds_bytes() { return ndfrag() * 1024 + (fa() + fz()) * R * 2; }
+  static constexpr int lds_bytes_with(int ntz) { return ndfrag() * 1024 + (fa() + ntz * fz()) * R * 2; }
+  // dz through LDS: the dgrad reads its B operands (dz_l, the wave's own
+  // rows) from the exchange tile and writes dz_{l-1} into a second one, so no
+  // dz is held in registers across phases.  The 64 registers that frees
+  // carry the per-layer prefetch below for 3-layer networks.
+  static constexpr bool dzl() { return !N::gen && !SEG && !RC && L <= 3 && lds_bytes_with(2) <= 163840; }
+  static constexpr int lds_bytes() { return lds_bytes_with(dzl() ? 2 : 1); }
   // Per-layer prefetch: every stash layer (and x) gets its own register
-  // buffer, reloaded for the next round right after its last use, so each
-  // load has a whole round to arrive instead of one wgrad.  Measured at
-  // M = 131072: the two-layer kernel (lower half of the 5-layer backward)
-  // 37.5 -> 34.4 us; the 3-layer 128-wide kernel spills with it, and the
-  // narrow one gains nothing (20.6 vs 21.2 us), so they share one buffer
-  // loaded one phase ahead.
-  static constexpr bool pf() { return !N::gen && !SEG && L <= 2; }
+  // buffer, reloaded for the next round right after its last use, so HBM
+  // always has this wave's next rows in flight instead of one phase's rows
+  // at a time between compute bursts.  Measured at M = 131072: the
+  // two-layer kernel (lower half of the 5-layer backward) 37.5 -> 34.4 us.
+  // Without dz through LDS the 3-layer 128-wide kernel spills with it, so
+  // such kernels share one buffer loaded one phase ahead.
+  static constexpr bool pf() { return !N::gen && !SEG && (L <= 2 || dzl()); }
   // Element offset of dW_l in the dW blocks laid out back to back.
   static constexpr int woff(int l) {
     int o = 0;
@@ -193,10 +205,10 @@ __device__ __forceinline__ void dgrad_load_all(const BwdParams& p, f16x8 (&v)[N:
   }
 }
 
+// Writes the fragment lanes dgrad_load_all loaded into LDS.
 template <class N, class Gm, int NT>
-__device__ __forceinline__ void stage_dgrad_weights(const BwdParams& p, f16x8* lds) {
-  f16x8 v[N::L][DgradStage<N, Gm>::template per<NT>()];
-  dgrad_load_all<N, Gm, NT>(p, v);
+__device__ __forceinline__ void dgrad_store_all(const f16x8 (&v)[N::L][DgradStage<N, Gm>::template per<NT>()],
+                                                f16x8* lds) {
 #pragma unroll
   for (int l = 0; l < N::L; ++l) {
     if (!Gm::has_dgrad(l)) continue;
@@ -226,11 +238,12 @@ struct BwdWave {
   static constexpr int KS0 = N::d[0] / 16;
   static constexpr int KSL = N::d[L] / 16;
   static constexpr int FA = Gm::fa(), FZ = Gm::fz();  // features per exchange-tile row
+  static constexpr bool DZL = Gm::dzl();
 
   const BwdParams& p;
   const f16x8* wfr;  // staged dgrad fragments
   f16* ta;           // exchange tile: a_l, [row][feature] (FA features per row)
-  f16* tz;           // exchange tile: dz_l, [row][feature] (FZ features per row)
+  f16* tz;           // exchange tile: dz_l, [row][feature] (FZ features per row); two of them with DZL
   int lane, n, g, wid;
   int64_t row0;    // first row of this wave's 32 in the current round
   int64_t rstep;   // rows between a workgroup's consecutive rounds
@@ -241,9 +254,21 @@ struct BwdWave {
 
   // Prefetched rows (issued one phase ahead of their use).
   static constexpr bool PF = Gm::pf();
+  // With DZL, x and dL/dout take turns in one buffer: dL/dout is written to
+  // its tile at the start of a round, then the round's x rows are loaded
+  // into the buffer, and once they are in the a_0 tile the next round's
+  // dL/dout is.
+  static constexpr bool SHX = DZL && PF && KS0 == KSL;
+  static constexpr bool EARLY = DZL && PF;  // next-round rows requested before the layer's barrier
   f16x8 gbuf[KSL];                 // dL/dout of the round = dz_{L-1}
   float hbuf[PF ? L : 1][KSH][8];  // h_l, fp32: buffer l (PF) or one shared buffer
-  f16x8 xbuf[KS0];     // x rows
+  f16x8 xown[SHX ? 1 : KS0];       // x rows (SHX: in gbuf)
+  __device__ __forceinline__ f16x8 (&xbuf())[KS0] {
+    if constexpr (SHX)
+      return *reinterpret_cast<f16x8(*)[KS0]>(gbuf);
+    else
+      return *reinterpret_cast<f16x8(*)[KS0]>(xown);
+  }
 
   // Tile layout: element (r, f) of a tile with F features per row sits at
   // r*F + (f ^ swz(r, F)).  The XOR moves whole 8-feature chunks, so every
@@ -342,7 +367,7 @@ struct BwdWave {
     const rsrc_t xr = rows_rsrc(p.x, D, 2, r0);
 #pragma unroll
     for (int s = 0; s < KS0; ++s)
-      xbuf[s] = (N::gen && 16 * s >= D)
+      xbuf()[s] = (N::gen && 16 * s >= D)
                     ? f16x8{}
                     : __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
                                                     xr, (int)((n * D + 16 * s + 8 * g) * 2), 0, 0));
@@ -376,8 +401,39 @@ struct BwdWave {
   // Wgrad of layer l over the R rows in the exchange tiles, for this wave's
   // tiles.  K-steps (16 rows) outermost keeps only one step's fragments live.
   template <int l>
-  __device__ __forceinline__ void wgrad() {
+  __device__ __forceinline__ void wgrad(const f16* tz) const {
     constexpr int OFF = Gm::tpw_off(l);
+    if constexpr (!N::gen && Gm::quad(l) && Gm::quads(l) == NW) {
+      // One 2x2 block of tiles per wave: the four operands of K-step kk + 1
+      // are read while the four MFMAs of K-step kk run (two register sets),
+      // one scheduling region per K-step.
+      constexpr int QO = Gm::wob(l) / 2;
+      constexpr int KK = R / 16;
+      const int fi = 64 * (wid / QO), fo = 64 * (wid % QO);
+      f16x8 op[2][4];
+      op[0][0] = xread<FA>(ta, fi, 0);
+      op[0][1] = xread<FA>(ta, fi + 32, 0);
+      op[0][2] = xread<FZ>(tz, fo, 0);
+      op[0][3] = xread<FZ>(tz, fo + 32, 0);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int c = kk & 1;
+        if (kk + 1 < KK) {
+          op[c ^ 1][0] = xread<FA>(ta, fi, kk + 1);
+          op[c ^ 1][1] = xread<FA>(ta, fi + 32, kk + 1);
+          op[c ^ 1][2] = xread<FZ>(tz, fo, kk + 1);
+          op[c ^ 1][3] = xread<FZ>(tz, fo + 32, kk + 1);
+        }
+        wacc[OFF + 0] = mfma32x32x16<N::bf>(op[c][0], op[c][2], wacc[OFF + 0]);
+        wacc[OFF + 1] = mfma32x32x16<N::bf>(op[c][0], op[c][3], wacc[OFF + 1]);
+        wacc[OFF + 2] = mfma32x32x16<N::bf>(op[c][1], op[c][2], wacc[OFF + 2]);
+        wacc[OFF + 3] = mfma32x32x16<N::bf>(op[c][1], op[c][3], wacc[OFF + 3]);
+        if (kk + 1 < KK) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads first
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                   // then the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
 #pragma unroll
     for (int kk = 0; kk < R / 16; ++kk) {
       if constexpr (Gm::quad(l)) {
@@ -406,6 +462,49 @@ struct BwdWave {
     }
   }
 
+  // dgrad output block mb of layer l (features 32mb .. 32mb+31 of a_l, this
+  // wave's 32 rows): registers 0..7 of the accumulator hold features 32mb +
+  // 8g + [0..7] (K-step 2mb of a_l), 8..15 hold 32mb + 16 + 8g + [0..7]
+  // (K-step 2mb + 1).  Through a stash layer (HA) it is multiplied by
+  // sigma(z) = 1 - exp(-h_l) into dz_{l-1} (or, for a segment's layer 0, the
+  // dz handed to the launch below through p.dx); otherwise it is dx itself.
+  template <int l, bool HA, int B>
+  __device__ __forceinline__ void dgrad_epilogue(int mb, const f32x16& acc, f16x8 (&dzn)[KSM], f16* tout) const {
+    if constexpr (HA) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[j] = acc[j] * sig_from_h(hbuf[B][2 * mb][j]);
+        v[8 + j] = acc[8 + j] * sig_from_h(hbuf[B][2 * mb + 1][j]);
+      }
+      const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+      const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
+      if constexpr (l >= 1 && DZL) {  // the wave's own rows of the dz_{l-1} tile
+        const int r = wsw, sw = swz(r, FZ);
+        *reinterpret_cast<f16x8*>(tout + r * FZ + ((32 * mb + 8 * g) ^ sw)) = lo;
+        *reinterpret_cast<f16x8*>(tout + r * FZ + ((32 * mb + 16 + 8 * g) ^ sw)) = hi;
+      } else if constexpr (l >= 1) {
+        dzn[2 * mb] = lo;
+        dzn[2 * mb + 1] = hi;
+      } else {  // segment: dz of the layer below leaves through p.dx
+        const int D = dw_(0);
+        const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
+        const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
+        if (!N::gen || 32 * mb < D) buf_store16(lo, dr, e * 2);
+        if (!N::gen || 32 * mb + 16 < D) buf_store16(hi, dr, e * 2 + 32);
+      }
+    } else {
+      const int D = dw_(0);  // a multiple of 16 for Gen networks
+      const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
+      const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
+      if (!N::gen || 32 * mb < D)
+        buf_store16(pack8<N::bf>(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
+      if (!N::gen || 32 * mb + 16 < D)
+        buf_store16(pack8<N::bf>(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
+                    e * 2 + 32);
+    }
+  }
+
   // One layer of the backward for this wave's 32 rows.  On entry dz holds
   // dz_l and hbuf (l >= 1, or a segment) or xbuf (l = 0) holds a_l.
   // Publishes a_l and dz_l to the exchange tiles, runs dgrad into
@@ -418,11 +517,15 @@ struct BwdWave {
     constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
     constexpr bool HA = l >= 1 || SEG;     // a_l came from a stash (fp32, in hbuf)
     constexpr int B = PF ? l : 0;          // its buffer
-    {
+    // dz tiles: dz_l is read from tin; with DZL the dgrad writes dz_{l-1}
+    // into the other tile (the layers alternate, starting from tile 0).
+    f16* const tin = tz + (DZL ? ((L - 1 - l) & 1) * FZ * R : 0);
+    f16* const tout = tz + (DZL ? ((L - l) & 1) * FZ * R : 0);
+    if constexpr (!DZL) {
       f16x8 zs[KSZ];
 #pragma unroll
       for (int s = 0; s < KSZ; ++s) zs[s] = dz[s];
-      xwrite<FZ>(tz, zs);
+      xwrite<FZ>(tin, zs);
     }
     if constexpr (HA) {
       f16x8 as[KSA];
@@ -432,53 +535,17 @@ struct BwdWave {
                       hbuf[B][s][6], hbuf[B][s][7]);
       xwrite<FA>(ta, as);
     } else {
-      xwrite<FA>(ta, xbuf);
+      xwrite<FA>(ta, xbuf());
+      if constexpr (SHX)
+        load_dout(row0 + rstep);  // x is consumed: the next round's dL/dout takes its buffer
+      else if constexpr (EARLY)
+        load_x(row0 + rstep);  // x is consumed: the next round's rows
     }
-    if constexpr (Gm::has_dgrad(l)) {
-      constexpr int MB = N::d[l] / 32;
-      const int fbase = (Gm::dfrag_off(l) * 64 + lane) * 16;
-      const char* wb = reinterpret_cast<const char*>(wfr);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSZ * 1024));
-        f32x16 acc = {};
-#pragma unroll
-        for (int s = 0; s < KSZ; ++s) acc = mfma32x32x16<N::bf>(frag[s * 64], dz[s], acc);
-        // Registers 0..7: features 32mb + 8g + [0..7] (K-step 2mb of a_l);
-        // 8..15: 32mb + 16 + 8g + [0..7] (K-step 2mb + 1).
-        if constexpr (HA) {
-          float v[16];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            v[j] = acc[j] * sig_from_h(hbuf[B][2 * mb][j]);
-            v[8 + j] = acc[8 + j] * sig_from_h(hbuf[B][2 * mb + 1][j]);
-          }
-          const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-          const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
-          if constexpr (l >= 1) {
-            dzn[2 * mb] = lo;
-            dzn[2 * mb + 1] = hi;
-          } else {  // segment: dz of the layer below leaves through p.dx
-            const int D = dw_(0);
-            const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
-            const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
-            if (!N::gen || 32 * mb < D) buf_store16(lo, dr, e * 2);
-            if (!N::gen || 32 * mb + 16 < D) buf_store16(hi, dr, e * 2 + 32);
-          }
-        } else {
-          const int D = dw_(0);  // a multiple of 16 for Gen networks
-          const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
-          const uint32_t e = (uint32_t)(n * D + 32 * mb + 8 * g);
-          if (!N::gen || 32 * mb < D)
-            buf_store16(pack8<N::bf>(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]), dr, e * 2);
-          if (!N::gen || 32 * mb + 16 < D)
-            buf_store16(pack8<N::bf>(acc[8], acc[9], acc[10], acc[11], acc[12], acc[13], acc[14], acc[15]), dr,
-                        e * 2 + 32);
-        }
-      }
-    }
+    if constexpr (Gm::has_dgrad(l)) dgrad<l, HA, B>(dz, dzn, tin, tout);
+    if constexpr (EARLY && HA) load_h<l>(row0 + rstep);  // h_l is consumed (sigma done): the next round's rows
     __syncthreads();  // every wave's rows are in the exchange tiles
-    if constexpr (PF) {  // this layer's buffer is free: the next round's rows
+    if constexpr (EARLY) {
+    } else if constexpr (PF) {  // this layer's buffer is free: the next round's rows
       if constexpr (HA)
         load_h<l>(row0 + rstep);
       else
@@ -494,8 +561,82 @@ struct BwdWave {
       else if constexpr (L >= 2)
         load_h<L - 1>(row0 + rstep);
     }
-    wgrad<l>();
+    wgrad<l>(tin);
     __syncthreads();  // the tiles are free for the next layer
+  }
+
+  // dgrad of layer l for this wave's 32 rows: dz_l (B operands: registers dz,
+  // or with DZL the wave's own rows of tile tin) times the staged W_l
+  // fragments, through the epilogue into dzn / tout / p.dx.
+  //
+  // Software pipeline over the 32-feature output blocks: block mb's MFMA
+  // chain shares a scheduling region with block mb - 1's epilogue (VALU), and
+  // the A fragments run through a ring of NQ reads in flight (fragment t + NQ
+  // is requested right after the MFMA that consumes fragment t), so neither
+  // the LDS latency nor the epilogue sits between two MFMAs of a chain.  One
+  // opaque base keeps the reads on immediate offsets of a single address
+  // register.  Runtime-width networks keep one block at a time: their
+  // register budget has no room for the ring.
+  template <int l, bool HA, int B>
+  __device__ __forceinline__ void dgrad(const f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM], const f16* tin, f16* tout) {
+    constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
+    constexpr int MB = N::d[l] / 32;
+    constexpr int NF = MB * KSZ;
+    constexpr int NQ = NF < 4 ? NF : 4;
+    if constexpr (N::gen) {
+      const int fbase = (Gm::dfrag_off(l) * 64 + lane) * 16;
+      const char* wb = reinterpret_cast<const char*>(wfr);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const f16x8* frag = reinterpret_cast<const f16x8*>(wb + opaque(fbase + mb * KSZ * 1024));
+        f32x16 a = {};
+#pragma unroll
+        for (int s = 0; s < KSZ; ++s) a = mfma32x32x16<N::bf>(frag[s * 64], dz[s], a);
+        dgrad_epilogue<l, HA, B>(mb, a, dzn, tout);
+      }
+      return;
+    }
+    f16x8 zb[KSZ];
+    const int zr = wsw, zsw = swz(zr, FZ);
+    auto zread = [&](int s) { return *reinterpret_cast<const f16x8*>(tin + zr * FZ + ((16 * s + 8 * g) ^ zsw)); };
+    if constexpr (DZL) {  // rows this wave wrote itself: no barrier needed
+    } else {
+#pragma unroll
+      for (int s = 0; s < KSZ; ++s) zb[s] = dz[s];
+    }
+    const char* wb = reinterpret_cast<const char*>(wfr) + opaque((Gm::dfrag_off(l) * 64 + lane) * 16);
+    f16x8 fq[NQ];
+#pragma unroll
+    for (int t = 0; t < NQ; ++t) fq[t] = *reinterpret_cast<const f16x8*>(wb + t * 1024);
+    f32x16 acc[2];
+#pragma unroll
+    for (int mb = 0; mb <= MB; ++mb) {
+      if (mb < MB) {
+        f32x16 a = {};
+#pragma unroll
+        for (int s = 0; s < KSZ; ++s) {
+          const int t = mb * KSZ + s;
+          a = mfma32x32x16<N::bf>(fq[t % NQ], DZL ? zread(s) : zb[s], a);
+          if (t + NQ < NF) fq[t % NQ] = *reinterpret_cast<const f16x8*>(wb + (t + NQ) * 1024);
+        }
+        if constexpr (DZL)
+          dgrad_epilogue<l, HA, B>(mb, a, dzn, tout);
+        else
+          acc[mb & 1] = a;
+      }
+      if (!DZL && mb > 0) dgrad_epilogue<l, HA, B>(mb - 1, acc[(mb - 1) & 1], dzn, tout);
+      if (mb < MB) {
+        // Per MFMA: the MFMA, the read it frees a ring slot for, a share of
+        // the previous block's epilogue.
+#pragma unroll
+        for (int s = 0; s < KSZ; ++s) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (mb * KSZ + s + NQ < NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (!DZL && mb > 0) __builtin_amdgcn_sched_group_barrier(0x002, 160 / KSZ, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   // First round with per-layer prefetch: every layer's rows.
@@ -503,7 +644,7 @@ struct BwdWave {
   __device__ __forceinline__ void prefetch_all(int64_t r0) {
     if constexpr (l >= 1 || SEG)
       load_h<l>(r0);
-    else
+    else if constexpr (!SHX)  // (SHX: each round loads its own x)
       load_x(r0);
     if constexpr (l > 0) prefetch_all<l - 1>(r0);
   }
@@ -643,9 +784,16 @@ struct BwdWave {
   __device__ __forceinline__ void round() {
     if constexpr (Gm::RC) recompute();
     f16x8 dz[KSM], dzn[KSM];
+    if constexpr (DZL) {
+      xwrite<FZ>(tz, gbuf);  // dz_{L-1} = dL/dout into tile 0
+    } else {
 #pragma unroll
-    for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
-    if constexpr (PF) load_dout(row0 + rstep);
+      for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
+    }
+    if constexpr (SHX)
+      load_x(row0);  // this round's x into the buffer dL/dout left
+    else if constexpr (PF)
+      load_dout(row0 + rstep);
     phases_from<L - 1>(dz, dzn);
   }
 
@@ -665,23 +813,41 @@ struct BwdWave {
       }
     }
     const int fo = 32 * to + (lane & 31);
-    float* const part = p.part ? p.part + (int64_t)blockIdx.x * welems + woff : nullptr;
+    // C layout: lane (o, g) holds rows 8a + 4g + b of its column, register 4a + b.
+    if (p.part) {
+      // Buffer stores over this workgroup's block of dW_l: a per-lane offset
+      // (column, g) and a wave-uniform one per register, so the stores need
+      // no 64-bit addresses.  Each element goes through an opaque copy:
+      // stores of single accumulator elements have been compiled as stores
+      // of element 0.
+      const rsrc_t r = make_rsrc(p.part + (int64_t)blockIdx.x * welems + woff, (uint32_t)(K * NO * 4));
+      const int vo = (4 * g * NO + fo) * 4;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      // C layout: lane (o, g) holds rows 8a + 4g + b of its column, register 4a + b.
-      const int fi = 32 * ti + 8 * (e >> 2) + 4 * g + (e & 3);
-      if (fi < K && fo < NO) {
-        if (part)
-          part[fi * NO + fo] = acc[e];
-        else
-          unsafeAtomicAdd(p.dw[l] + (int64_t)fi * NO + fo, acc[e]);
+      for (int e = 0; e < 16; ++e) {
+        const int fr = 32 * ti + 8 * (e >> 2) + (e & 3);
+        float t = acc[e];
+        asm volatile("" : "+v"(t));
+        if (fr + 4 * g < K && fo < NO)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, t), r, vo, fr * NO * 4, 0);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int fi = 32 * ti + 8 * (e >> 2) + 4 * g + (e & 3);
+        if (fi < K && fo < NO) unsafeAtomicAdd(p.dw[l] + (int64_t)fi * NO + fo, acc[e]);
       }
     }
   }
 
-  // Adds the owned tiles of every dW_l to global memory (fp32 atomics).
   template <int l>
-  __device__ __forceinline__ void flush() {
+  __device__ __forceinline__ void flush_all() const {
+    flush<l>();
+    if constexpr (l + 1 < L) flush_all<l + 1>();
+  }
+  // Adds this wave's tiles of dW_l to global memory (fp32 atomics) or
+  // stores them into the workgroup's partial-sum block.
+  template <int l>
+  __device__ __forceinline__ void flush() const {
     constexpr int OFF = Gm::tpw_off(l);
     if constexpr (Gm::quad(l)) {
       constexpr int QO = Gm::wob(l) / 2;
@@ -702,18 +868,34 @@ struct BwdWave {
         if (t < Gm::tiles(l)) flush_tile<l>(wacc[OFF + k], t / WOB, t % WOB);
       }
     }
-    if constexpr (l + 1 < L) flush<l + 1>();
   }
 };
 
+#ifdef MLPMK_BWD_TIMELINE
+// Measurement build only (make timeline -> libmlpmk_timeline.so): every wave
+// records, in 100 MHz ticks (s_memrealtime), when it started, when the weight
+// staging barrier released it, when its first round ended, when its last
+// round ended (the weight-gradient flush is issued within that round) and
+// when it left the kernel, then its
+// shader-clock cycles over the whole span (s_memtime), XCD and CU ids and its
+// round count.  mlpmk_bwd_timeline copies the records out.
+constexpr int kBwdTimelineWaves = 4096;
+__device__ unsigned long long g_bwd_timeline[kBwdTimelineWaves * 8];
+#endif
+
 template <class N, int NW, bool DX, bool SEG>
 __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
+#ifdef MLPMK_BWD_TIMELINE
+  const unsigned long long tl_t0 = __builtin_amdgcn_s_memrealtime(), tl_c0 = __builtin_amdgcn_s_memtime();
+  unsigned long long tl_t1 = 0, tl_t2 = 0, tl_t3 = 0;
+  unsigned int tl_nr = 0;
+#endif
   using Gm = BwdGeom<N, NW, DX, SEG>;
   static_assert(Gm::valid(), "unsupported backward shape");
   constexpr int R = Gm::R;
   __shared__ f16x8 wfr[Gm::ndfrag() * 64];
   __shared__ f16 ta[Gm::fa() * R];
-  __shared__ f16 tz[Gm::fz() * R];
+  __shared__ f16 tz[Gm::fz() * R * (Gm::dzl() ? 2 : 1)];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   f32x16 wacc[Gm::ntpw()];
@@ -723,25 +905,57 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   wv.init_slots();
 
   // Every wave of a workgroup runs the same rounds (the barriers need all of them).
-  // The first round's rows are requested before the weight staging, so the
-  // two memory round trips overlap.
+  // The weight staging's loads (L2 hits once any workgroup has read W) are
+  // issued first and the first round's rows right after them, so the rows
+  // stream in while the staging completes: the LDS writes of the staging
+  // wait for the weights alone (memory operations are counted in issue
+  // order).
   const int64_t nrounds = (p.M + R - 1) / R;
-  wv.row0 = (int64_t)blockIdx.x * R + wid * 32;
-  wv.load_dout(wv.row0);
-  if constexpr (BwdWave<N, NW, DX, SEG>::PF) {
-    wv.template prefetch_all<N::L - 1>(wv.row0);
-  } else if constexpr (Gm::RC) {
-    wv.template load_h<N::L - 2>(wv.row0);
-  } else if constexpr (N::L >= 2) {
-    wv.template load_h<N::L - 1>(wv.row0);
+  {
+    f16x8 sv[N::L][DgradStage<N, Gm>::template per<NW * 64>()];
+    dgrad_load_all<N, Gm, NW * 64>(p, sv);
+    wv.row0 = (int64_t)blockIdx.x * R + wid * 32;
+    wv.load_dout(wv.row0);
+    if constexpr (BwdWave<N, NW, DX, SEG>::PF) {
+      wv.template prefetch_all<N::L - 1>(wv.row0);
+    } else if constexpr (Gm::RC) {
+      wv.template load_h<N::L - 2>(wv.row0);
+    } else if constexpr (N::L >= 2) {
+      wv.template load_h<N::L - 1>(wv.row0);
+    }
+    dgrad_store_all<N, Gm, NW * 64>(sv, wfr);
   }
-  stage_dgrad_weights<N, Gm, NW * 64>(p, wfr);
   __syncthreads();
+#ifdef MLPMK_BWD_TIMELINE
+  tl_t1 = __builtin_amdgcn_s_memrealtime();
+#endif
   for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
     wv.round();
     wv.row0 += wv.rstep;
+#ifdef MLPMK_BWD_TIMELINE
+    if (tl_nr++ == 0) tl_t2 = __builtin_amdgcn_s_memrealtime();
+#endif
   }
-  wv.template flush<0>();
+#ifdef MLPMK_BWD_TIMELINE
+  tl_t3 = __builtin_amdgcn_s_memrealtime();
+#endif
+  wv.template flush_all<0>();
+#ifdef MLPMK_BWD_TIMELINE
+  const unsigned long long tl_t4 = __builtin_amdgcn_s_memrealtime(), tl_c4 = __builtin_amdgcn_s_memtime();
+  const int tl_w = (int)blockIdx.x * NW + wid;
+  if (lane == 0 && tl_w < kBwdTimelineWaves) {
+    unsigned long long* r = g_bwd_timeline + tl_w * 8;
+    r[0] = tl_t0;
+    r[1] = tl_t1;
+    r[2] = tl_t2;
+    r[3] = tl_t3;
+    r[4] = tl_t4;
+    r[5] = tl_c4 - tl_c0;
+    r[6] = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) |               // XCC_ID
+           ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4) << 8);  // HW_ID
+    r[7] = tl_nr;
+  }
+#endif
 }
 
 // Sums the per-workgroup weight-gradient partials into dw.  A workgroup owns
@@ -790,6 +1004,20 @@ __global__ __launch_bounds__(kCombineCols* kCombineGroups) void bwd_combine_kern
 // ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
+
+#ifdef MLPMK_BWD_TIMELINE
+}  // namespace mlpmk
+// Copies the records of the last backward launch (8 x 64-bit words per wave,
+// kBwdTimelineWaves waves) to dst and clears them.  Measurement build only.
+extern "C" int mlpmk_bwd_timeline(void* dst, int64_t bytes) {
+  if (bytes < (int64_t)sizeof(mlpmk::g_bwd_timeline)) return -1;
+  if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(mlpmk::g_bwd_timeline), sizeof(mlpmk::g_bwd_timeline)) != hipSuccess)
+    return -2;
+  static unsigned long long zeros[mlpmk::kBwdTimelineWaves * 8];
+  return hipMemcpyToSymbol(HIP_SYMBOL(mlpmk::g_bwd_timeline), zeros, sizeof(zeros)) == hipSuccess ? 0 : -3;
+}
+namespace mlpmk {
+#endif
 
 typedef Net<128, 128, 128, 128> BNet3L128;
 typedef Net<128, 128, 128, 128, 128, 128> BNet5L128;
