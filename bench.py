@@ -571,6 +571,9 @@ def main():
                          "sustained run, bf16 figure or copy reference)")
     ap.add_argument("--timeline", action="store_true",
                     help="per-XCD clock and finish times of one launch (needs libmlpmk_timeline.so via MLPMK_LIBRARY)")
+    ap.add_argument("--train-step", type=int, default=None, metavar="M",
+                    help="counter-collection runs of the training kernels: only the 3-layer WN training step at M "
+                         "rows (no headline, no other legs); prints its timing JSON")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -589,6 +592,11 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+
+    if args.train_step:
+        print(json.dumps({"training_step": {str(args.train_step): train_step_bench(
+            torch, args.train_step, steps=args.steps, warmup=args.warmup)}}))
+        return
 
     dims = CONFIG_DIMS[args.config]
     uniform = args.config == "narrow"
