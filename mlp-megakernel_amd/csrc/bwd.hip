@@ -65,7 +65,14 @@ template <class N, int NW, bool DX, bool SEG = false>
 struct BwdGeom {
   static_assert(!SEG || DX, "a segment always hands on the gradient below it");
   static constexpr int L = N::L;
-  static constexpr int R = 32 * NW;  // rows per round
+  // Feature split (FS, 8 waves): wave w takes 32-row block w mod 4 of the
+  // round and feature half w / 4 of everything it loads, packs and produces
+  // (its share of the dgrad: half the output blocks), and 2 of each layer's
+  // 16 dW tiles; half the accumulators per wave let two waves share a SIMD.
+  static constexpr bool FS = NW == 8;
+  static constexpr int RB = FS ? NW / 2 : NW;  // 32-row blocks per round
+  static constexpr int NFH = FS ? 2 : 1;       // feature parts
+  static constexpr int R = 32 * RB;            // rows per round
   static constexpr bool has_dgrad(int l) { return l >= 1 || DX; }
   // dgrad of layer l: 32-feature output blocks over d[l], K-steps over d[l+1].
   static constexpr int dmb(int l) { return N::d[l] / 32; }
@@ -148,6 +155,11 @@ struct BwdGeom {
       if (N::d[i] % 32 != 0) return false;  // hidden widths in whole 32-feature blocks
     if (DX && N::d[0] % 32 != 0) return false;
     if (RC && (L != 3 || N::gen)) return false;  // recompute: 3-layer (segment) kernels of 128-wide networks
+    if (FS) {  // dz through LDS (the partner wave's half), whole 64-feature halves
+      if (!dzl()) return false;
+      for (int i = 0; i <= L; ++i)
+        if (N::d[i] % 64 != 0) return false;
+    }
     return N::valid() && R >= 128 && lds_bytes() <= 163840;
   }
 };
@@ -239,6 +251,8 @@ struct BwdWave {
   static constexpr int KSL = N::d[L] / 16;
   static constexpr int FA = Gm::fa(), FZ = Gm::fz();  // features per exchange-tile row
   static constexpr bool DZL = Gm::dzl();
+  static constexpr int NFH = Gm::NFH;  // feature parts (FS: 2)
+  static constexpr int KSHW = KSH / NFH, KS0W = KS0 / NFH, KSLW = KSL / NFH;  // K-steps this wave holds
 
   const BwdParams& p;
   const f16x8* wfr;  // staged dgrad fragments
@@ -251,6 +265,7 @@ struct BwdWave {
   int rrow[2];     // rows (within a K-step of 16) of this lane's two transposed reads
   int rcol;        // first of the 4 features the lane addresses in a read, less the block base
   f32x16 (&wacc)[Gm::ntpw()];
+  int rb = 0, fh = 0;  // row block of the round and feature part (FS; else rb = wid)
 
   // Prefetched rows (issued one phase ahead of their use).
   static constexpr bool PF = Gm::pf();
@@ -260,14 +275,15 @@ struct BwdWave {
   // dL/dout is.
   static constexpr bool SHX = DZL && PF && KS0 == KSL;
   static constexpr bool EARLY = DZL && PF;  // next-round rows requested before the layer's barrier
-  f16x8 gbuf[KSL];                 // dL/dout of the round = dz_{L-1}
-  float hbuf[PF ? L : 1][KSH][8];  // h_l, fp32: buffer l (PF) or one shared buffer
-  f16x8 xown[SHX ? 1 : KS0];       // x rows (SHX: in gbuf)
-  __device__ __forceinline__ f16x8 (&xbuf())[KS0] {
+  // (Each holds this wave's feature part: K-steps fh * KS..W onwards.)
+  f16x8 gbuf[KSLW];                 // dL/dout of the round = dz_{L-1}
+  float hbuf[PF ? L : 1][KSHW][8];  // h_l, fp32: buffer l (PF) or one shared buffer
+  f16x8 xown[SHX ? 1 : KS0W];       // x rows (SHX: in gbuf)
+  __device__ __forceinline__ f16x8 (&xbuf())[KS0W] {
     if constexpr (SHX)
-      return *reinterpret_cast<f16x8(*)[KS0]>(gbuf);
+      return *reinterpret_cast<f16x8(*)[KS0W]>(gbuf);
     else
-      return *reinterpret_cast<f16x8(*)[KS0]>(xown);
+      return *reinterpret_cast<f16x8(*)[KS0W]>(xown);
   }
 
   // Tile layout: element (r, f) of a tile with F features per row sits at
@@ -281,7 +297,9 @@ struct BwdWave {
   }
 
   __device__ __forceinline__ void init_slots() {
-    wsw = wid * 32 + n;  // the row this lane writes (swizzle taken per tile width)
+    rb = Gm::FS ? wid % Gm::RB : wid;
+    fh = Gm::FS ? wid / Gm::RB : 0;
+    wsw = rb * 32 + n;  // the row this lane writes (swizzle taken per tile width)
     // ds_read_b64_tr_b16, per 16-lane group: result lane i, element j is
     // element (i & 3) of the 8 bytes addressed by lane (i >> 2) + 4j.  Lane
     // 4j + c of group q addresses row 8*(q >> 1) + j (+4 for the second read)
@@ -317,8 +335,8 @@ struct BwdWave {
       // resource ends at the row's OW-th element, and a broadcast row may be
       // exactly OW long), pieces past OW zero.
 #pragma unroll
-      for (int s = 0; s < KSL; ++s) {
-        const int c = 16 * s + 8 * g;
+      for (int s = 0; s < KSLW; ++s) {
+        const int c = 16 * (s + fh * KSLW) + 8 * g;
         if (c + 8 <= OW) {
           gbuf[s] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + c) * 2), 0, 0));
         } else {
@@ -334,9 +352,9 @@ struct BwdWave {
       return;
     }
 #pragma unroll
-    for (int s = 0; s < KSL; ++s)
+    for (int s = 0; s < KSLW; ++s)
       gbuf[s] = __builtin_bit_cast(
-          f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + 16 * s + 8 * g) * 2), 0, 0));
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((n * st + 16 * (s + fh * KSLW) + 8 * g) * 2), 0, 0));
   }
   // a_l = h_l (stash[l-1], or p.h0 for layer 0 of a segment; fp32) rows from
   // r0: 8 consecutive features per K-step.
@@ -345,14 +363,16 @@ struct BwdWave {
     constexpr int B = PF ? l : 0;
     const int HW = dw_(l);  // a multiple of 16 for Gen networks: K-steps past it are zero
     const rsrc_t hr = rows_rsrc(l == 0 ? p.h0 : p.stash[l > 0 ? l - 1 : 0], HW, 4, r0);
+    constexpr int KW = N::d[l] / 16 / NFH;  // K-steps of this wave's feature part
 #pragma unroll
-    for (int s = 0; s < N::d[l] / 16; ++s) {
-      if (N::gen && 16 * s >= HW) {
+    for (int s = 0; s < KW; ++s) {
+      const int sg = s + fh * KW;
+      if (N::gen && 16 * sg >= HW) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) hbuf[B][s][j] = 0.0f;
         continue;
       }
-      const int off = (n * HW + 16 * s + 8 * g) * 4;
+      const int off = (n * HW + 16 * sg + 8 * g) * 4;
       const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0));
       const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, 0));
 #pragma unroll
@@ -366,21 +386,24 @@ struct BwdWave {
     const int D = dw_(0);
     const rsrc_t xr = rows_rsrc(p.x, D, 2, r0);
 #pragma unroll
-    for (int s = 0; s < KS0; ++s)
-      xbuf()[s] = (N::gen && 16 * s >= D)
+    for (int s = 0; s < KS0W; ++s) {
+      const int sg = s + fh * KS0W;
+      xbuf()[s] = (N::gen && 16 * sg >= D)
                     ? f16x8{}
                     : __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    xr, (int)((n * D + 16 * s + 8 * g) * 2), 0, 0));
+                                                    xr, (int)((n * D + 16 * sg + 8 * g) * 2), 0, 0));
+    }
   }
 
-  // Writes the wave's 32 rows of KS K-steps of features (row-per-lane B
-  // operands v[s]: row n, features 16s + 8g + [0..7]) into an exchange tile:
-  // one 16-byte write per K-step, straight from the registers.
+  // Writes the wave's 32 rows of KS K-steps of features from K-step s0 on
+  // (row-per-lane B operands v[s]: row n, features 16(s0 + s) + 8g + [0..7])
+  // into an exchange tile: one 16-byte write per K-step, straight from the
+  // registers.
   template <int F, int KS>
-  __device__ __forceinline__ void xwrite(f16* t, const f16x8 (&v)[KS]) const {
+  __device__ __forceinline__ void xwrite(f16* t, const f16x8 (&v)[KS], int s0 = 0) const {
     const int r = wsw, sw = swz(r, F);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) *reinterpret_cast<f16x8*>(t + r * F + ((16 * s + 8 * g) ^ sw)) = v[s];
+    for (int s = 0; s < KS; ++s) *reinterpret_cast<f16x8*>(t + r * F + ((16 * (s0 + s) + 8 * g) ^ sw)) = v[s];
   }
   // MFMA operand for features fb .. fb+31 (fb % 32 == 0) over rows
   // 16kk .. 16kk+15 of the round: lane (m, g) gets rows 16kk + 8g + [0..7] of
@@ -465,17 +488,19 @@ struct BwdWave {
   // dgrad output block mb of layer l (features 32mb .. 32mb+31 of a_l, this
   // wave's 32 rows): registers 0..7 of the accumulator hold features 32mb +
   // 8g + [0..7] (K-step 2mb of a_l), 8..15 hold 32mb + 16 + 8g + [0..7]
-  // (K-step 2mb + 1).  Through a stash layer (HA) it is multiplied by
+  // (K-step 2mb + 1); h_l's K-steps 2mb, 2mb + 1 sit at 2hj, 2hj + 1 of this
+  // wave's buffer.  Through a stash layer (HA) it is multiplied by
   // sigma(z) = 1 - exp(-h_l) into dz_{l-1} (or, for a segment's layer 0, the
   // dz handed to the launch below through p.dx); otherwise it is dx itself.
   template <int l, bool HA, int B>
-  __device__ __forceinline__ void dgrad_epilogue(int mb, const f32x16& acc, f16x8 (&dzn)[KSM], f16* tout) const {
+  __device__ __forceinline__ void dgrad_epilogue(int mb, int hj, const f32x16& acc, f16x8 (&dzn)[KSM],
+                                                 f16* tout) const {
     if constexpr (HA) {
       float v[16];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        v[j] = acc[j] * sig_from_h(hbuf[B][2 * mb][j]);
-        v[8 + j] = acc[8 + j] * sig_from_h(hbuf[B][2 * mb + 1][j]);
+        v[j] = acc[j] * sig_from_h(hbuf[B][2 * hj][j]);
+        v[8 + j] = acc[8 + j] * sig_from_h(hbuf[B][2 * hj + 1][j]);
       }
       const f16x8 lo = pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
       const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
@@ -528,22 +553,30 @@ struct BwdWave {
       xwrite<FZ>(tin, zs);
     }
     if constexpr (HA) {
-      f16x8 as[KSA];
+      constexpr int KW = KSA / NFH;
+      f16x8 as[KW];
 #pragma unroll
-      for (int s = 0; s < KSA; ++s)
+      for (int s = 0; s < KW; ++s)
         as[s] = pack8<N::bf>(hbuf[B][s][0], hbuf[B][s][1], hbuf[B][s][2], hbuf[B][s][3], hbuf[B][s][4], hbuf[B][s][5],
                       hbuf[B][s][6], hbuf[B][s][7]);
-      xwrite<FA>(ta, as);
+      xwrite<FA>(ta, as, fh * KW);
     } else {
-      xwrite<FA>(ta, xbuf());
+      xwrite<FA>(ta, xbuf(), fh * KS0W);
       if constexpr (SHX)
         load_dout(row0 + rstep);  // x is consumed: the next round's dL/dout takes its buffer
       else if constexpr (EARLY)
         load_x(row0 + rstep);  // x is consumed: the next round's rows
     }
-    if constexpr (Gm::has_dgrad(l)) dgrad<l, HA, B>(dz, dzn, tin, tout);
-    if constexpr (EARLY && HA) load_h<l>(row0 + rstep);  // h_l is consumed (sigma done): the next round's rows
+    // The dgrad reads all of dz_l for the wave's rows.  With the feature
+    // split the partner wave wrote half of them: of the round's dL/dout
+    // tile (l = L-1) just now, so that dgrad waits for the barrier; the
+    // dz_l of lower layers were written before the previous layer's.
+    constexpr bool DG_LATE = Gm::FS && l == L - 1;
+    if constexpr (Gm::has_dgrad(l) && !DG_LATE) dgrad<l, HA, B>(dz, dzn, tin, tout);
+    if constexpr (EARLY && HA && !DG_LATE) load_h<l>(row0 + rstep);  // h_l is consumed (sigma done): the next round's rows
     __syncthreads();  // every wave's rows are in the exchange tiles
+    if constexpr (Gm::has_dgrad(l) && DG_LATE) dgrad<l, HA, B>(dz, dzn, tin, tout);
+    if constexpr (EARLY && HA && DG_LATE) load_h<l>(row0 + rstep);
     if constexpr (EARLY) {
     } else if constexpr (PF) {  // this layer's buffer is free: the next round's rows
       if constexpr (HA)
@@ -581,7 +614,7 @@ struct BwdWave {
   __device__ __forceinline__ void dgrad(const f16x8 (&dz)[KSM], f16x8 (&dzn)[KSM], const f16* tin, f16* tout) {
     constexpr int KSZ = N::d[l + 1] / 16;  // K-steps of dz_l
     constexpr int MB = N::d[l] / 32;
-    constexpr int NF = MB * KSZ;
+    constexpr int NF = MB * KSZ / NFH;  // fragments this wave reads
     constexpr int NQ = NF < 4 ? NF : 4;
     if constexpr (N::gen) {
       const int fbase = (Gm::dfrag_off(l) * 64 + lane) * 16;
@@ -592,47 +625,51 @@ struct BwdWave {
         f32x16 a = {};
 #pragma unroll
         for (int s = 0; s < KSZ; ++s) a = mfma32x32x16<N::bf>(frag[s * 64], dz[s], a);
-        dgrad_epilogue<l, HA, B>(mb, a, dzn, tout);
+        dgrad_epilogue<l, HA, B>(mb, mb, a, dzn, tout);
       }
       return;
     }
     f16x8 zb[KSZ];
     const int zr = wsw, zsw = swz(zr, FZ);
     auto zread = [&](int s) { return *reinterpret_cast<const f16x8*>(tin + zr * FZ + ((16 * s + 8 * g) ^ zsw)); };
-    if constexpr (DZL) {  // rows this wave wrote itself: no barrier needed
+    if constexpr (DZL) {  // rows this wave (and with FS its partner, before a barrier) wrote
     } else {
 #pragma unroll
       for (int s = 0; s < KSZ; ++s) zb[s] = dz[s];
     }
-    const char* wb = reinterpret_cast<const char*>(wfr) + opaque((Gm::dfrag_off(l) * 64 + lane) * 16);
+    // This wave's output blocks: MBW of them from block mb0 (FS: its half).
+    constexpr int MBW = MB / NFH, NFW = MBW * KSZ;
+    const int mb0 = fh * MBW;
+    const char* wb =
+        reinterpret_cast<const char*>(wfr) + opaque((Gm::dfrag_off(l) * 64 + lane) * 16 + mb0 * KSZ * 1024);
     f16x8 fq[NQ];
 #pragma unroll
     for (int t = 0; t < NQ; ++t) fq[t] = *reinterpret_cast<const f16x8*>(wb + t * 1024);
     f32x16 acc[2];
 #pragma unroll
-    for (int mb = 0; mb <= MB; ++mb) {
-      if (mb < MB) {
+    for (int j = 0; j <= MBW; ++j) {
+      if (j < MBW) {
         f32x16 a = {};
 #pragma unroll
         for (int s = 0; s < KSZ; ++s) {
-          const int t = mb * KSZ + s;
+          const int t = j * KSZ + s;
           a = mfma32x32x16<N::bf>(fq[t % NQ], DZL ? zread(s) : zb[s], a);
-          if (t + NQ < NF) fq[t % NQ] = *reinterpret_cast<const f16x8*>(wb + (t + NQ) * 1024);
+          if (t + NQ < NFW) fq[t % NQ] = *reinterpret_cast<const f16x8*>(wb + (t + NQ) * 1024);
         }
         if constexpr (DZL)
-          dgrad_epilogue<l, HA, B>(mb, a, dzn, tout);
+          dgrad_epilogue<l, HA, B>(mb0 + j, j, a, dzn, tout);
         else
-          acc[mb & 1] = a;
+          acc[j & 1] = a;
       }
-      if (!DZL && mb > 0) dgrad_epilogue<l, HA, B>(mb - 1, acc[(mb - 1) & 1], dzn, tout);
-      if (mb < MB) {
+      if (!DZL && j > 0) dgrad_epilogue<l, HA, B>(mb0 + j - 1, j - 1, acc[(j - 1) & 1], dzn, tout);
+      if (j < MBW) {
         // Per MFMA: the MFMA, the read it frees a ring slot for, a share of
         // the previous block's epilogue.
 #pragma unroll
         for (int s = 0; s < KSZ; ++s) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (mb * KSZ + s + NQ < NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          if (!DZL && mb > 0) __builtin_amdgcn_sched_group_barrier(0x002, 160 / KSZ, 0);
+          if (j * KSZ + s + NQ < NFW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (!DZL && j > 0) __builtin_amdgcn_sched_group_barrier(0x002, 160 / KSZ, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -785,7 +822,7 @@ struct BwdWave {
     if constexpr (Gm::RC) recompute();
     f16x8 dz[KSM], dzn[KSM];
     if constexpr (DZL) {
-      xwrite<FZ>(tz, gbuf);  // dz_{L-1} = dL/dout into tile 0
+      xwrite<FZ>(tz, gbuf, fh * KSLW);  // dz_{L-1} = dL/dout into tile 0
     } else {
 #pragma unroll
       for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
@@ -914,7 +951,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
   {
     f16x8 sv[N::L][DgradStage<N, Gm>::template per<NW * 64>()];
     dgrad_load_all<N, Gm, NW * 64>(p, sv);
-    wv.row0 = (int64_t)blockIdx.x * R + wid * 32;
+    wv.row0 = (int64_t)blockIdx.x * R + wv.rb * 32;
     wv.load_dout(wv.row0);
     if constexpr (BwdWave<N, NW, DX, SEG>::PF) {
       wv.template prefetch_all<N::L - 1>(wv.row0);
@@ -1032,7 +1069,7 @@ static bool bdims_match(int L, const int* dims) {
   return true;
 }
 
-// Grid of the persistent backward: one workgroup per round of 32*NW rows, at
+// Grid of the persistent backward: one workgroup per round of R rows, at
 // most CUs x occupancy.
 template <class N, int NW, bool DX, bool SEG>
 static int bwd_grid(int64_t M, int* grid) {
@@ -1051,7 +1088,8 @@ static int bwd_grid(int64_t M, int* grid) {
     if (rc != MLPMK_OK) return rc;
     if (dev >= 0 && dev < kMaxDev) occ_cache[dev] = occ;
   }
-  const int64_t nrounds = (M + 32 * NW - 1) / (32 * NW);
+  constexpr int R = BwdGeom<N, NW, DX, SEG>::R;
+  const int64_t nrounds = (M + R - 1) / R;
   const int64_t cap = (int64_t)cus * occ;
   *grid = (int)(nrounds < cap ? nrounds : cap);
   return MLPMK_OK;
@@ -1093,9 +1131,16 @@ static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
   return MLPMK_OK;
 }
 
-template <class N, int NW>
+// Waves per workgroup of the backward for N: the 8-wave feature split where
+// its geometry is valid (dz through LDS, whole 64-feature halves), else 4.
+template <class N, bool DX>
+constexpr int bwd_waves() {
+  return BwdGeom<N, 8, DX, false>::valid() ? 8 : 4;
+}
+
+template <class N>
 static int launch_bwd_any(const BwdParams& p, hipStream_t st) {
-  return p.dx ? launch_bwd<N, NW, true>(p, st) : launch_bwd<N, NW, false>(p, st);
+  return p.dx ? launch_bwd<N, bwd_waves<N, true>(), true>(p, st) : launch_bwd<N, bwd_waves<N, false>(), false>(p, st);
 }
 
 static int64_t weight_elems_of(int L, const int* dims) {
@@ -1114,9 +1159,10 @@ static int partial_bytes(int64_t M, int64_t welems, int64_t* bytes) {
   return rc;
 }
 
-template <class N, int NW>
+template <class N>
 static int bwd_workspace_any(int64_t M, bool dx, int64_t welems, int64_t* bytes) {
-  return dx ? partial_bytes<N, NW, true>(M, welems, bytes) : partial_bytes<N, NW, false>(M, welems, bytes);
+  return dx ? partial_bytes<N, bwd_waves<N, true>(), true>(M, welems, bytes)
+            : partial_bytes<N, bwd_waves<N, false>(), false>(M, welems, bytes);
 }
 
 // Deeper networks in two launches: layers L-1..2 as a segment (kernel A, the
@@ -1135,7 +1181,7 @@ static int bwd_split_workspace(int L, const int* dims, int64_t M, bool dx, int64
   int rc = partial_bytes<TOP, 4, true, true>(M, weight_elems_of(L - 2, dims + 2), &a);
   if (rc != MLPMK_OK) return rc;
   const int64_t wb = weight_elems_of(2, dims);
-  rc = dx ? partial_bytes<BOT, 4, true>(M, wb, &b) : partial_bytes<BOT, 4, false>(M, wb, &b);
+  rc = bwd_workspace_any<BOT>(M, dx, wb, &b);
   if (rc != MLPMK_OK) return rc;
   *bytes = dz_bytes(M) + (a > b ? a : b);
   return MLPMK_OK;
@@ -1179,7 +1225,7 @@ static int launch_bwd_split(const BwdParams& p, int L, hipStream_t st) {
   b.dx = p.dx;
   b.M = p.M;
   b.part = part;
-  return launch_bwd_any<BOT, 4>(b, st);
+  return launch_bwd_any<BOT>(b, st);
 }
 
 // Runtime-width networks (compiled at width 128, true widths in BwdParams::dims):
@@ -1214,10 +1260,10 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
   // (the last stash entry NULL, decided per call), whose kernel has its own
   // grid: size for the larger of the two.
   if (bdims_match<BNet3L128>(L, dims)) {
-    int rc = bwd_workspace_any<N3, 4>(M, dx, we, bytes);
+    int rc = bwd_workspace_any<N3>(M, dx, we, bytes);
     if (rc != MLPMK_OK) return rc;
     int64_t rcb = 0;
-    rc = dx ? partial_bytes<Recompute<N3>, 4, true>(M, we, &rcb) : partial_bytes<Recompute<N3>, 4, false>(M, we, &rcb);
+    rc = bwd_workspace_any<Recompute<N3>>(M, dx, we, &rcb);
     if (rc == MLPMK_OK && rcb > *bytes) *bytes = rcb;
     return rc;
   }
@@ -1229,11 +1275,11 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
     if (rc == MLPMK_OK && rcb > *bytes) *bytes = rcb;
     return rc;
   }
-  if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<NN, 4>(M, dx, we, bytes);
+  if (bdims_match<BNetNarrow>(L, dims)) return bwd_workspace_any<NN>(M, dx, we, bytes);
   if (bwd_generic_dims(L, dims)) {
     switch (L) {
-      case 2: return bwd_workspace_any<G2, 4>(M, dx, we, bytes);
-      case 3: return bwd_workspace_any<G3, 4>(M, dx, we, bytes);
+      case 2: return bwd_workspace_any<G2>(M, dx, we, bytes);
+      case 3: return bwd_workspace_any<G3>(M, dx, we, bytes);
       case 4: return bwd_split_workspace<G2, G2>(L, dims, M, dx, bytes);
       default: return bwd_split_workspace<G3, G2>(L, dims, M, dx, bytes);
     }
@@ -1299,15 +1345,17 @@ static int bwd_dispatch_t(int L, const int* dims, const BwdParams& p, hipStream_
   typedef typename ElemNet<B, BNetNarrow>::type NN;
   typedef typename ElemNet<B, GBNet2>::type G2;
   typedef typename ElemNet<B, GBNet3>::type G3;
-  if (bdims_match<BNet3L128>(L, dims) && !p.stash[1]) return launch_bwd_any<Recompute<N3>, 4>(p, st);
-  if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<N3, 4>(p, st);
+  if (bdims_match<BNet3L128>(L, dims) && !p.stash[1]) return launch_bwd_any<Recompute<N3>>(p, st);
+  // Without dx the 8-wave feature split (two waves per SIMD); with dx the
+  // third layer's dgrad fragments leave no LDS for the second dz tile.
+  if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<N3>(p, st);
   if (bdims_match<BNet5L128>(L, dims) && !p.stash[3]) return launch_bwd_split<Recompute<N3>, N2>(p, L, st);
   if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<N3, N2>(p, L, st);
-  if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<NN, 4>(p, st);
+  if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<NN>(p, st);
   if (bwd_generic_dims(L, dims)) {
     switch (L) {
-      case 2: return launch_bwd_any<G2, 4>(p, st);
-      case 3: return launch_bwd_any<G3, 4>(p, st);
+      case 2: return launch_bwd_any<G2>(p, st);
+      case 3: return launch_bwd_any<G3>(p, st);
       case 4: return launch_bwd_split<G2, G2>(p, L, st);
       default: return launch_bwd_split<G3, G2>(p, L, st);
     }
