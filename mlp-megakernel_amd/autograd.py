@@ -34,11 +34,13 @@ import torch
 from . import ops
 
 # Activation recomputation policy: "auto" recomputes h_{L-1} from
-# RECOMPUTE_MIN_ROWS rows on, where the training step is as fast or faster
-# with it (3-layer 128-wide network on MI355X, forward + backward replayed as
-# one HIP graph: 101.9 -> 101.8 us at 131072 rows, 377 -> 339 us at 524288,
-# 713 -> 633 us at 1048576; 46.1 -> 48.0 us at 16384) and the stash is half
-# the size; "always" / "never" force the choice where the shape allows it.
+# RECOMPUTE_MIN_ROWS rows on where that makes the training step faster (MI355X,
+# the weight-norm module's step replayed as one HIP graph): the 5-layer
+# network (0.267 -> 0.259 ms at 131072 rows, 1.557 -> 1.454 ms at 1048576) and
+# steps that also need dx; the 3-layer step without dx keeps the stash, whose
+# 8-wave backward is the faster one (0.149 ms stashing vs 0.162 ms
+# recomputing at 131072 rows, 0.833 vs 0.840 ms at 1048576).  "always" /
+# "never" force the choice where the shape allows it.
 RECOMPUTE = "auto"
 RECOMPUTE_MIN_ROWS = 1 << 17
 
@@ -80,7 +82,6 @@ def _run_bwd(x, weights, hs, dout, dws, dx):
 
 
 def _use_recompute(dims, m, need_dx):
-    del need_dx  # the recomputing backward also writes dx
     if RECOMPUTE == "never" or _backward_impl() == "fallback" or not _fused_bwd_supported(tuple(dims)):
         return False
     if RECOMPUTE not in ("auto", "always"):
@@ -88,7 +89,10 @@ def _use_recompute(dims, m, need_dx):
     ok = _rc_shapes.get(dims)
     if ok is None:
         ok = _rc_shapes[dims] = ops.bwd_recompute_supported(list(dims))
-    return ok and (RECOMPUTE == "always" or m >= RECOMPUTE_MIN_ROWS)
+    if RECOMPUTE == "always":
+        return ok
+    # (the recomputing backward also writes dx)
+    return ok and m >= RECOMPUTE_MIN_ROWS and (len(dims) != 4 or need_dx)
 
 
 def kernel_dtype(x):
