@@ -132,7 +132,7 @@ struct BwdGeom {
   // rows) from the exchange tile and writes dz_{l-1} into a second one, so no
   // dz is held in registers across phases.  The 64 registers that frees
   // carry the per-layer prefetch below for 3-layer networks.
-  static constexpr bool dzl() { return !N::gen && !SEG && !RC && L <= 3 && lds_bytes_with(2) <= 163840; }
+  static constexpr bool dzl() { return !N::gen && !RC && L <= 3 && lds_bytes_with(2) <= 163840; }
   static constexpr int lds_bytes() { return lds_bytes_with(dzl() ? 2 : 1); }
   // Per-layer prefetch: every stash layer (and x) gets its own register
   // buffer, reloaded for the next round right after its last use, so HBM
@@ -141,7 +141,7 @@ struct BwdGeom {
   // two-layer kernel (lower half of the 5-layer backward) 37.5 -> 34.4 us.
   // Without dz through LDS the 3-layer 128-wide kernel spills with it, so
   // such kernels share one buffer loaded one phase ahead.
-  static constexpr bool pf() { return !N::gen && !SEG && (L <= 2 || dzl()); }
+  static constexpr bool pf() { return !N::gen && (SEG ? dzl() : (L <= 2 || dzl())); }
   // Element offset of dW_l in the dW blocks laid out back to back.
   static constexpr int woff(int l) {
     int o = 0;
@@ -154,7 +154,8 @@ struct BwdGeom {
     for (int i = 1; i < L; ++i)
       if (N::d[i] % 32 != 0) return false;  // hidden widths in whole 32-feature blocks
     if (DX && N::d[0] % 32 != 0) return false;
-    if (RC && (L != 3 || N::gen)) return false;  // recompute: 3-layer (segment) kernels of 128-wide networks
+    // recompute: 3-layer kernels and 2-layer segments of 128-wide networks
+    if (RC && (N::gen || !(L == 3 || (L == 2 && SEG)))) return false;
     if (FS) {  // dz through LDS (the partner wave's half), whole 64-feature halves
       if (!dzl()) return false;
       for (int i = 0; i <= L; ++i)
@@ -273,7 +274,7 @@ struct BwdWave {
   // its tile at the start of a round, then the round's x rows are loaded
   // into the buffer, and once they are in the a_0 tile the next round's
   // dL/dout is.
-  static constexpr bool SHX = DZL && PF && KS0 == KSL;
+  static constexpr bool SHX = DZL && PF && !SEG && KS0 == KSL;
   static constexpr bool EARLY = DZL && PF;  // next-round rows requested before the layer's barrier
   // (Each holds this wave's feature part: K-steps fh * KS..W onwards.)
   f16x8 gbuf[KSLW];                 // dL/dout of the round = dz_{L-1}
@@ -1133,9 +1134,9 @@ static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
 
 // Waves per workgroup of the backward for N: the 8-wave feature split where
 // its geometry is valid (dz through LDS, whole 64-feature halves), else 4.
-template <class N, bool DX>
+template <class N, bool DX, bool SEG = false>
 constexpr int bwd_waves() {
-  return BwdGeom<N, 8, DX, false>::valid() ? 8 : 4;
+  return BwdGeom<N, 8, DX, SEG>::valid() ? 8 : 4;
 }
 
 template <class N>
@@ -1165,22 +1166,25 @@ static int bwd_workspace_any(int64_t M, bool dx, int64_t welems, int64_t* bytes)
             : partial_bytes<N, bwd_waves<N, false>(), false>(M, welems, bytes);
 }
 
-// Deeper networks in two launches: layers L-1..2 as a segment (kernel A, the
-// dgrad fragments of those layers + 64 KiB of exchange tiles), whose fp16 dz_1
-// goes through the workspace to layers 1..0 (kernel B, the 2-layer network
-// with dz_1 as its output gradient).  For the 5-layer 128-wide network the
-// four dgrad weight blocks and the exchange tiles would not fit the 160 KiB of
-// one workgroup together.  Workspace: dz_1 [M, d[2]] fp16, then the
-// weight-gradient partials of whichever launch needs more (the launches run in
-// stream order, so they share the block).
+// Deeper networks in two launches: layers L-1..S as a segment (kernel A, the
+// top L - S layers), whose fp16 dz_{S-1} goes through the workspace to
+// layers S-1..0 (kernel B, the S-layer network with dz_{S-1} as its output
+// gradient); S = BOT::L.  The 5-layer 128-wide network splits at S = 3: a
+// 2-layer segment and the 3-layer network, both on the 8-wave kernel (four
+// dgrad weight blocks and the exchange tiles would not fit the 160 KiB of
+// one workgroup together).  Runtime-width networks split at S = 2.
+// Workspace: dz_{S-1} [M, d[S] <= 128] fp16, then the weight-gradient
+// partials of whichever launch needs more (the launches run in stream
+// order, so they share the block).
 static int64_t dz_bytes(int64_t M) { return (M * 128 * 2 + 255) / 256 * 256; }
 
 template <class TOP, class BOT>
 static int bwd_split_workspace(int L, const int* dims, int64_t M, bool dx, int64_t* bytes) {
+  constexpr int S = BOT::L;
   int64_t a = 0, b = 0;
-  int rc = partial_bytes<TOP, 4, true, true>(M, weight_elems_of(L - 2, dims + 2), &a);
+  int rc = partial_bytes<TOP, bwd_waves<TOP, true, true>(), true, true>(M, weight_elems_of(L - S, dims + S), &a);
   if (rc != MLPMK_OK) return rc;
-  const int64_t wb = weight_elems_of(2, dims);
+  const int64_t wb = weight_elems_of(S, dims);
   rc = bwd_workspace_any<BOT>(M, dx, wb, &b);
   if (rc != MLPMK_OK) return rc;
   *bytes = dz_bytes(M) + (a > b ? a : b);
@@ -1189,39 +1193,41 @@ static int bwd_split_workspace(int L, const int* dims, int64_t M, bool dx, int64
 
 template <class TOP, class BOT>
 static int launch_bwd_split(const BwdParams& p, int L, hipStream_t st) {
-  static_assert(TOP::L >= 2 && BOT::L == 2, "segment shapes");
+  constexpr int S = BOT::L;
+  static_assert(TOP::L >= 2 && S >= 2, "segment shapes");
+  if (L != TOP::L + S) return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "split backward: %d layers", L);
   if (!p.part)
     return fail(MLPMK_ERR_INVALID_ARG,
                 "a backward of more than 3 layers passes dz between two launches through the workspace: "
                 "use mlpmk_bwd_ws");
   char* const ws = reinterpret_cast<char*>(p.part);
-  _Float16* const dz1 = reinterpret_cast<_Float16*>(ws);
+  _Float16* const dzs = reinterpret_cast<_Float16*>(ws);
   float* const part = reinterpret_cast<float*>(ws + dz_bytes(p.M));
   BwdParams a = {};
-  for (int l = 0; l < L - 2; ++l) {
-    a.w[l] = p.w[2 + l];
-    a.dw[l] = p.dw[2 + l];
+  for (int l = 0; l < L - S; ++l) {
+    a.w[l] = p.w[S + l];
+    a.dw[l] = p.dw[S + l];
   }
-  for (int l = 0; l + 1 < L - 2; ++l) a.stash[l] = p.stash[2 + l];  // h_3 .. h_{L-1}
-  for (int l = 0; l <= L - 2; ++l) a.dims[l] = p.dims[2 + l];
-  a.h0 = p.stash[1];  // h_2
+  for (int l = 0; l + 1 < L - S; ++l) a.stash[l] = p.stash[S + l];  // h_{S+1} .. h_{L-1}
+  for (int l = 0; l <= L - S; ++l) a.dims[l] = p.dims[S + l];
+  a.h0 = p.stash[S - 1];  // h_S
   a.dout = p.dout;
   a.dout_stride = p.dout_stride;
-  a.dx = dz1;
+  a.dx = dzs;
   a.M = p.M;
   a.part = part;
-  int rc = launch_bwd<TOP, 4, true, true>(a, st);
+  int rc = launch_bwd<TOP, bwd_waves<TOP, true, true>(), true, true>(a, st);
   if (rc != MLPMK_OK) return rc;
   BwdParams b = {};
   b.x = p.x;
-  for (int l = 0; l < 2; ++l) {
+  for (int l = 0; l < S; ++l) {
     b.w[l] = p.w[l];
     b.dw[l] = p.dw[l];
   }
-  for (int l = 0; l <= 2; ++l) b.dims[l] = p.dims[l];
-  b.stash[0] = p.stash[0];  // h_1
-  b.dout = dz1;
-  b.dout_stride = p.dims[2];
+  for (int l = 0; l <= S; ++l) b.dims[l] = p.dims[l];
+  for (int l = 0; l + 1 < S; ++l) b.stash[l] = p.stash[l];  // h_1 .. h_{S-1}
+  b.dout = dzs;
+  b.dout_stride = p.dims[S];
   b.dx = p.dx;
   b.M = p.M;
   b.part = part;
@@ -1268,10 +1274,10 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
     return rc;
   }
   if (bdims_match<BNet5L128>(L, dims)) {
-    int rc = bwd_split_workspace<N3, N2>(L, dims, M, dx, bytes);
+    int rc = bwd_split_workspace<N2, N3>(L, dims, M, dx, bytes);
     if (rc != MLPMK_OK) return rc;
     int64_t rcb = 0;
-    rc = bwd_split_workspace<Recompute<N3>, N2>(L, dims, M, dx, &rcb);
+    rc = bwd_split_workspace<Recompute<N2>, N3>(L, dims, M, dx, &rcb);
     if (rc == MLPMK_OK && rcb > *bytes) *bytes = rcb;
     return rc;
   }
@@ -1349,8 +1355,8 @@ static int bwd_dispatch_t(int L, const int* dims, const BwdParams& p, hipStream_
   // Without dx the 8-wave feature split (two waves per SIMD); with dx the
   // third layer's dgrad fragments leave no LDS for the second dz tile.
   if (bdims_match<BNet3L128>(L, dims)) return launch_bwd_any<N3>(p, st);
-  if (bdims_match<BNet5L128>(L, dims) && !p.stash[3]) return launch_bwd_split<Recompute<N3>, N2>(p, L, st);
-  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<N3, N2>(p, L, st);
+  if (bdims_match<BNet5L128>(L, dims) && !p.stash[3]) return launch_bwd_split<Recompute<N2>, N3>(p, L, st);
+  if (bdims_match<BNet5L128>(L, dims)) return launch_bwd_split<N2, N3>(p, L, st);
   if (bdims_match<BNetNarrow>(L, dims)) return launch_bwd_any<NN>(p, st);
   if (bwd_generic_dims(L, dims)) {
     switch (L) {
