@@ -182,10 +182,11 @@ int mlpmk_bwd(int num_layers, const int* dims, int dtype, const void* x, const v
  * (256 workgroups x 49152 dW elements).  Grids below 64 workgroups (small M)
  * keep the atomic flush, which is then cheaper, and leave the partial-sum
  * part of the workspace untouched.
- * Networks of 4 and 5 layers run as two launches: layers L-1..2 (for the
- * 5-layer 128-wide network their dgrad weights and exchange tiles fill one
- * workgroup's 160 KiB of LDS), whose fp16 gradient of h_1 goes through the
- * first M * 256 bytes of the workspace (rounded up to 256) to layers 1..0.  Numerically the same as one
+ * Networks of 4 and 5 layers run as two launches (all their dgrad weights
+ * and exchange tiles do not fit one workgroup's 160 KiB of LDS): layers
+ * L-1..S, whose fp16 gradient of h_S goes through the first M * 256 bytes
+ * of the workspace (rounded up to 256) to layers S-1..0; S = 3 for the
+ * 5-layer 128-wide network, 2 otherwise.  Numerically the same as one
  * launch: the in-register chain also hands dz on as fp16.
  *   workspace        device memory, 16-byte aligned, at least the size that
  *                    mlpmk_bwd_workspace_size reports for the same

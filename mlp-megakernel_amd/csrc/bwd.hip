@@ -45,7 +45,7 @@
 // the layer below (p.h0) instead of x, and its data gradient leaves through
 // p.dx already multiplied by 1 - exp(-h) -- exactly the fp16 dz operand the
 // in-register chain would have handed to the next layer.  The 5-layer
-// backward is two launches this way (layers 4..2, then 1..0), because its
+// backward is two launches this way (layers 4..3, then 2..0), because its
 // four dgrad weight blocks and the exchange tiles do not fit the 160 KiB LDS
 // of one workgroup together.
 //
@@ -1059,7 +1059,7 @@ namespace mlpmk {
 
 typedef Net<128, 128, 128, 128> BNet3L128;
 typedef Net<128, 128, 128, 128, 128, 128> BNet5L128;
-typedef Net<128, 128, 128> BNet2L128;  // layers 1..0 of the 5-layer network
+typedef Net<128, 128, 128> BNet2L128;  // layers 4..3 of the 5-layer network
 typedef Net<32, 64, 64, 16> BNetNarrow;
 
 template <class N>
@@ -1338,7 +1338,7 @@ bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims
 // The 3- and 5-layer 128-wide networks also run in recompute mode: with a
 // NULL stash entry for h_{L-1} (the forward then does not write it) the
 // backward recomputes it from h_{L-2} at the start of every round (for 5
-// layers in the launch of layers 4..2), with or without dx.  The workspace
+// layers in the launch of layers 4..3), with or without dx.  The workspace
 // size covers both kernels' grids (bwd_workspace_t).
 bool bwd_recompute_supported(int L, const int* dims) {
   return bdims_match<BNet3L128>(L, dims) || bdims_match<BNet5L128>(L, dims);
