@@ -134,13 +134,20 @@ struct BwdGeom {
   // carry the per-layer prefetch below for 3-layer networks.
   static constexpr bool dzl() { return !N::gen && !RC && L <= 3 && lds_bytes_with(2) <= 163840; }
   static constexpr int lds_bytes() { return lds_bytes_with(dzl() ? 2 : 1); }
+  // The feature split with one dz tile (its dgrad fragments leave no room
+  // for a second): dz_l goes into the tile at the start of the layer, the
+  // dgrad reads it back (all of it, the partner's half too) after the
+  // layer's barrier, and its output stays in registers until the next layer.
+  static constexpr bool dzr() { return FS && !dzl() && !N::gen && !RC && L <= 3 && lds_bytes_with(1) <= 163840; }
   // Per-layer prefetch: every stash layer (and x) gets its own register
   // buffer, reloaded for the next round right after its last use, so HBM
   // always has this wave's next rows in flight instead of one phase's rows
   // at a time between compute bursts.  Measured at M = 131072: the
   // two-layer kernel (lower half of the 5-layer backward) 37.5 -> 34.4 us.
   // Without dz through LDS the 3-layer 128-wide kernel spills with it, so
-  // such kernels share one buffer loaded one phase ahead.
+  // such kernels (the 4-wave ones and the single-tile feature split, 3-layer
+  // with dx: 88.5 us with the prefetch, which spills, 77.9 us without, at
+  // M = 131072) share one buffer loaded one phase ahead.
   static constexpr bool pf() { return !N::gen && (SEG ? dzl() : (L <= 2 || dzl())); }
   // Element offset of dW_l in the dW blocks laid out back to back.
   static constexpr int woff(int l) {
@@ -157,7 +164,7 @@ struct BwdGeom {
     // recompute: 3-layer kernels and 2-layer segments of 128-wide networks
     if (RC && (N::gen || !(L == 3 || (L == 2 && SEG)))) return false;
     if (FS) {  // dz through LDS (the partner wave's half), whole 64-feature halves
-      if (!dzl()) return false;
+      if (!dzl() && !dzr()) return false;
       for (int i = 0; i <= L; ++i)
         if (N::d[i] % 64 != 0) return false;
     }
@@ -510,8 +517,8 @@ struct BwdWave {
         *reinterpret_cast<f16x8*>(tout + r * FZ + ((32 * mb + 8 * g) ^ sw)) = lo;
         *reinterpret_cast<f16x8*>(tout + r * FZ + ((32 * mb + 16 + 8 * g) ^ sw)) = hi;
       } else if constexpr (l >= 1) {
-        dzn[2 * mb] = lo;
-        dzn[2 * mb + 1] = hi;
+        dzn[2 * hj] = lo;
+        dzn[2 * hj + 1] = hi;
       } else {  // segment: dz of the layer below leaves through p.dx
         const int D = dw_(0);
         const rsrc_t dr = rows_rsrc(p.dx, D, 2, row0);
@@ -547,11 +554,12 @@ struct BwdWave {
     // into the other tile (the layers alternate, starting from tile 0).
     f16* const tin = tz + (DZL ? ((L - 1 - l) & 1) * FZ * R : 0);
     f16* const tout = tz + (DZL ? ((L - l) & 1) * FZ * R : 0);
-    if constexpr (!DZL) {
-      f16x8 zs[KSZ];
+    if constexpr (!DZL) {  // (the wave's feature part of dz_l)
+      constexpr int KW = KSZ / NFH;
+      f16x8 zs[KW];
 #pragma unroll
-      for (int s = 0; s < KSZ; ++s) zs[s] = dz[s];
-      xwrite<FZ>(tin, zs);
+      for (int s = 0; s < KW; ++s) zs[s] = dz[s];
+      xwrite<FZ>(tin, zs, fh * KW);
     }
     if constexpr (HA) {
       constexpr int KW = KSA / NFH;
@@ -572,7 +580,7 @@ struct BwdWave {
     // split the partner wave wrote half of them: of the round's dL/dout
     // tile (l = L-1) just now, so that dgrad waits for the barrier; the
     // dz_l of lower layers were written before the previous layer's.
-    constexpr bool DG_LATE = Gm::FS && l == L - 1;
+    constexpr bool DG_LATE = Gm::FS && (l == L - 1 || !DZL);
     if constexpr (Gm::has_dgrad(l) && !DG_LATE) dgrad<l, HA, B>(dz, dzn, tin, tout);
     if constexpr (EARLY && HA && !DG_LATE) load_h<l>(row0 + rstep);  // h_l is consumed (sigma done): the next round's rows
     __syncthreads();  // every wave's rows are in the exchange tiles
@@ -633,7 +641,7 @@ struct BwdWave {
     f16x8 zb[KSZ];
     const int zr = wsw, zsw = swz(zr, FZ);
     auto zread = [&](int s) { return *reinterpret_cast<const f16x8*>(tin + zr * FZ + ((16 * s + 8 * g) ^ zsw)); };
-    if constexpr (DZL) {  // rows this wave (and with FS its partner, before a barrier) wrote
+    if constexpr (DZL || Gm::FS) {  // rows this wave (and with FS its partner, before a barrier) wrote
     } else {
 #pragma unroll
       for (int s = 0; s < KSZ; ++s) zb[s] = dz[s];
@@ -654,15 +662,15 @@ struct BwdWave {
 #pragma unroll
         for (int s = 0; s < KSZ; ++s) {
           const int t = j * KSZ + s;
-          a = mfma32x32x16<N::bf>(fq[t % NQ], DZL ? zread(s) : zb[s], a);
+          a = mfma32x32x16<N::bf>(fq[t % NQ], (DZL || Gm::FS) ? zread(s) : zb[s], a);
           if (t + NQ < NFW) fq[t % NQ] = *reinterpret_cast<const f16x8*>(wb + (t + NQ) * 1024);
         }
-        if constexpr (DZL)
+        if constexpr (DZL || Gm::FS)
           dgrad_epilogue<l, HA, B>(mb0 + j, j, a, dzn, tout);
         else
           acc[j & 1] = a;
       }
-      if (!DZL && j > 0) dgrad_epilogue<l, HA, B>(mb0 + j - 1, j - 1, acc[(j - 1) & 1], dzn, tout);
+      if (!(DZL || Gm::FS) && j > 0) dgrad_epilogue<l, HA, B>(mb0 + j - 1, j - 1, acc[(j - 1) & 1], dzn, tout);
       if (j < MBW) {
         // Per MFMA: the MFMA, the read it frees a ring slot for, a share of
         // the previous block's epilogue.
@@ -670,7 +678,7 @@ struct BwdWave {
         for (int s = 0; s < KSZ; ++s) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           if (j * KSZ + s + NQ < NFW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          if (!DZL && j > 0) __builtin_amdgcn_sched_group_barrier(0x002, 160 / KSZ, 0);
+          if (!(DZL || Gm::FS) && j > 0) __builtin_amdgcn_sched_group_barrier(0x002, 160 / KSZ, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -826,7 +834,7 @@ struct BwdWave {
       xwrite<FZ>(tz, gbuf, fh * KSLW);  // dz_{L-1} = dL/dout into tile 0
     } else {
 #pragma unroll
-      for (int s = 0; s < KSL; ++s) dz[s] = gbuf[s];
+      for (int s = 0; s < KSLW; ++s) dz[s] = gbuf[s];
     }
     if constexpr (SHX)
       load_x(row0);  // this round's x into the buffer dL/dout left
