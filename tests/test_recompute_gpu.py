@@ -203,10 +203,9 @@ def test_five_layer_recompute_backward_matches_oracle_and_stash(m, dout_mode):
 @pytest.mark.parametrize("wn", [False, True])
 def test_modules_recompute_policy(wn):
     # The drop-in modules take the recomputing backward under RECOMPUTE =
-    # "always" (and under "auto" for 5 layers from RECOMPUTE_MIN_ROWS_5L rows
-    # and for 3-layer steps that need dx from RECOMPUTE_MIN_ROWS; the 3-layer
-    # step without dx keeps the stash); the gradients agree with the
-    # stashing path.
+    # "always" (and under "auto" from RECOMPUTE_MIN_ROWS rows for 5 layers
+    # and for 3-layer steps that need dx; the 3-layer step without dx keeps
+    # the stash); the gradients agree with the stashing path.
     import fused_mlp
     from mlpmk import autograd as mag
 
