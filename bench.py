@@ -469,7 +469,7 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
         "graph_rows_per_s": m / (gms * 1e-3),
         "graph_roofline_frac": round(nbytes * m / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd" if n_layers == 3 else
-                    "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..2, then 1..0) + wn_bwd",
+                    "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..3, then 2..0) + wn_bwd",
         "x_buffers": nx,
         "recompute_h_last": rc,
         "dtype": str(dtype).replace("torch.", ""),
@@ -572,8 +572,8 @@ def main():
     ap.add_argument("--timeline", action="store_true",
                     help="per-XCD clock and finish times of one launch (needs libmlpmk_timeline.so via MLPMK_LIBRARY)")
     ap.add_argument("--train-step", type=int, default=None, metavar="M",
-                    help="counter-collection runs of the training kernels: only the 3-layer WN training step at M "
-                         "rows (no headline, no other legs); prints its timing JSON")
+                    help="counter-collection runs of the training kernels: only the WN training step at M rows "
+                         "(3 layers; 5 with --config 5l128; no headline, no other legs); prints its timing JSON")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -594,8 +594,10 @@ def main():
         sys.exit(1)
 
     if args.train_step:
+        n_layers = 5 if args.config == "5l128" else 3
         print(json.dumps({"training_step": {str(args.train_step): train_step_bench(
-            torch, args.train_step, steps=args.steps, warmup=args.warmup)}}))
+            torch, args.train_step, steps=args.steps, warmup=args.warmup, n_layers=n_layers)},
+                          "layers": n_layers}))
         return
 
     dims = CONFIG_DIMS[args.config]
