@@ -61,8 +61,9 @@ def run_train(dims, m, seed, *, dout_mode="ones", with_dx=True, x_dist="normal",
     return out, hs, dws, dx, rdws, rdx
 
 
-@pytest.mark.parametrize("m", [64, 256, 4096, 16384])
+@pytest.mark.parametrize("m", [64, 256, 4096, 16384, 65536])
 def test_3l128_weight_and_data_gradients(m):
+    # (65536 rows: two rounds per workgroup of the 8-wave kernel with dx.)
     _, _, dws, dx, rdws, rdx = run_train(D3, m, seed=m)
     for i in range(3):
         check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")
@@ -72,9 +73,9 @@ def test_3l128_weight_and_data_gradients(m):
 
 @pytest.mark.parametrize("m", [64, 4096, 16384, 65536])
 def test_5l128_weight_and_data_gradients(m):
-    # Two launches: layers 4..2 as a segment (its layer-0 activation is the
-    # stash h_2, its data gradient the fp16 dz_1 in the workspace), then
-    # layers 1..0 with dz_1 as their output gradient.
+    # Two launches: layers 4..3 as a segment (its layer-0 activation is the
+    # stash h_3, its data gradient the fp16 dz_2 in the workspace), then
+    # layers 2..0 with dz_2 as their output gradient.
     _, _, dws, dx, rdws, rdx = run_train(D5, m, seed=50 + m)
     for i in range(5):
         check_dw(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1} M={m}")

@@ -286,8 +286,8 @@ def test_wn_module_matches_committed_golden_training_step():
 
 
 def test_five_layer_module_forward_and_backward():
-    # The 5-layer backward runs as two launches (layers 4..2 as a segment
-    # handing fp16 dz_1 to layers 1..0 through the workspace).
+    # The 5-layer backward runs as two launches (layers 4..3 as a segment
+    # handing fp16 dz_2 to layers 2..0 through the workspace).
     import fused_mlp5
 
     torch.manual_seed(4)
