@@ -33,18 +33,18 @@ import torch
 
 from . import ops
 
-# Activation recomputation policy: "auto" recomputes h_{L-1} from
-# RECOMPUTE_MIN_ROWS rows on where that makes the training step faster
-# (MI355X, stash -> recompute): the 5-layer network (the weight-norm
-# module's step as one HIP graph: 0.256 -> 0.260 ms at 131072 rows, 0.443 ->
-# 0.452 ms at 262144, 1.443 -> 1.404 ms at 1048576) and 3-layer steps that
-# also need dx (forward + backward: 123 -> 135 us at 131072 rows, 838 -> 797
-# us at 1048576); the 3-layer step without dx keeps the stash at every size,
-# its 8-wave backward being the faster one (module step 0.148 -> 0.164 ms at
-# 131072 rows, 0.822 -> 0.836 ms at 1048576).  "always" / "never" force the
-# choice where the shape allows it.
+# Activation recomputation policy: "auto" recomputes h_{L-1} where that makes
+# the training step faster (MI355X, stash -> recompute; the weight-norm
+# module's step replayed as one HIP graph, or forward + backward with dx):
+# 3 layers from RECOMPUTE_MIN_ROWS rows (0.147 -> 0.152 ms at 131072 rows,
+# 0.266 -> 0.251 ms at 262144, 0.854 -> 0.784 ms at 1048576; with dx 124 ->
+# 133 us at 131072 rows, 855 -> 830 us at 1048576), 5 layers from
+# RECOMPUTE_MIN_ROWS_5L (0.256 -> 0.253 ms at 131072 rows, 1.481 -> 1.379 ms
+# at 1048576; with dx 221 -> 211 us at 131072).  "always" / "never" force
+# the choice where the shape allows it.
 RECOMPUTE = "auto"
-RECOMPUTE_MIN_ROWS = 1 << 20
+RECOMPUTE_MIN_ROWS = 1 << 18
+RECOMPUTE_MIN_ROWS_5L = 1 << 17
 
 # Backward implementation: "fused" (the backward megakernel, every M) or
 # "fallback" (the reference's large-M path of library GEMMs and the fused
@@ -93,8 +93,8 @@ def _use_recompute(dims, m, need_dx):
         ok = _rc_shapes[dims] = ops.bwd_recompute_supported(list(dims))
     if RECOMPUTE == "always" or not ok:
         return ok
-    # (the recomputing backward also writes dx)
-    return m >= RECOMPUTE_MIN_ROWS and (len(dims) == 6 or need_dx)
+    del need_dx  # (the recomputing backward also writes dx)
+    return m >= (RECOMPUTE_MIN_ROWS_5L if len(dims) == 6 else RECOMPUTE_MIN_ROWS)
 
 
 def kernel_dtype(x):

@@ -132,13 +132,17 @@ struct BwdGeom {
   // rows) from the exchange tile and writes dz_{l-1} into a second one, so no
   // dz is held in registers across phases.  The 64 registers that frees
   // carry the per-layer prefetch below for 3-layer networks.
-  static constexpr bool dzl() { return !N::gen && !RC && L <= 3 && lds_bytes_with(2) <= 163840; }
+  static constexpr bool dzl() { return !N::gen && (!RC || FS) && L <= 3 && lds_bytes_with(2) <= 163840; }
   static constexpr int lds_bytes() { return lds_bytes_with(dzl() ? 2 : 1); }
   // The feature split with one dz tile (its dgrad fragments leave no room
   // for a second): dz_l goes into the tile at the start of the layer, the
   // dgrad reads it back (all of it, the partner's half too) after the
   // layer's barrier, and its output stays in registers until the next layer.
   static constexpr bool dzr() { return FS && !dzl() && !N::gen && !RC && L <= 3 && lds_bytes_with(1) <= 163840; }
+  // Recompute under the feature split (RC with FS, dz through LDS): the
+  // wave pair writes its halves of h_{L-2} as MFMA operands into the second
+  // dz tile, which holds nothing at the start of a round, and each wave
+  // recomputes its half of h_{L-1} with B operands read from there.
   // Per-layer prefetch: every stash layer (and x) gets its own register
   // buffer, reloaded for the next round right after its last use, so HBM
   // always has this wave's next rows in flight instead of one phase's rows
@@ -581,11 +585,12 @@ struct BwdWave {
     // tile (l = L-1) just now, so that dgrad waits for the barrier; the
     // dz_l of lower layers were written before the previous layer's.
     constexpr bool DG_LATE = Gm::FS && (l == L - 1 || !DZL);
+    constexpr bool NEXT_H = EARLY && HA && !(Gm::RC && l == L - 1);  // (a recomputed h has no stash)
     if constexpr (Gm::has_dgrad(l) && !DG_LATE) dgrad<l, HA, B>(dz, dzn, tin, tout);
-    if constexpr (EARLY && HA && !DG_LATE) load_h<l>(row0 + rstep);  // h_l is consumed (sigma done): the next round's rows
+    if constexpr (NEXT_H && !DG_LATE) load_h<l>(row0 + rstep);  // h_l is consumed (sigma done): the next round's rows
     __syncthreads();  // every wave's rows are in the exchange tiles
     if constexpr (Gm::has_dgrad(l) && DG_LATE) dgrad<l, HA, B>(dz, dzn, tin, tout);
-    if constexpr (EARLY && HA && DG_LATE) load_h<l>(row0 + rstep);
+    if constexpr (NEXT_H && DG_LATE) load_h<l>(row0 + rstep);
     if constexpr (EARLY) {
     } else if constexpr (PF) {  // this layer's buffer is free: the next round's rows
       if constexpr (HA)
@@ -688,10 +693,13 @@ struct BwdWave {
   // First round with per-layer prefetch: every layer's rows.
   template <int l>
   __device__ __forceinline__ void prefetch_all(int64_t r0) {
-    if constexpr (l >= 1 || SEG)
+    if constexpr (Gm::RC && l == L - 1) {
+      // recomputed every round
+    } else if constexpr (l >= 1 || SEG) {
       load_h<l>(r0);
-    else if constexpr (!SHX)  // (SHX: each round loads its own x)
+    } else if constexpr (!SHX) {  // (SHX: each round loads its own x)
       load_x(r0);
+    }
     if constexpr (l > 0) prefetch_all<l - 1>(r0);
   }
 
@@ -827,8 +835,107 @@ struct BwdWave {
     }
   }
 
+  // Recompute under the feature split (see BwdGeom::dzr): h_{L-1}'s half of
+  // this wave from all of h_{L-2} (its half in buffer L-2, the partner's
+  // through the second dz tile), into buffer L-1.
+  template <bool HALF, bool FIX>
+  __device__ __forceinline__ bool recompute_fs_t(const f16* th) {
+    constexpr int l = L - 2;
+    constexpr int KSI = N::d[l] / 16, MBO = N::d[l + 1] / 32 / NFH;
+    constexpr int KSD = Gm::dks(l);
+    const int zr = wsw, zsw = swz(zr, FZ);
+    int lk[2];
+    {
+      const int q = lane >> 4, u = lane & 15, a = u & 3, e = u >> 2;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int r = 8 * (q >> 1) + 4 * k + e;
+        const int h = 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
+        lk[k] = Gm::dfrag_off(l) * 1024 + (q & 1) * 1024 + (32 * (a & 1) + h) * 16 + 8 * (a >> 1) +
+                2 * fh * MBO * 1024;  // (this wave's first output block)
+      }
+    }
+    const char* wb = reinterpret_cast<const char*>(wfr);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    f32x16 acc[2];
+    float umax = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb <= MBO; ++mb) {
+      if (mb < MBO) {
+        const char* b0 = wb + opaque(lk[0]);
+        const char* b1 = wb + opaque(lk[1]);
+        f32x16 a = {};
+#pragma unroll
+        for (int s = 0; s < KSI; ++s) {
+          const int off = (s >> 1) * KSD * 1024 + 2 * mb * 1024 + 256 * (s & 1);  // a constant after unrolling
+          const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)const_cast<char*>(b0 + off));
+          const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)const_cast<char*>(b1 + off));
+          const f16x8 bo = *reinterpret_cast<const f16x8*>(th + zr * FZ + ((16 * s + 8 * g) ^ zsw));
+          a = mfma32x32x16<N::bf>(__builtin_bit_cast(f16x8, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7)),
+                                  bo, a);
+        }
+        acc[mb & 1] = a;
+      }
+      if (mb > 0) {
+        const int q = mb - 1;
+        const f32x16& a = acc[q & 1];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float u0 = HALF ? 2.0f * a[j] : a[j], u1 = HALF ? 2.0f * a[8 + j] : a[8 + j];
+          if constexpr (FIX) {
+            hbuf[L - 1][2 * q][j] = sp2_fix(u0, sp2(u0)) * kLn2;
+            hbuf[L - 1][2 * q + 1][j] = sp2_fix(u1, sp2(u1)) * kLn2;
+          } else {
+            hbuf[L - 1][2 * q][j] = sp2(u0) * kLn2;
+            hbuf[L - 1][2 * q + 1][j] = sp2(u1) * kLn2;
+            umax = fmaxf(umax, fmaxf(u0, u1));
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return !FIX && __builtin_amdgcn_ballot_w64(umax >= 128.0f) != 0;
+  }
+  __device__ __forceinline__ void recompute_fs() {
+    constexpr int l = L - 2;
+    constexpr int KW = N::d[l] / 16 / NFH;
+    static_assert(PF && DZL, "buffers L-2 and L-1, the second dz tile");
+    // The operands are always halved (and the products doubled), so every
+    // h_{L-2} the forward can produce (up to ~90,800) fits fp16 without a
+    // workgroup-wide decision; only values below ~8.5e-5, whose products
+    // are negligible, lose bits as fp16 subnormals.  The tile was last read
+    // before the previous round's last barriers.
+    f16* const th = tz + FZ * R;  // the second dz tile
+    {
+      constexpr float sc = 0.5f * kLog2e;
+      f16x8 v[KW];
+#pragma unroll
+      for (int s = 0; s < KW; ++s)
+        v[s] = pack8<N::bf>(hbuf[l][s][0] * sc, hbuf[l][s][1] * sc, hbuf[l][s][2] * sc, hbuf[l][s][3] * sc,
+                            hbuf[l][s][4] * sc, hbuf[l][s][5] * sc, hbuf[l][s][6] * sc, hbuf[l][s][7] * sc);
+      xwrite<FZ>(th, v, fh * KW);
+    }
+    __syncthreads();  // both halves of every row's operands are in the tile
+    // The exact form at once (two more VALU per value than the fast form
+    // and its overflow check; a second instance of the loop for the rare
+    // rerun did not fit beside the rest).
+    recompute_fs_t<true, true>(th);
+    // Rows past M: h_{L-1} = 0 as a stash would hold (see recompute()).
+    if (nrows_at(row0) < 32 && row0 + n >= p.M) {
+#pragma unroll
+      for (int s = 0; s < N::d[L - 1] / 16 / NFH; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hbuf[L - 1][s][j] = 0.0f;
+    }
+  }
+
   __device__ __forceinline__ void round() {
-    if constexpr (Gm::RC) recompute();
+    if constexpr (Gm::RC && Gm::FS)
+      recompute_fs();
+    else if constexpr (Gm::RC)
+      recompute();
     f16x8 dz[KSM], dzn[KSM];
     if constexpr (DZL) {
       xwrite<FZ>(tz, gbuf, fh * KSLW);  // dz_{L-1} = dL/dout into tile 0

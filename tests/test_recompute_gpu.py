@@ -203,9 +203,9 @@ def test_five_layer_recompute_backward_matches_oracle_and_stash(m, dout_mode):
 @pytest.mark.parametrize("wn", [False, True])
 def test_modules_recompute_policy(wn):
     # The drop-in modules take the recomputing backward under RECOMPUTE =
-    # "always" (and under "auto" from RECOMPUTE_MIN_ROWS rows for 5 layers
-    # and for 3-layer steps that need dx; the 3-layer step without dx keeps
-    # the stash); the gradients agree with the stashing path.
+    # "always" (and under "auto" from RECOMPUTE_MIN_ROWS rows for 3 layers,
+    # RECOMPUTE_MIN_ROWS_5L for 5); the gradients agree with the stashing
+    # path.
     import fused_mlp
     from mlpmk import autograd as mag
 
@@ -213,11 +213,11 @@ def test_modules_recompute_policy(wn):
     cls = fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus
     model = cls().cuda()
     x = torch.randn(5000, 128, device="cuda").half()
-    assert not mag._use_recompute(tuple(model.dims), 1 << 20, False)  # 3 layers without dx: the stash
+    assert mag._use_recompute(tuple(model.dims), 1 << 20, False)
     assert mag._use_recompute(tuple(model.dims), 1 << 20, True)  # dx too
-    assert not mag._use_recompute(tuple(model.dims), 1 << 16, True)
-    assert mag._use_recompute((128,) * 6, 1 << 20, False)
-    assert not mag._use_recompute((128,) * 6, 1 << 18, False)
+    assert not mag._use_recompute(tuple(model.dims), 1 << 17, False)
+    assert mag._use_recompute((128,) * 6, 1 << 17, False)
+    assert not mag._use_recompute((128,) * 6, 1 << 16, False)
     assert not mag._use_recompute((128,) * 5, 1 << 20, False)  # 4 layers: no recomputing kernel
     grads = {}
     policy = mag.RECOMPUTE
