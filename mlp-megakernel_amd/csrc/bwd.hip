@@ -837,9 +837,9 @@ struct BwdWave {
 
   // Recompute under the feature split (see BwdGeom::dzr): h_{L-1}'s half of
   // this wave from all of h_{L-2} (its half in buffer L-2, the partner's
-  // through the second dz tile), into buffer L-1.
-  template <bool HALF, bool FIX>
-  __device__ __forceinline__ bool recompute_fs_t(const f16* th) {
+  // through the second dz tile, halved operands), into buffer L-1: the
+  // exact form, products doubled.
+  __device__ __forceinline__ void recompute_fs_t(const f16* th) {
     constexpr int l = L - 2;
     constexpr int KSI = N::d[l] / 16, MBO = N::d[l + 1] / 32 / NFH;
     constexpr int KSD = Gm::dks(l);
@@ -858,7 +858,6 @@ struct BwdWave {
     const char* wb = reinterpret_cast<const char*>(wfr);
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     f32x16 acc[2];
-    float umax = -INFINITY;
 #pragma unroll
     for (int mb = 0; mb <= MBO; ++mb) {
       if (mb < MBO) {
@@ -883,20 +882,13 @@ struct BwdWave {
         const f32x16& a = acc[q & 1];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float u0 = HALF ? 2.0f * a[j] : a[j], u1 = HALF ? 2.0f * a[8 + j] : a[8 + j];
-          if constexpr (FIX) {
-            hbuf[L - 1][2 * q][j] = sp2_fix(u0, sp2(u0)) * kLn2;
-            hbuf[L - 1][2 * q + 1][j] = sp2_fix(u1, sp2(u1)) * kLn2;
-          } else {
-            hbuf[L - 1][2 * q][j] = sp2(u0) * kLn2;
-            hbuf[L - 1][2 * q + 1][j] = sp2(u1) * kLn2;
-            umax = fmaxf(umax, fmaxf(u0, u1));
-          }
+          const float u0 = 2.0f * a[j], u1 = 2.0f * a[8 + j];
+          hbuf[L - 1][2 * q][j] = sp2_fix(u0, sp2(u0)) * kLn2;
+          hbuf[L - 1][2 * q + 1][j] = sp2_fix(u1, sp2(u1)) * kLn2;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    return !FIX && __builtin_amdgcn_ballot_w64(umax >= 128.0f) != 0;
   }
   __device__ __forceinline__ void recompute_fs() {
     constexpr int l = L - 2;
@@ -921,7 +913,7 @@ struct BwdWave {
     // The exact form at once (two more VALU per value than the fast form
     // and its overflow check; a second instance of the loop for the rare
     // rerun did not fit beside the rest).
-    recompute_fs_t<true, true>(th);
+    recompute_fs_t(th);
     // Rows past M: h_{L-1} = 0 as a stash would hold (see recompute()).
     if (nrows_at(row0) < 32 && row0 + n >= p.M) {
 #pragma unroll
