@@ -11,7 +11,9 @@
 //     dz_{l-1} = (dz_l . W_l^T) * (1 - exp(-h_l))  (l >= 1; sigmoid(z) = 1 - exp(-h))
 //     dx       = dz_0 . W_0^T                      (optional)
 //
-// Machine mapping (one workgroup of NW waves, R = 32*NW rows per round):
+// Machine mapping (one workgroup of NW waves per CU, R rows per round: 32
+// per wave with 4 waves; with the 8-wave feature split below, 32 per wave
+// pair):
 //
 //  * dgrad runs in registers exactly like the forward chain, in the
 //    transposed orientation (MFMA M = features of a_l, N = 32 rows, K =
@@ -39,6 +41,13 @@
 //    registers that frees let every layer's rows of the next round be
 //    requested as soon as this round has consumed them: HBM always has the
 //    next rows in flight.
+//  * Feature split (FS, 8 waves, the 128-wide networks): wave pairs share a
+//    32-row block and split every activation, gradient and dgrad output
+//    block in feature halves, each wave owning 2 of each layer's 16 dW
+//    tiles: 96 accumulator registers instead of 192, so two waves share a
+//    SIMD and hide each other's waits.  The dgrad reads all of dz_l (the
+//    partner's half too) from the exchange tile.  With recompute, the pair
+//    publishes its halves of h_{L-2} through the second dz tile.
 //
 // Segment mode (SEG) runs the upper layers of a deeper network on their own:
 // layer 0 of the segment then takes its activation from the fp32 stash of
