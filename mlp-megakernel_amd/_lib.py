@@ -101,6 +101,15 @@ def int_array(vals):
     return arr, arr
 
 
+def dims_array(key):
+    """``int_array`` for a tuple of Python ints, returning the array alone
+    (the launch paths' form: one dictionary lookup)."""
+    arr = _int_arrays.get(key)
+    if arr is None:
+        arr = _int_arrays[key] = (c_int * len(key))(*key)
+    return arr
+
+
 def ptr_array(ptrs):
     """A C array of device pointers (None for NULL); ``(array, keepalive)``."""
     arr = (c_void_p * len(ptrs))(*ptrs)

@@ -144,52 +144,6 @@ class FusedMLPFunction(torch.autograd.Function):
             rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0])
             out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
             ctx.save_for_backward(x, *weights, *[h for h in hs if h is not None])
-            ctx.n_layers = len(weights)
-            ctx.recompute = rc
-        else:
-            out = ops.fwd(x, weights)
-        return out
-
-    @staticmethod
-    @torch.amp.custom_bwd(device_type="cuda")
-    def backward(ctx, dout):
-        L = ctx.n_layers
-        saved = ctx.saved_tensors
-        x, weights, hs = saved[0], list(saved[1 : 1 + L]), list(saved[1 + L :])
-        if ctx.recompute:
-            hs.append(None)  # h_{L-1}: recomputed by the backward kernel
-        dout = _as_row_broadcast(dout.to(x.dtype))
-        dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
-        dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        _run_bwd(x, weights, hs, dout, dws, dx)
-        return (dx, *[d if need else None for d, need in zip(dws, ctx.needs_input_grad[1:])])
-
-
-class FusedMLPWNFunction(torch.autograd.Function):
-    """Weight-normalised MLP: ``W_l[:, j] = g_l[j] v_l[:, j] / ||v_l[:, j]||``
-    for every layer from the contiguous blocks ``v_all`` / ``g_all``
-    (mlp_fused.md:478-480), then the fused MLP.
-
-    Launches: forward = weight norm (all layers) + forward megakernel;
-    backward = backward megakernel + weight-norm backward (all layers).
-    """
-
-    @staticmethod
-    @torch.amp.custom_fwd(device_type="cuda")
-    def forward(ctx, x, v_all, g_all, dims):
-        x = x.to(kernel_dtype(x)).contiguous()
-        dims = tuple(int(d) for d in dims)
-        L = len(dims) - 1
-        dev = x.device
-        nw = sum(dims[i] * dims[i + 1] for i in range(L))
-        w_all = torch.empty(nw, dtype=x.dtype, device=dev)  # the megakernels' element type
-        inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=dev)
-        ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
-        weights = _split(w_all, dims)
-        if any(ctx.needs_input_grad):
-            rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0])
-            out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
-            ctx.save_for_backward(x, v_all, g_all, w_all, inv_all, *[h for h in hs if h is not None])
             ctx.dims = dims
             ctx.recompute = rc
         else:
@@ -200,20 +154,123 @@ class FusedMLPWNFunction(torch.autograd.Function):
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, dout):
         dims = ctx.dims
+        L = len(dims) - 1
+        saved = ctx.saved_tensors
+        x, weights, hs = saved[0], list(saved[1 : 1 + L]), list(saved[1 + L :])
+        if ctx.recompute:
+            hs.append(None)  # h_{L-1}: recomputed by the backward kernel
+        dout = _as_row_broadcast(dout.to(x.dtype))
+        dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
+        dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        if _backward_impl() == "fused" and _fused_bwd_supported(dims):
+            # x, the weights and the stash were checked by the forward.
+            M = int(x.shape[0])
+            dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, x.device)
+            ops._bwd_raw(x.device, dims, ops._elem_code(x.dtype), x.data_ptr(), [w.data_ptr() for w in weights],
+                         [h.data_ptr() if h is not None else None for h in hs], dout.data_ptr(), row_stride,
+                         dx.data_ptr() if dx is not None else None, [d.data_ptr() for d in dws], M)
+        else:
+            _run_bwd(x, weights, hs, dout, dws, dx)
+        return (dx, *[d if need else None for d, need in zip(dws, ctx.needs_input_grad[1:])])
+
+
+class FusedMLPWNFunction(torch.autograd.Function):
+    """Weight-normalised MLP: ``W_l[:, j] = g_l[j] v_l[:, j] / ||v_l[:, j]||``
+    for every layer from the contiguous blocks ``v_all`` / ``g_all``
+    (mlp_fused.md:478-480), then the fused MLP.
+
+    Launches: forward = weight norm (all layers) + forward megakernel;
+    backward = backward megakernel + weight-norm backward (all layers).
+    The buffers between them (W, 1/||v||, the stash, dW, dv, dg) are
+    allocated here with known shapes, so the launches take their pointers
+    directly (``ops._*_raw``) instead of per-layer views.
+    """
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx, x, v_all, g_all, dims):
+        x = x.to(kernel_dtype(x)).contiguous()
+        dims = tuple(int(d) for d in dims)
+        nw, ng, woff = _layout(dims)
+        dev = x.device
+        if dev.type != "cuda":
+            raise ValueError(f"x must be on a GPU device, got {dev}")
+        if x.dim() != 2 or int(x.shape[1]) != dims[0]:
+            raise ValueError(f"x has shape {tuple(x.shape)}, expected [M, {dims[0]}]")
+        v_all = v_all.contiguous()
+        g_all = g_all.contiguous()
+        pcode = ops._param_dtype(v_all)
+        if g_all.dtype != v_all.dtype or v_all.device != dev or g_all.device != dev:
+            raise TypeError("v_all and g_all must share a dtype and x's device")
+        if v_all.numel() != nw or g_all.numel() != ng:
+            raise ValueError("weight-norm block sizes do not match dims")
+        code = ops._elem_code(x.dtype)
+        w_all = torch.empty(nw, dtype=x.dtype, device=dev)  # the megakernels' element type
+        inv_all = torch.empty(ng, dtype=torch.float32, device=dev)
+        ops._wn_fwd_raw(dev, dims, pcode, code, v_all.data_ptr(), g_all.data_ptr(), w_all.data_ptr(),
+                        inv_all.data_ptr())
+        wb = w_all.data_ptr()
+        w_ptrs = [wb + 2 * o for o in woff]
+        M = int(x.shape[0])
+        out = torch.empty((M, dims[-1]), dtype=x.dtype, device=dev)
+        if any(ctx.needs_input_grad):
+            rc = _use_recompute(dims, M, ctx.needs_input_grad[0])
+            hs = [torch.empty((M, d), dtype=torch.float32, device=dev) for d in dims[1:-1]]
+            if rc:
+                hs[-1] = None
+            ops._fwd_raw(dev, dims, code, x.data_ptr(), w_ptrs, out.data_ptr(),
+                         [h.data_ptr() if h is not None else None for h in hs], M)
+            ctx.save_for_backward(x, v_all, g_all, w_all, inv_all, *[h for h in hs if h is not None])
+            ctx.dims = dims
+            ctx.recompute = rc
+        else:
+            ops._fwd_raw(dev, dims, code, x.data_ptr(), w_ptrs, out.data_ptr(), None, M)
+        return out
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dout):
+        dims = ctx.dims
+        nw, ng, woff = _layout(dims)
         x, v_all, g_all, w_all, inv_all, *hs = ctx.saved_tensors
         if ctx.recompute:
             hs.append(None)  # h_{L-1}: recomputed by the backward kernel
-        weights = _split(w_all, dims)
+        dev = x.device
+        M = int(x.shape[0])
         dout = _as_row_broadcast(dout.to(x.dtype))
-        dw_all = torch.zeros(w_all.numel(), dtype=torch.float32, device=x.device)
+        dw_all = torch.zeros(nw, dtype=torch.float32, device=dev)
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        _run_bwd(x, weights, hs, dout, _split(dw_all, dims), dx)
+        if _backward_impl() == "fused" and _fused_bwd_supported(dims):
+            dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, dev)
+            wb, gb = w_all.data_ptr(), dw_all.data_ptr()
+            ops._bwd_raw(dev, dims, ops._elem_code(x.dtype), x.data_ptr(), [wb + 2 * o for o in woff],
+                         [h.data_ptr() if h is not None else None for h in hs], dout.data_ptr(), row_stride,
+                         dx.data_ptr() if dx is not None else None, [gb + 4 * o for o in woff], M)
+        else:
+            _run_bwd(x, _split(w_all, dims), hs, dout, _split(dw_all, dims), dx)
         dv = dg = None
         if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
             dv = torch.empty_like(v_all)
             dg = torch.empty_like(g_all)
-            ops.wn_bwd(dims, dw_all, v_all.contiguous(), g_all.contiguous(), inv_all, dv, dg)
+            ops._wn_bwd_raw(dev, dims, ops._param_dtype(v_all), dw_all.data_ptr(), v_all.data_ptr(),
+                            g_all.data_ptr(), inv_all.data_ptr(), dv.data_ptr(), dg.data_ptr())
         return dx, dv, dg, None
+
+
+_layouts = {}
+
+
+def _layout(dims):
+    """``(n_weights, n_columns, element offsets of each W_l)`` of the flat
+    weight-norm blocks of ``dims`` (cached)."""
+    lay = _layouts.get(dims)
+    if lay is None:
+        offs, o = [], 0
+        for i in range(len(dims) - 1):
+            offs.append(o)
+            o += dims[i] * dims[i + 1]
+        lay = _layouts[dims] = (o, sum(dims[1:]), tuple(offs))
+    return lay
 
 
 def _split(flat, dims):

@@ -85,6 +85,12 @@ def _fwd_code(dtype, name="x"):
     return code
 
 
+def _ok(t, dtype, device):
+    """The checks of ``_require`` as one boolean (no name formatting on the
+    launch path; ``_require`` then names what failed)."""
+    return isinstance(t, torch.Tensor) and t.dtype == dtype and t.device == device and t.is_contiguous()
+
+
 def _require(t, name, dtype, device):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
@@ -97,13 +103,15 @@ def _require(t, name, dtype, device):
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+# Current device without torch.cuda.current_device()'s Python layers (~1 us).
+_cur_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
 def _stream(device):
     """Handle of the current torch stream of ``device`` (the raw query costs
     ~0.1 us per call against ~3 us for ``current_stream().cuda_stream``)."""
     if _raw_stream is not None:
-        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+        return _raw_stream(device.index if device.index is not None else _cur_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -111,11 +119,81 @@ def _launch(device, fn, *args):
     """``fn(*args, stream)`` with ``device`` current: the library launches on
     the calling thread's current HIP device.  Switches only when needed (the
     device context manager costs ~2.4 us per call)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    if torch.cuda.current_device() == idx:
-        return fn(*args, _stream(device))
+    cur = _cur_device()
+    idx = device.index
+    if idx is None or idx == cur:
+        if _raw_stream is not None:
+            return fn(*args, _raw_stream(cur))
+        return fn(*args, torch.cuda.current_stream(cur).cuda_stream)
     with torch.cuda.device(idx):
         return fn(*args, _stream(device))
+
+
+# Pointer-level launches.  The public wrappers below validate tensors and call
+# these; the autograd Functions call them directly for buffers they allocated
+# themselves (shapes known), which keeps a training step's host time down.
+# ``dims`` is a tuple of ints; pointers are ints (None for NULL).
+def _fwd_raw(dev, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M):
+    lib = _lib.get()
+    L = len(dims) - 1
+    pw = (_lib.c_void_p * L)(*w_ptrs)
+    ps = None if stash_ptrs is None else (_lib.c_void_p * (L - 1))(*stash_ptrs)
+    rc = _launch(dev, lib.mlpmk_fwd, L, _lib.dims_array(dims), code, x_ptr, pw, out_ptr, ps, M)
+    if rc:
+        _check("mlpmk_fwd", rc)
+
+
+def _bwd_raw(dev, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, dx_ptr, dw_ptrs, M, workspace=True):
+    lib = _lib.get()
+    L = len(dims) - 1
+    pd = _lib.dims_array(dims)
+    pw = (_lib.c_void_p * L)(*w_ptrs)
+    ps = (_lib.c_void_p * (L - 1))(*stash_ptrs)
+    pg = (_lib.c_void_p * L)(*dw_ptrs)
+    if workspace and M > 0:
+        nbytes = _workspace_bytes(dev.index if dev.index is not None else _cur_device(), dims, M, dx_ptr is not None,
+                                  code)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        rc = _launch(dev, lib.mlpmk_bwd_ws, L, pd, code, x_ptr, pw, ps, dout_ptr, row_stride, dx_ptr, pg,
+                     ws.data_ptr(), nbytes, M)
+        if rc:
+            _check("mlpmk_bwd_ws", rc)
+    else:
+        rc = _launch(dev, lib.mlpmk_bwd, L, pd, code, x_ptr, pw, ps, dout_ptr, row_stride, dx_ptr, pg, M)
+        if rc:
+            _check("mlpmk_bwd", rc)
+
+
+def _wn_fwd_raw(dev, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr):
+    rc = _launch(dev, _lib.get().mlpmk_wn_fwd, len(dims) - 1, _lib.dims_array(dims), pcode, wcode, v_ptr, g_ptr, w_ptr,
+                 inv_ptr)
+    if rc:
+        _check("mlpmk_wn_fwd", rc)
+
+
+def _wn_bwd_raw(dev, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr):
+    rc = _launch(dev, _lib.get().mlpmk_wn_bwd, len(dims) - 1, _lib.dims_array(dims), pcode, dw_ptr, v_ptr, g_ptr,
+                 inv_ptr, dv_ptr, dg_ptr)
+    if rc:
+        _check("mlpmk_wn_bwd", rc)
+
+
+def _dout_rows(dout, M, out_w, dtype, dev):
+    """``(dout, row_stride)`` as the library reads it: [M, OUT] rows with unit
+    column stride whose row stride (0 for a broadcast row) is a multiple of 8
+    elements; other row strides are copied into padded rows."""
+    if dout.dtype != dtype or dout.device != dev:
+        raise TypeError(f"dout must be {dtype} on the same device as x")
+    if tuple(dout.shape) != (M, out_w) or dout.stride(1) != 1:
+        raise ValueError(f"dout must be [M, OUT]={M, out_w} with unit column stride")
+    row_stride = int(dout.stride(0)) if M > 1 else -(-out_w // 8) * 8
+    if row_stride % 8 != 0:
+        # The library reads dout rows from 16-byte boundaries: an output width
+        # that is not a multiple of 8 gets rows padded to the next multiple.
+        padded = torch.zeros((M, -(-out_w // 8) * 8), dtype=dtype, device=dev)
+        padded[:, :out_w] = dout
+        dout, row_stride = padded, padded.shape[1]
+    return dout, row_stride
 
 
 def fwd_into(x, weights, out, stash=None):
@@ -131,15 +209,19 @@ def fwd_into(x, weights, out, stash=None):
     dev = x.device
     if dev.type != "cuda":
         raise ValueError(f"x must be on a GPU device, got {dev}")
-    code = _fwd_code(x.dtype)
-    _require(x, "x", x.dtype, dev)
+    xd = x.dtype
+    code = _fwd_code(xd)
+    if not x.is_contiguous():
+        _require(x, "x", xd, dev)
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
     for i, w in enumerate(weights):
-        _require(w, f"w{i + 1}", x.dtype, dev)
+        if not _ok(w, xd, dev):
+            _require(w, f"w{i + 1}", xd, dev)
     dims = _dims_of(x, weights)
     M = int(x.shape[0])
-    _require(out, "out", x.dtype, dev)
+    if not _ok(out, xd, dev):
+        _require(out, "out", xd, dev)
     if tuple(out.shape) != (M, dims[-1]):
         raise ValueError(f"out has shape {tuple(out.shape)}, expected {(M, dims[-1])}")
     stash_ptrs = None
@@ -149,16 +231,12 @@ def fwd_into(x, weights, out, stash=None):
         for i, s in enumerate(stash):
             if s is None:
                 continue
-            _require(s, f"stash[{i}]", torch.float32, dev)
+            if not _ok(s, torch.float32, dev):
+                _require(s, f"stash[{i}]", torch.float32, dev)
             if tuple(s.shape) != (M, dims[i + 1]):
                 raise ValueError(f"stash[{i}] has shape {tuple(s.shape)}, expected {(M, dims[i + 1])}")
         stash_ptrs = [s.data_ptr() if s is not None else None for s in stash]
-    lib = _lib.get()
-    pd, _k1 = _lib.int_array(dims)
-    pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
-    ps, _k3 = (_lib.ptr_array(stash_ptrs) if stash_ptrs is not None else (None, None))
-    rc = _launch(dev, lib.mlpmk_fwd, len(weights), pd, code, x.data_ptr(), pw, out.data_ptr(), ps, M)
-    _check("mlpmk_fwd", rc)
+    _fwd_raw(dev, tuple(dims), code, x.data_ptr(), [w.data_ptr() for w in weights], out.data_ptr(), stash_ptrs, M)
     return out
 
 
@@ -208,16 +286,19 @@ _ws_bytes = {}
 def bwd_workspace_bytes(dims, M, with_dx, device=None, dtype=torch.float16):
     """Bytes of workspace ``mlpmk_bwd_ws`` needs on ``device`` (default: the
     current device) for tensors of ``dtype``; cached per device, shape and M."""
-    idx = torch.cuda.current_device() if device is None or device.index is None else device.index
-    code = _elem_code(dtype)
-    key = (idx, tuple(dims), int(M), bool(with_dx), code)
+    idx = _cur_device() if device is None or device.index is None else device.index
+    return _workspace_bytes(idx, tuple(int(d) for d in dims), int(M), bool(with_dx), _elem_code(dtype))
+
+
+def _workspace_bytes(idx, dims, M, with_dx, code):
+    key = (idx, dims, M, with_dx, code)
     n = _ws_bytes.get(key)
     if n is None:
         lib = _lib.get()
-        pd, _k = _lib.int_array(dims)
         out = ctypes.c_int64(0)
         with torch.cuda.device(idx):
-            rc = lib.mlpmk_bwd_workspace_size(len(dims) - 1, pd, code, M, int(with_dx), ctypes.byref(out))
+            rc = lib.mlpmk_bwd_workspace_size(len(dims) - 1, _lib.dims_array(dims), code, M, int(with_dx),
+                                              ctypes.byref(out))
         _check("mlpmk_bwd_workspace_size", rc)
         n = _ws_bytes[key] = out.value
     return n
@@ -236,10 +317,13 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     recomputing backward (``bwd_recompute_supported``; with or without dx).
     """
     dev = x.device
-    code = _elem_code(x.dtype)
-    _require(x, "x", x.dtype, dev)
+    xd = x.dtype
+    code = _elem_code(xd)
+    if not _ok(x, xd, dev):
+        _require(x, "x", xd, dev)
     for i, w in enumerate(weights):
-        _require(w, f"w{i + 1}", x.dtype, dev)
+        if not _ok(w, xd, dev):
+            _require(w, f"w{i + 1}", xd, dev)
     dims = _dims_of(x, weights)
     M = int(x.shape[0])
     if len(stash) != len(weights) - 1:
@@ -247,44 +331,23 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     for i, s in enumerate(stash):
         if s is None and i == len(stash) - 1:
             continue  # recompute mode: the library checks that the shape has it
-        _require(s, f"stash[{i}]", torch.float32, dev)
+        if not _ok(s, torch.float32, dev):
+            _require(s, f"stash[{i}]", torch.float32, dev)
         if tuple(s.shape) != (M, dims[i + 1]):
             raise ValueError(f"stash[{i}] has shape {tuple(s.shape)}, expected {(M, dims[i + 1])}")
     for i, d in enumerate(dws):
-        _require(d, f"dw[{i}]", torch.float32, dev)
+        if not _ok(d, torch.float32, dev):
+            _require(d, f"dw[{i}]", torch.float32, dev)
         if tuple(d.shape) != (dims[i], dims[i + 1]):
             raise ValueError(f"dw[{i}] has shape {tuple(d.shape)}, expected {(dims[i], dims[i + 1])}")
-    if dout.dtype != x.dtype or dout.device != dev:
-        raise TypeError(f"dout must be {x.dtype} on the same device as x")
-    if tuple(dout.shape) != (M, dims[-1]) or dout.stride(1) != 1:
-        raise ValueError(f"dout must be [M, OUT]={M, dims[-1]} with unit column stride")
-    row_stride = int(dout.stride(0)) if M > 1 else -(-dims[-1] // 8) * 8
-    if row_stride % 8 != 0:
-        # The library reads dout rows from 16-byte boundaries: an output width
-        # that is not a multiple of 8 gets rows padded to the next multiple.
-        padded = torch.zeros((M, -(-dims[-1] // 8) * 8), dtype=x.dtype, device=dev)
-        padded[:, : dims[-1]] = dout
-        dout, row_stride = padded, padded.shape[1]
+    dout, row_stride = _dout_rows(dout, M, dims[-1], x.dtype, dev)
     if dx is not None:
         _require(dx, "dx", x.dtype, dev)
         if tuple(dx.shape) != (M, dims[0]):
             raise ValueError(f"dx has shape {tuple(dx.shape)}, expected {(M, dims[0])}")
-    lib = _lib.get()
-    pd, _k1 = _lib.int_array(dims)
-    pw, _k2 = _lib.ptr_array([w.data_ptr() for w in weights])
-    ps, _k3 = _lib.ptr_array([s.data_ptr() if s is not None else None for s in stash])
-    pg, _k4 = _lib.ptr_array([d.data_ptr() for d in dws])
-    dxp = dx.data_ptr() if dx is not None else None
-    if workspace and M > 0:
-        nbytes = bwd_workspace_bytes(dims, M, dx is not None, dev, x.dtype)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        rc = _launch(dev, lib.mlpmk_bwd_ws, len(weights), pd, code, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
-                     dxp, pg, ws.data_ptr(), nbytes, M)
-        _check("mlpmk_bwd_ws", rc)
-    else:
-        rc = _launch(dev, lib.mlpmk_bwd, len(weights), pd, code, x.data_ptr(), pw, ps, dout.data_ptr(), row_stride,
-                     dxp, pg, M)
-        _check("mlpmk_bwd", rc)
+    _bwd_raw(dev, tuple(dims), code, x.data_ptr(), [w.data_ptr() for w in weights],
+             [s.data_ptr() if s is not None else None for s in stash], dout.data_ptr(), row_stride,
+             dx.data_ptr() if dx is not None else None, [d.data_ptr() for d in dws], M, workspace)
     return dws, dx
 
 
@@ -311,11 +374,8 @@ def wn_fwd(dims, v_all, g_all, w_all, inv_all):
     ng = sum(dims[1:])
     if v_all.numel() != nw or w_all.numel() != nw or g_all.numel() != ng or inv_all.numel() != ng:
         raise ValueError("weight-norm block sizes do not match dims")
-    lib = _lib.get()
-    pd, _k = _lib.int_array(dims)
-    rc = _launch(dev, lib.mlpmk_wn_fwd, len(dims) - 1, pd, dt, wcode, v_all.data_ptr(), g_all.data_ptr(),
-                 w_all.data_ptr(), inv_all.data_ptr())
-    _check("mlpmk_wn_fwd", rc)
+    _wn_fwd_raw(dev, tuple(int(d) for d in dims), dt, wcode, v_all.data_ptr(), g_all.data_ptr(), w_all.data_ptr(),
+                inv_all.data_ptr())
     return w_all, inv_all
 
 
@@ -335,11 +395,8 @@ def wn_bwd(dims, dw_all, v_all, g_all, inv_all, dv_all, dg_all):
         raise ValueError("weight-norm block sizes do not match dims")
     if g_all.numel() != ng or inv_all.numel() != ng or dg_all.numel() != ng:
         raise ValueError("weight-norm block sizes do not match dims")
-    lib = _lib.get()
-    pd, _k = _lib.int_array(dims)
-    rc = _launch(dev, lib.mlpmk_wn_bwd, len(dims) - 1, pd, dt, dw_all.data_ptr(), v_all.data_ptr(),
-                 g_all.data_ptr(), inv_all.data_ptr(), dv_all.data_ptr(), dg_all.data_ptr())
-    _check("mlpmk_wn_bwd", rc)
+    _wn_bwd_raw(dev, tuple(int(d) for d in dims), dt, dw_all.data_ptr(), v_all.data_ptr(), g_all.data_ptr(),
+                inv_all.data_ptr(), dv_all.data_ptr(), dg_all.data_ptr())
     return dv_all, dg_all
 
 

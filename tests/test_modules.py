@@ -65,6 +65,8 @@ def test_product_path_refuses_cpu_tensors():
     ws = [torch.randn(128, 128).half() for _ in range(3)]
     with pytest.raises(ValueError, match="GPU"):
         kernel._fused_mlp_fwd(x, *ws)
+    with pytest.raises(ValueError, match="GPU"):
+        fused_mlp.FusedMLPSoftplusWN()(torch.randn(4, 128).half())
     # The eager reference model of kernel.py stays available and runs anywhere.
     ref = kernel.Model()(x.float(), *[w.float() for w in ws])
     assert ref.shape == (4, 128)

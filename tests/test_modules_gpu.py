@@ -139,20 +139,18 @@ def test_module_under_autocast_with_fp32_parameters():
 
 
 class _RecordStash:
-    """Wraps ops.fwd (the autograd module's binding) and records the stash
-    argument of every forward launch."""
+    """Wraps ops._fwd_raw (every forward launch of the package goes through
+    it) and records whether each launch wrote a stash."""
 
     def __init__(self, monkeypatch):
-        import mlpmk.autograd as ag
-
         self.calls = []
-        real = ops.fwd
+        real = ops._fwd_raw
 
-        def fwd(x, weights, stash=False, **kw):
-            self.calls.append(bool(stash))
-            return real(x, weights, stash=stash, **kw)
+        def fwd_raw(dev, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M):
+            self.calls.append(stash_ptrs is not None)
+            return real(dev, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M)
 
-        monkeypatch.setattr(ag.ops, "fwd", fwd)
+        monkeypatch.setattr(ops, "_fwd_raw", fwd_raw)
 
 
 @pytest.mark.parametrize("wn", [False, True])
