@@ -10,7 +10,7 @@ import torch
 import fused_mlp
 import fused_mlp5
 import kernel
-from mlpmk.autograd import _as_row_broadcast, _split
+from mlpmk.autograd import _as_row_broadcast, _layout, _split
 
 
 def test_parameter_layout_and_init():
@@ -44,6 +44,12 @@ def test_weight_norm_blocks_are_contiguous_views():
     flat = torch.arange(10.0)
     parts = _split(flat, (1, 2, 4))
     assert [tuple(p.shape) for p in parts] == [(1, 2), (2, 4)] and parts[1][1, 3] == 9
+    # The autograd Functions launch on element offsets into the flat blocks
+    # (no per-layer views): they must be where _split's views start.
+    nw, ng, woff = _layout((32, 64, 64, 16))
+    views = _split(m.v_all.detach(), m.dims)
+    assert nw == m.v_all.numel() and ng == m.g_all.numel()
+    assert [m.v_all.data_ptr() + 4 * o for o in woff] == [v.data_ptr() for v in views]
 
 
 def test_sum_gradient_becomes_one_broadcast_row():
