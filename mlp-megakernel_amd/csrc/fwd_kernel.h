@@ -292,6 +292,7 @@ struct BlockIO {
   rsrc_t x, out;
   rsrc_t stash[kMaxLayers];
   i32x4* stage;  // this wave's LDS staging tile for the output rows (STAGE only)
+  unsigned stash_on;  // bit l: stash entry l requested (STASH only)
   int dl[kMaxLayers + 1];  // true widths (Gen networks only)
 };
 
@@ -304,7 +305,11 @@ struct BlockIO {
 //    per instruction and complete a row's lines piecemeal, which costs HBM
 //    write efficiency once rows are wider than 64 bytes.  The tile holds two
 //    32-feature output blocks (128 bytes per row) and is flushed after every
-//    second block.  Needs output rows of a multiple of 64 features;
+//    second block.  Needs output rows of a multiple of 64 features.  In the
+//    training forwards of 8+ waves the same tile also carries each hidden
+//    layer's fp32 stash rows, one 32-feature block (128 bytes per row) at a
+//    time (flush_stash_stage): 3L-128 at 131072 rows 48.3 -> 42.2 us, at 1M
+//    rows 360 -> 325 us;
 //  * the 16-byte row-block claim counter.  Without it waves would split the
 //    workgroup's blocks statically, and the SIMD arbiter's preference for the
 //    older of two waves then lets one wave of each pair finish far ahead of
@@ -354,10 +359,13 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
   io.x = make_rsrc(reinterpret_cast<const char*>(p.x) + row0 * io.dl[0] * E, rows * io.dl[0] * E);
   io.out = make_rsrc(reinterpret_cast<const char*>(p.out) + row0 * io.dl[N::L] * E, rows * io.dl[N::L] * E);
   if constexpr (STASH) {
+    io.stash_on = 0;
 #pragma unroll
-    for (int l = 0; l < N::L - 1; ++l)
+    for (int l = 0; l < N::L - 1; ++l) {
       io.stash[l] = p.stash[l] ? make_rsrc(p.stash[l] + row0 * io.dl[l + 1], rows * io.dl[l + 1] * 4u)
                                : make_rsrc(nullptr, 0u);  // not requested: every store dropped
+      if (p.stash[l]) io.stash_on |= 1u << l;
+    }
   }
   return io;
 }
@@ -552,7 +560,28 @@ constexpr bool kPropagate = N::L <= 3;
 template <int ROW_BYTES>
 constexpr int kDirectOutStore = ROW_BYTES > 64 ? kStashStore : kStreamStore;
 
-template <class N, int l, int NB, bool STASH, bool STAGE, bool EXACT, int KSM>
+// Stores the staged 128-byte segment mb (fp32 features [32 mb, 32 mb + 32))
+// of the wave's 32 stash rows of width W: 8 rows x 128 bytes (8 whole cache
+// lines) per instruction, against 32 rows x 2 pieces of 16 bytes for stores
+// straight from the MFMA layout.  Default cache policy, as those.
+template <int W>
+__device__ __forceinline__ void flush_stash_stage(const BlockIO& io, const rsrc_t& sr, int mb, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = 64 * i + lane;
+    const int row = q >> 3, c = q & 7;
+    const i32x4 v = io.stage[stage_slot(row, c)];
+    __builtin_amdgcn_raw_buffer_store_b128(v, sr, row * W * 4 + mb * 128 + c * 16, 0, kStashStore);
+  }
+  // The next writes into the tile must stay behind these reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <class N, int l, int NB, bool STASH, int STAGE, bool EXACT, int KSM>
 __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[NB], int mb,
                                          f16x8 (&nxt)[KSM][NB], bool& bad, f16x2& m, int lane) {
   constexpr int Nout = N::d[l + 1];
@@ -680,6 +709,20 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
           buf_store16<kStashStore>((f32x4){h[8], h[9], h[10], h[11]}, sr, e4 + 64);
           buf_store16<kStashStore>((f32x4){h[12], h[13], h[14], h[15]}, sr, e4 + 80);
         }
+      } else if constexpr (STASH && STAGE == 2 && NB == 1 && Nout % 32 == 0) {
+        // Through the wave's staging tile, so that the stash leaves as whole
+        // 128-byte lines (flush_stash_stage); registers 0..7 are chunks 2g,
+        // 2g + 1 of the row's 128-byte segment mb, 8..15 chunks 4 + 2g, 5 + 2g.
+        if ((io.stash_on >> l) & 1u) {  // (an entry not requested: nothing to stage)
+          float h[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) h[e] = s[e] * kLn2;
+          io.stage[stage_slot(n, 2 * g)] = __builtin_bit_cast(i32x4, (f32x4){h[0], h[1], h[2], h[3]});
+          io.stage[stage_slot(n, 2 * g + 1)] = __builtin_bit_cast(i32x4, (f32x4){h[4], h[5], h[6], h[7]});
+          io.stage[stage_slot(n, 2 * g + 4)] = __builtin_bit_cast(i32x4, (f32x4){h[8], h[9], h[10], h[11]});
+          io.stage[stage_slot(n, 2 * g + 5)] = __builtin_bit_cast(i32x4, (f32x4){h[12], h[13], h[14], h[15]});
+          flush_stash_stage<Nout>(io, io.stash[l], mb, lane);
+        }
       } else if constexpr (STASH) {
         const rsrc_t sr = io.stash[l];
         float h[16];
@@ -758,7 +801,7 @@ struct Chain {
 // layer's outputs.  c.fr holds step t+1's fragments on entry; the chain
 // replaces them with those of step t+2 (step 0 of the next row block after
 // the last chain of this one).
-template <class N, int t, int NB, bool STASH, bool STAGE, bool EXACT, int KSM, int RF>
+template <class N, int t, int NB, bool STASH, int STAGE, bool EXACT, int KSM, int RF>
 __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chain<N, NB, KSM>& c,
                                      const FragBase<N, RF>& fb, int64_t next, int lane) {
   using S = Steps<N>;
@@ -800,7 +843,7 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
 // step 0; on exit they hold the same for block `next`.  Returns (wave-
 // uniform) whether the fast form overflowed or met a NaN somewhere in the
 // block (see epilogue).
-template <class N, int NB, bool STASH, bool STAGE, bool EXACT, int KSM, int RF>
+template <class N, int NB, bool STASH, int STAGE, bool EXACT, int KSM, int RF>
 __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
                                           int lane_off, i32x4* stage, int64_t b, int64_t next, int lane) {
   constexpr int ROWS = 32 * NB;
@@ -823,7 +866,7 @@ __device__ __forceinline__ bool fwd_block(const FwdParams& p, Chain<N, NB, KSM>&
 // -- again with the exact form, from a fresh read of its x rows and step-0
 // fragments.  The second pass rewrites
 // every output (and stash) row of the block and leaves c as the first did.
-template <class N, int NB, bool STASH, bool STAGE, int KSM, int RF>
+template <class N, int NB, bool STASH, int STAGE, int KSM, int RF>
 __device__ __forceinline__ void fwd_block_checked(const FwdParams& p, Chain<N, NB, KSM>& c, const char* lds_b,
                                                   int lane_off, i32x4* stage, int64_t b, int64_t next,
                                                   int lane) {
@@ -866,7 +909,11 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   using Plan = LdsPlan<N, NB, NW>;
   constexpr int KSM = N::ksmax();
   constexpr int ROWS = 32 * NB;
-  constexpr bool STAGE = Plan::stage;
+  // Staging tile use: 0 none, 1 the output rows, 2 the output rows and the
+  // stash (workgroups of 8+ waves; with one block per wave, in the 4-wave
+  // kernels of small batches, the staging's LDS round trip is not hidden:
+  // M = 16384 11.3 -> 11.9 us).
+  constexpr int STAGE = Plan::stage ? (STASH && NW >= 8 ? 2 : 1) : 0;
   constexpr int TC = Plan::kTileChunks;
   constexpr int RF = Plan::reg_frags;
   constexpr bool CLAIM = Plan::claim;
