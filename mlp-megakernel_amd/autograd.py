@@ -36,9 +36,10 @@ from . import ops
 # Activation recomputation policy: "auto" recomputes h_{L-1} where that makes
 # the training step faster (MI355X, stash -> recompute; the weight-norm
 # module's step replayed as one HIP graph, or forward + backward with dx):
-# 3 layers from RECOMPUTE_MIN_ROWS rows (0.147 -> 0.152 ms at 131072 rows,
-# 0.266 -> 0.251 ms at 262144, 0.854 -> 0.784 ms at 1048576; with dx 124 ->
-# 133 us at 131072 rows, 855 -> 830 us at 1048576), 5 layers from
+# 3 layers from RECOMPUTE_MIN_ROWS rows (0.137 -> 0.140 ms at 131072 rows,
+# 0.239 -> 0.223 ms at 262144, 0.782 -> 0.726 ms at 1048576; with dx 118 ->
+# 125 us at 131072 rows, 229 -> 227 us at 262144, 785 -> 779 us at
+# 1048576), 5 layers from
 # RECOMPUTE_MIN_ROWS_5L (0.256 -> 0.253 ms at 131072 rows, 1.481 -> 1.379 ms
 # at 1048576; with dx 221 -> 211 us at 131072).  "always" / "never" force
 # the choice where the shape allows it.
