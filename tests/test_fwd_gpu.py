@@ -170,6 +170,33 @@ def test_stash_matches_hidden_activations():
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("m,recompute", [(131072 + 77, False), (131072 + 77, True), (40000 + 5, False)])
+def test_stash_rows_of_the_persistent_kernels(m, recompute):
+    # M = 131149 runs the 8-wave persistent training forward, whose stash
+    # rows leave through the LDS staging tile (ragged last block); M = 40005
+    # the 8-wave kernel at ~5 blocks per CU.  With recompute the last stash
+    # entry is not requested.
+    info = ops.fwd_launch_info((128, 128, 128, 128), m, stash=True)
+    assert (info["kernel"], info["waves"]) == ("persistent", 8), info
+    x, ws = orc.make_inputs((128, 128, 128, 128), m, seed=7)
+    xd, wd = _to_dev(x, ws)
+    out, hs = ops.fwd(xd, wd, stash=True, recompute=recompute)
+    ref, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    _check(out.float().cpu().numpy(), ref, f"stash-mode out M={m}")
+    assert torch.equal(out, ops.fwd(xd, wd))
+    for i, h in enumerate(hs):
+        if h is None:
+            assert recompute and i == len(hs) - 1
+            continue
+        got = h.cpu().numpy()
+        ok, err, _ = orc.allclose_report(got, ref_h[i], 2e-3, 2e-3)
+        assert ok, f"h{i + 1} M={m}: {err}"
+    # Every element of a requested entry is written (over a canary fill).
+    canary = torch.full((m, 128), 7.0, device="cuda")
+    ops.fwd_into(xd, wd, torch.empty_like(out), [canary, None])
+    assert torch.equal(canary, hs[0])
+
+
 def test_threshold_edges_through_identity_weights():
     # W1 = W2 = I makes out = softplus(softplus(x)) @ W3; with W3 = I the
     # output is the activation itself on chosen pre-activations, including the
