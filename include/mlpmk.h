@@ -50,6 +50,13 @@ typedef enum mlpmk_status {
  * INPUT_DTYPE constexpr (/root/reference/mlp_fused.md:159-166). */
 enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1, MLPMK_DTYPE_BF16 = 2 };
 
+/* dout_row_stride of the backward entry points for a dL/dout that is one
+ * value everywhere (the gradient of loss = out.sum(), possibly scaled): dout
+ * then points at that single element (2-byte aligned).  No counterpart in the
+ * reference, whose launcher receives the expanded tensor; it spares callers
+ * the copy that would materialise a broadcast row. */
+enum { MLPMK_DOUT_SCALAR = -1 };
+
 /* Library ABI version (major * 100 + minor). */
 int mlpmk_version(void);
 
@@ -157,9 +164,11 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
  *                    mlpmk_bwd_recompute_supported says so: the kernel then
  *                    recomputes h_{num_layers-1} from h_{num_layers-2}
  *   dout             dL/dout, dtype, row l at dout + l * dout_row_stride
- *                    elements; dout_row_stride = 0 broadcasts one row
- *                    (the expanded ones of loss = out.sum()), otherwise a
- *                    multiple of 8 (16-byte rows) not below the output width
+ *                    elements; dout_row_stride = 0 broadcasts one row,
+ *                    MLPMK_DOUT_SCALAR one element to every row and column
+ *                    (the expanded gradient of loss = out.sum()), otherwise
+ *                    a multiple of 8 (16-byte rows) not below the output
+ *                    width
  *   dx               NULL, or [M, dims[0]] dtype (written)
  *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
  *                    caller zeroes them for a fresh gradient

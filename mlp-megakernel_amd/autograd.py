@@ -115,9 +115,10 @@ def _needs_graph(*tensors):
 
 def _as_row_broadcast(dout):
     """``dout`` with unit column stride, keeping a broadcast row (stride 0)
-    as a broadcast: ``loss = out.sum()`` hands back a fully expanded scalar
-    (strides (0, 0)); that becomes one materialised row expanded over M."""
-    if dout.dim() == 2 and dout.stride(1) == 1:
+    as a broadcast and a fully expanded scalar (strides (0, 0): what ``loss =
+    out.sum()`` hands back) as it is -- the backward kernels read that one
+    element for every row and column."""
+    if dout.dim() == 2 and (dout.stride(1) == 1 or dout.stride() == (0, 0)):
         return dout
     m, n = dout.shape
     if dout.stride(0) == 0:

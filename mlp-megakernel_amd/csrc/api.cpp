@@ -217,17 +217,19 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
   if (rc) return rc;
   if ((rc = check_elem_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
-  if (dout_row_stride < 0)
-    return fail(MLPMK_ERR_INVALID_ARG, "dout_row_stride=%lld is negative", (long long)dout_row_stride);
+  const bool dout_scalar = dout_row_stride == MLPMK_DOUT_SCALAR;
+  if (dout_row_stride < 0 && !dout_scalar)
+    return fail(MLPMK_ERR_INVALID_ARG, "dout_row_stride=%lld is negative (MLPMK_DOUT_SCALAR is %d)",
+                (long long)dout_row_stride, (int)MLPMK_DOUT_SCALAR);
   if (!w || !dw) return fail(MLPMK_ERR_INVALID_ARG, "w or dw is NULL");
   if (num_layers > 1 && !stash) return fail(MLPMK_ERR_INVALID_ARG, "stash is NULL");
   if (!bwd_supported_dims(num_layers, dims))
     return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
   const int out_w = dims[num_layers];
-  if (dout_row_stride != 0 && dout_row_stride < out_w)
+  if (dout_row_stride > 0 && dout_row_stride < out_w)
     return fail(MLPMK_ERR_INVALID_ARG, "dout_row_stride=%lld is below the output width %d",
                 (long long)dout_row_stride, out_w);
-  if (dout_row_stride % 8 != 0)
+  if (!dout_scalar && dout_row_stride % 8 != 0)
     return fail(MLPMK_ERR_MISALIGNED, "dout_row_stride=%lld is not a multiple of 8 elements",
                 (long long)dout_row_stride);
   BwdParams p = {};
@@ -242,7 +244,13 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
   }
   if (M == 0) return MLPMK_OK;
   if ((rc = check_ptr(x, "x"))) return rc;
-  if ((rc = check_ptr(dout, "dout"))) return rc;
+  if (dout_scalar) {
+    if (!dout) return fail(MLPMK_ERR_INVALID_ARG, "dout is NULL");
+    if (reinterpret_cast<uintptr_t>(dout) & 1u)
+      return fail(MLPMK_ERR_MISALIGNED, "dout=%p is not 2-byte aligned", dout);
+  } else if ((rc = check_ptr(dout, "dout"))) {
+    return rc;
+  }
   for (int l = 0; l < num_layers - 1; ++l) {
     char name[16];
     snprintf(name, sizeof(name), "stash[%d]", l);

@@ -343,11 +343,24 @@ struct BwdWave {
     return make_rsrc(static_cast<const char*>(base) + r0 * width * elem, nrows_at(r0) * width * elem);
   }
 
-  // dL/dout rows from r0 as B operands.  Row stride 0 broadcasts row 0.
+  // dL/dout rows from r0 as B operands.  Row stride 0 broadcasts row 0; a
+  // negative one (MLPMK_DOUT_SCALAR) element 0 to every row and feature below
+  // the output width.
   __device__ __forceinline__ void load_dout(int64_t r0) {
     const int64_t st = p.dout_stride;
     const int OW = dw_(L);
     const uint32_t nr = nrows_at(r0);
+    if (st < 0) {
+      const rsrc_t r1 = make_rsrc(p.dout, nr ? 2u : 0u);
+      const f16 v = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(r1, 0, 0, 0));
+#pragma unroll
+      for (int s = 0; s < KSLW; ++s) {
+        const int c = 16 * (s + fh * KSLW) + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) gbuf[s][j] = (!N::gen || c + j < OW) ? v : (f16)0.0f;
+      }
+      return;
+    }
     const uint32_t bytes = nr ? (uint32_t)(((int64_t)(nr - 1) * st + OW) * 2) : 0u;
     const rsrc_t r = make_rsrc(p.dout + r0 * st, bytes);
     if constexpr (N::gen) {

@@ -26,7 +26,7 @@ struct BwdParams {
   const _Float16* w[kMaxLayersHost];
   const float* stash[kMaxLayersHost];  // stash[l] = h_{l+1}, fp32 [M, d[l+1]]
   const _Float16* dout;                // dL/dout; row r at dout + r * dout_stride
-  int64_t dout_stride;                 // elements; 0 broadcasts row 0
+  int64_t dout_stride;                 // elements; 0 broadcasts row 0, -1 element 0
   _Float16* dx;                        // nullable
   float* dw[kMaxLayersHost];           // fp32 [d[l], d[l+1]], accumulated with atomics
   int64_t M;

@@ -178,13 +178,21 @@ def _wn_bwd_raw(dev, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr)
         _check("mlpmk_wn_bwd", rc)
 
 
+DOUT_SCALAR = -1  # MLPMK_DOUT_SCALAR
+
+
 def _dout_rows(dout, M, out_w, dtype, dev):
-    """``(dout, row_stride)`` as the library reads it: [M, OUT] rows with unit
+    """``(dout, row_stride)`` as the library reads it: one element broadcast
+    everywhere (both strides 0: ``DOUT_SCALAR``), or [M, OUT] rows with unit
     column stride whose row stride (0 for a broadcast row) is a multiple of 8
     elements; other row strides are copied into padded rows."""
     if dout.dtype != dtype or dout.device != dev:
         raise TypeError(f"dout must be {dtype} on the same device as x")
-    if tuple(dout.shape) != (M, out_w) or dout.stride(1) != 1:
+    if tuple(dout.shape) != (M, out_w):
+        raise ValueError(f"dout must be [M, OUT]={M, out_w}")
+    if M > 0 and dout.stride() == (0, 0):
+        return dout, DOUT_SCALAR
+    if dout.stride(1) != 1:
         raise ValueError(f"dout must be [M, OUT]={M, out_w} with unit column stride")
     row_stride = int(dout.stride(0)) if M > 1 else -(-out_w // 8) * 8
     if row_stride % 8 != 0:
@@ -309,7 +317,9 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     (callers zero them first) and writes ``dx`` if given.
 
     ``dout`` is [M, OUT] fp16 with unit column stride; a row stride of 0
-    (``t.expand(M, OUT)`` of one row) is passed through as a broadcast.
+    (``t.expand(M, OUT)`` of one row) is passed through as a broadcast, and
+    so is one element expanded over both dimensions (what ``loss =
+    out.sum()`` hands back: ``MLPMK_DOUT_SCALAR``, no copy).
     With ``workspace`` (default) the weight-gradient partials of the
     workgroups go through a workspace from torch's allocator and a second
     kernel (``mlpmk_bwd_ws``); otherwise every workgroup adds its partials

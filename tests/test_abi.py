@@ -110,7 +110,7 @@ def test_bwd_validation_codes():
         3, pd, kw.get("dtype", 1), kw.get("x", A), pw, kw.get("stash", ps), kw.get("dout", A), kw.get("stride", 128),
         kw.get("dx", None), kw.get("dw", pg), kw.get("m", 256), None)
     assert call(m=-1) == INVALID
-    assert call(stride=-1) == INVALID
+    assert call(stride=-2) == INVALID  # negative, and not MLPMK_DOUT_SCALAR
     assert call(dw=None) == INVALID
     assert call(dtype=0) == UNSUPPORTED
     assert call(dtype=3) == INVALID
@@ -119,6 +119,9 @@ def test_bwd_validation_codes():
         assert call(stride=130) == MISALIGNED
         assert call(dout=A + 4) == MISALIGNED
         assert call(m=0) == OK
+        # MLPMK_DOUT_SCALAR: one element, 2-byte aligned, any output width
+        assert call(stride=-1, dout=A + 1) == MISALIGNED
+        assert call(stride=-1, dout=A + 2, m=0) == OK
     else:
         assert call() == UNSUPPORTED
 

@@ -49,6 +49,9 @@ def run_train(dims, m, seed, *, dout_mode="ones", with_dx=True, x_dist="normal",
         row = rng.standard_normal(dims[-1]).astype(np.float16)
         dout_np = np.broadcast_to(row, (m, dims[-1]))
         dout = torch.from_numpy(row).cuda().reshape(1, -1).expand(m, dims[-1])
+    elif dout_mode == "scalar":  # one element expanded everywhere, as loss = out.sum() hands back
+        dout_np = np.full((m, dims[-1]), 0.75, np.float16)
+        dout = torch.full((), 0.75, dtype=torch.float16, device="cuda").expand(m, dims[-1])
     else:
         dout_np = rng.standard_normal((m, dims[-1])).astype(np.float16)
         dout = torch.from_numpy(dout_np).cuda()
@@ -272,3 +275,34 @@ def test_saturated_units_weight_gradients(m):
     # and the matrix as a whole, as everywhere else
     for i in range(3):
         check_dw(dws[i].cpu().numpy(), rdws[i], f"saturated net dW{i + 1}")
+
+
+# MLPMK_DOUT_SCALAR: the backward reads one element for every row and column.
+# Against the oracle, and against the same value materialised as a broadcast
+# row (bit for bit where the partials go through the workspace and the
+# combine's fixed order; the atomic flush of small grids sums in any order).
+@pytest.mark.parametrize("dims,m,with_dx", [(D3, 131072 + 5, False), (D3, 4096, True), (D5, 65536, False),
+                                            (NARROW, 100000, True), ((48, 96, 80, 10), 3000, True)])
+def test_scalar_dout_matches_oracle_and_broadcast_row(dims, m, with_dx):
+    run_train(dims, m, 23, dout_mode="scalar", with_dx=with_dx)
+    x, ws = orc.make_inputs(dims, m, seed=23)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    c = torch.full((), 0.75, dtype=torch.float16, device="cuda")
+    douts = [c.expand(m, dims[-1]), c.reshape(1, 1).expand(1, dims[-1]).contiguous().expand(m, dims[-1])]
+    res = []
+    for dout in douts:
+        dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(len(dims) - 1)]
+        dx = torch.empty_like(xd) if with_dx else None
+        ops.bwd(xd, wd, hs, dout, dws, dx)
+        res.append((dws, dx))
+    (da, xa), (db, xb) = res
+    deterministic = -(-m // 128) >= 128  # 128-row rounds: grids well above the 64-workgroup atomic cut
+    for i, (a, b) in enumerate(zip(da, db)):
+        if deterministic:
+            assert torch.equal(a, b), f"dW{i + 1}"
+        else:
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-6 * float(b.abs().max())), f"dW{i + 1}"
+    if with_dx:
+        assert torch.equal(xa, xb)

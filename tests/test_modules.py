@@ -52,11 +52,18 @@ def test_weight_norm_blocks_are_contiguous_views():
     assert [m.v_all.data_ptr() + 4 * o for o in woff] == [v.data_ptr() for v in views]
 
 
-def test_sum_gradient_becomes_one_broadcast_row():
-    g = torch.ones((), dtype=torch.float16).expand(5, 7)  # what out.sum() hands back
+def test_sum_gradient_stays_one_element():
+    # What out.sum() hands back stays as it is (the kernels read its one
+    # element, MLPMK_DOUT_SCALAR); ops._dout_rows tags it so.
+    from mlpmk import ops
+
+    g = torch.ones((), dtype=torch.float16).expand(5, 7)
     assert g.stride() == (0, 0)
     r = _as_row_broadcast(g)
-    assert r.shape == (5, 7) and r.stride() == (0, 1) and torch.all(r == 1)
+    assert r is g
+    d, st = ops._dout_rows(r, 5, 7, torch.float16, r.device)
+    assert d is r and st == ops.DOUT_SCALAR
+    assert ops.DOUT_SCALAR == -1
     row = torch.randn(1, 7).half().expand(5, 7)
     assert _as_row_broadcast(row).stride() == (0, 1)
     dense = torch.randn(7, 5).half().t()
