@@ -132,48 +132,108 @@ def _launch(device, fn, *args):
 # Pointer-level launches.  The public wrappers below validate tensors and call
 # these; the autograd Functions call them directly for buffers they allocated
 # themselves (shapes known), which keeps a training step's host time down.
-# ``dims`` is a tuple of ints; pointers are ints (None for NULL).
-def _fwd_raw(dev, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M):
+# ``dims`` is a tuple of ints; pointers are ints (None for NULL).  They go
+# through the CPython shims of ``_mlpmk_launch`` (csrc/pylaunch.c, bound to
+# the entry points of the library ctypes loaded) when that module is built,
+# else through ctypes.
+try:
+    from . import _mlpmk_launch as _shim
+except ImportError:  # not built: ctypes only
+    _shim = None
+_shim_lib = None  # the ctypes library whose entry points the shim is bound to
+
+
+def _fast():
+    """The shim module bound to the current library, or None."""
+    global _shim_lib
     lib = _lib.get()
-    L = len(dims) - 1
-    pw = (_lib.c_void_p * L)(*w_ptrs)
-    ps = None if stash_ptrs is None else (_lib.c_void_p * (L - 1))(*stash_ptrs)
-    rc = _launch(dev, lib.mlpmk_fwd, L, _lib.dims_array(dims), code, x_ptr, pw, out_ptr, ps, M)
+    if _shim is None:
+        return None
+    if _shim_lib is not lib:
+        addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
+        _shim.bind(addr(lib.mlpmk_fwd), addr(lib.mlpmk_bwd), addr(lib.mlpmk_bwd_ws), addr(lib.mlpmk_wn_fwd),
+                   addr(lib.mlpmk_wn_bwd))
+        _shim_lib = lib
+    return _shim
+
+
+def _stream_of(dev):
+    """``(device index, raw stream)`` for a launch on ``dev`` from the current
+    device, or None when the device must be switched first."""
+    cur = _cur_device()
+    idx = dev.index
+    if idx is not None and idx != cur:
+        return None
+    return _raw_stream(cur) if _raw_stream is not None else torch.cuda.current_stream(cur).cuda_stream
+
+
+def _shim_launch(dev, fn, *args):
+    st = _stream_of(dev)
+    if st is not None:
+        return fn(*args, st)
+    with torch.cuda.device(dev.index):
+        return fn(*args, _stream_of(dev))
+
+
+def _fwd_raw(dev, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M):
+    f = _fast()
+    if f is not None:
+        rc = _shim_launch(dev, f.fwd, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M)
+    else:
+        lib = _lib.get()
+        L = len(dims) - 1
+        pw = (_lib.c_void_p * L)(*w_ptrs)
+        ps = None if stash_ptrs is None else (_lib.c_void_p * (L - 1))(*stash_ptrs)
+        rc = _launch(dev, lib.mlpmk_fwd, L, _lib.dims_array(dims), code, x_ptr, pw, out_ptr, ps, M)
     if rc:
         _check("mlpmk_fwd", rc)
 
 
 def _bwd_raw(dev, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, dx_ptr, dw_ptrs, M, workspace=True):
-    lib = _lib.get()
-    L = len(dims) - 1
-    pd = _lib.dims_array(dims)
-    pw = (_lib.c_void_p * L)(*w_ptrs)
-    ps = (_lib.c_void_p * (L - 1))(*stash_ptrs)
-    pg = (_lib.c_void_p * L)(*dw_ptrs)
+    ws, nbytes = None, 0
     if workspace and M > 0:
         nbytes = _workspace_bytes(dev.index if dev.index is not None else _cur_device(), dims, M, dx_ptr is not None,
                                   code)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        rc = _launch(dev, lib.mlpmk_bwd_ws, L, pd, code, x_ptr, pw, ps, dout_ptr, row_stride, dx_ptr, pg,
-                     ws.data_ptr(), nbytes, M)
-        if rc:
-            _check("mlpmk_bwd_ws", rc)
+    name = "mlpmk_bwd_ws" if ws is not None else "mlpmk_bwd"
+    f = _fast()
+    if f is not None:
+        rc = _shim_launch(dev, f.bwd, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, dx_ptr, dw_ptrs,
+                          ws.data_ptr() if ws is not None else None, nbytes, M)
     else:
-        rc = _launch(dev, lib.mlpmk_bwd, L, pd, code, x_ptr, pw, ps, dout_ptr, row_stride, dx_ptr, pg, M)
-        if rc:
-            _check("mlpmk_bwd", rc)
+        lib = _lib.get()
+        L = len(dims) - 1
+        pd = _lib.dims_array(dims)
+        pw = (_lib.c_void_p * L)(*w_ptrs)
+        ps = (_lib.c_void_p * (L - 1))(*stash_ptrs)
+        pg = (_lib.c_void_p * L)(*dw_ptrs)
+        if ws is not None:
+            rc = _launch(dev, lib.mlpmk_bwd_ws, L, pd, code, x_ptr, pw, ps, dout_ptr, row_stride, dx_ptr, pg,
+                         ws.data_ptr(), nbytes, M)
+        else:
+            rc = _launch(dev, lib.mlpmk_bwd, L, pd, code, x_ptr, pw, ps, dout_ptr, row_stride, dx_ptr, pg, M)
+    if rc:
+        _check(name, rc)
 
 
 def _wn_fwd_raw(dev, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr):
-    rc = _launch(dev, _lib.get().mlpmk_wn_fwd, len(dims) - 1, _lib.dims_array(dims), pcode, wcode, v_ptr, g_ptr, w_ptr,
-                 inv_ptr)
+    f = _fast()
+    if f is not None:
+        rc = _shim_launch(dev, f.wn_fwd, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr)
+    else:
+        rc = _launch(dev, _lib.get().mlpmk_wn_fwd, len(dims) - 1, _lib.dims_array(dims), pcode, wcode, v_ptr, g_ptr,
+                     w_ptr, inv_ptr)
     if rc:
         _check("mlpmk_wn_fwd", rc)
 
 
 def _wn_bwd_raw(dev, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr):
-    rc = _launch(dev, _lib.get().mlpmk_wn_bwd, len(dims) - 1, _lib.dims_array(dims), pcode, dw_ptr, v_ptr, g_ptr,
-                 inv_ptr, dv_ptr, dg_ptr)
+    f = _fast()
+    if f is not None:
+        rc = _shim_launch(dev, f.wn_bwd, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr)
+    else:
+        rc = _launch(dev, _lib.get().mlpmk_wn_bwd, len(dims) - 1, _lib.dims_array(dims), pcode, dw_ptr, v_ptr, g_ptr,
+                     inv_ptr, dv_ptr, dg_ptr)
     if rc:
         _check("mlpmk_wn_bwd", rc)
 

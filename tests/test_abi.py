@@ -235,3 +235,25 @@ def test_model_reference_matches_oracle_on_cpu():
     x, ws = orc.make_inputs((128, 128, 128, 128), 64, seed=0)
     got = kernel.Model()(*[torch.from_numpy(a.astype(np.float32)) for a in [x] + ws]).numpy()
     np.testing.assert_allclose(got, orc.forward(x, ws), rtol=1e-4, atol=1e-5)
+
+
+def test_launch_shim_converts_arguments_like_ctypes():
+    # The CPython shims (csrc/pylaunch.c) call the entry points of the library
+    # ctypes loaded; argument validation answers exactly as through ctypes.
+    shim = ops._fast()
+    if shim is None:
+        pytest.skip("the _mlpmk_launch module is not built")
+    d = (128, 128, 128, 128)
+    w, dw, st = (A, A, A), (A, A, A), (A, A)
+    assert shim.fwd(d, 99, A, w, A, None, 256, None) == INVALID  # bad dtype
+    assert shim.fwd(d, 1, A, w, A, None, -1, None) == INVALID  # negative M
+    assert shim.bwd(d, 1, A, w, st, A, -2, None, dw, None, 0, 256, None) == INVALID  # bad dout stride
+    assert shim.bwd(d, 1, A, w, st, A + 1, -1, None, dw, None, 0, 256, None) == MISALIGNED
+    if ops.bwd_supported(list(d)):
+        assert shim.bwd(d, 1, A, w, st, A, 128, None, dw, None, 0, 0, None) == OK  # M = 0: nothing to do
+    with pytest.raises(ValueError):
+        shim.fwd(d, 1, A, (A, A), A, None, 256, None)  # one weight short
+    with pytest.raises(TypeError):
+        shim.fwd(list(d), 1, A, w, A, None, 256, None)  # dims must be a tuple
+    with pytest.raises(TypeError):
+        shim.fwd(d, 1, A, w, A, None, 256)  # stream missing
