@@ -574,6 +574,9 @@ def main():
     ap.add_argument("--train-step", type=int, default=None, metavar="M",
                     help="counter-collection runs of the training kernels: only the WN training step at M rows "
                          "(3 layers; 5 with --config 5l128; no headline, no other legs); prints its timing JSON")
+    ap.add_argument("--sweep", action="store_true",
+                    help="only the small-batch latency sweep of --config (M = 64 .. 4096; kernel-trace runs); "
+                         "prints its JSON")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -592,6 +595,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+
+    if args.sweep:
+        with gc_paused():
+            print(json.dumps({"latency_sweep": latency_sweep(torch, ops, CONFIG_DIMS[args.config]),
+                              "config": args.config}))
+        return
 
     if args.train_step:
         n_layers = 5 if args.config == "5l128" else 3
