@@ -107,26 +107,25 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _cur_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
-def _stream(device):
-    """Handle of the current torch stream of ``device`` (the raw query costs
-    ~0.1 us per call against ~3 us for ``current_stream().cuda_stream``)."""
-    if _raw_stream is not None:
-        return _raw_stream(device.index if device.index is not None else _cur_device())
-    return torch.cuda.current_stream(device).cuda_stream
-
-
-def _launch(device, fn, *args):
-    """``fn(*args, stream)`` with ``device`` current: the library launches on
-    the calling thread's current HIP device.  Switches only when needed (the
-    device context manager costs ~2.4 us per call)."""
+def _stream_of(dev):
+    """The raw current stream of ``dev`` when ``dev`` is the current device
+    (or names none), else None: the caller switches first.  The raw queries
+    cost ~0.1 us against ~3 us for ``current_stream().cuda_stream``."""
     cur = _cur_device()
-    idx = device.index
-    if idx is None or idx == cur:
-        if _raw_stream is not None:
-            return fn(*args, _raw_stream(cur))
-        return fn(*args, torch.cuda.current_stream(cur).cuda_stream)
-    with torch.cuda.device(idx):
-        return fn(*args, _stream(device))
+    if dev.index is not None and dev.index != cur:
+        return None
+    return _raw_stream(cur) if _raw_stream is not None else torch.cuda.current_stream(cur).cuda_stream
+
+
+def _launch(dev, fn, *args):
+    """``fn(*args, stream)`` with ``dev`` current: the library launches on the
+    calling thread's current HIP device.  Switches only when needed (the
+    device context manager costs ~2.4 us per call)."""
+    st = _stream_of(dev)
+    if st is not None:
+        return fn(*args, st)
+    with torch.cuda.device(dev.index):
+        return fn(*args, _stream_of(dev))
 
 
 # Pointer-level launches.  The public wrappers below validate tensors and call
@@ -157,28 +156,10 @@ def _fast():
     return _shim
 
 
-def _stream_of(dev):
-    """``(device index, raw stream)`` for a launch on ``dev`` from the current
-    device, or None when the device must be switched first."""
-    cur = _cur_device()
-    idx = dev.index
-    if idx is not None and idx != cur:
-        return None
-    return _raw_stream(cur) if _raw_stream is not None else torch.cuda.current_stream(cur).cuda_stream
-
-
-def _shim_launch(dev, fn, *args):
-    st = _stream_of(dev)
-    if st is not None:
-        return fn(*args, st)
-    with torch.cuda.device(dev.index):
-        return fn(*args, _stream_of(dev))
-
-
 def _fwd_raw(dev, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M):
     f = _fast()
     if f is not None:
-        rc = _shim_launch(dev, f.fwd, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M)
+        rc = _launch(dev, f.fwd, dims, code, x_ptr, w_ptrs, out_ptr, stash_ptrs, M)
     else:
         lib = _lib.get()
         L = len(dims) - 1
@@ -198,7 +179,7 @@ def _bwd_raw(dev, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, d
     name = "mlpmk_bwd_ws" if ws is not None else "mlpmk_bwd"
     f = _fast()
     if f is not None:
-        rc = _shim_launch(dev, f.bwd, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, dx_ptr, dw_ptrs,
+        rc = _launch(dev, f.bwd, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, dx_ptr, dw_ptrs,
                           ws.data_ptr() if ws is not None else None, nbytes, M)
     else:
         lib = _lib.get()
@@ -219,7 +200,7 @@ def _bwd_raw(dev, dims, code, x_ptr, w_ptrs, stash_ptrs, dout_ptr, row_stride, d
 def _wn_fwd_raw(dev, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr):
     f = _fast()
     if f is not None:
-        rc = _shim_launch(dev, f.wn_fwd, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr)
+        rc = _launch(dev, f.wn_fwd, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr)
     else:
         rc = _launch(dev, _lib.get().mlpmk_wn_fwd, len(dims) - 1, _lib.dims_array(dims), pcode, wcode, v_ptr, g_ptr,
                      w_ptr, inv_ptr)
@@ -230,7 +211,7 @@ def _wn_fwd_raw(dev, dims, pcode, wcode, v_ptr, g_ptr, w_ptr, inv_ptr):
 def _wn_bwd_raw(dev, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr):
     f = _fast()
     if f is not None:
-        rc = _shim_launch(dev, f.wn_bwd, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr)
+        rc = _launch(dev, f.wn_bwd, dims, pcode, dw_ptr, v_ptr, g_ptr, inv_ptr, dv_ptr, dg_ptr)
     else:
         rc = _launch(dev, _lib.get().mlpmk_wn_bwd, len(dims) - 1, _lib.dims_array(dims), pcode, dw_ptr, v_ptr, g_ptr,
                      inv_ptr, dv_ptr, dg_ptr)
