@@ -54,7 +54,7 @@ enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1, MLPMK_DTYPE_BF16 = 2 };
  * value everywhere (the gradient of loss = out.sum(), possibly scaled): dout
  * then points at that single element (2-byte aligned).  No counterpart in the
  * reference, whose launcher receives the expanded tensor; it spares callers
- * the copy that would materialise a broadcast row. */
+ * the copy that would materialise a broadcast row.  Since ABI version 201. */
 enum { MLPMK_DOUT_SCALAR = -1 };
 
 /* Library ABI version (major * 100 + minor). */

@@ -115,7 +115,7 @@ using namespace mlpmk;
 
 extern "C" {
 
-int mlpmk_version(void) { return 200; }
+int mlpmk_version(void) { return 201; }  // 2.01: MLPMK_DOUT_SCALAR
 
 const char* mlpmk_status_string(int status) {
   switch (status) {
