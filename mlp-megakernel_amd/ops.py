@@ -231,7 +231,7 @@ def _dout_rows(dout, M, out_w, dtype, dev):
         raise TypeError(f"dout must be {dtype} on the same device as x")
     if tuple(dout.shape) != (M, out_w):
         raise ValueError(f"dout must be [M, OUT]={M, out_w}")
-    if M > 0 and dout.stride() == (0, 0):
+    if dout.stride() == (0, 0):  # (M = 0 too: the library then reads nothing)
         return dout, DOUT_SCALAR
     if dout.stride(1) != 1:
         raise ValueError(f"dout must be [M, OUT]={M, out_w} with unit column stride")

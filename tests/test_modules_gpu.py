@@ -323,3 +323,22 @@ def test_five_layer_wn_module(m):
         check_grad(model.v_all.grad[nw:nw + k * n].cpu().numpy(), ref_dv[nw:nw + k * n], f"dv{i + 1}")
         nw += k * n
     check_grad(model.g_all.grad.cpu().numpy(), ref_dg, "dg")
+
+
+@pytest.mark.parametrize("wn", [False, True])
+def test_empty_batch_trains_to_zero_gradients(wn):
+    # M = 0: the forward returns [0, OUT], and out.sum().backward() (whose
+    # gradient is one element expanded over nothing) gives zero weight
+    # gradients through the fused backward.
+    torch.manual_seed(5)
+    cls = fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus
+    model = cls().cuda()
+    x = torch.randn(0, 128, device="cuda").half()
+    out = model(x)
+    assert tuple(out.shape) == (0, 128) and out.dtype == torch.float16
+    out.sum().backward()
+    for p_ in model.parameters():
+        assert p_.grad is not None and p_.grad.shape == p_.shape
+        assert torch.count_nonzero(p_.grad) == 0
+    with torch.no_grad():
+        assert tuple(model(x).shape) == (0, 128)
