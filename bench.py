@@ -16,7 +16,9 @@ M = 64..4096 latency sweep (event timing, one-launch and 20-launch graph
 replays, and the replay floor of a one-workgroup kernel), and the
 weight-norm training step at M = 4096 / 16384 / 131072.  ``cpu_baseline`` is
 the reference's eager PyTorch path (kernel.py:163-171) in fp32 on the host
-cores; the numpy oracle's time is reported beside it.
+cores over the workload itself (all M rows of the seed-0 inputs the GPU
+reads; median of at least 3 passes); the numpy oracle's time is reported
+beside it.
 
 Prints ONE JSON line (the driver's contract).  ``--config`` / ``--m`` move the
 headline to another config, ``--no-extra`` skips the extra configs (for
@@ -157,6 +159,28 @@ def time_graph(torch, fn, iters=100, warmup=20, per_graph=1):
     return ts[len(ts) // 2]
 
 
+def time_per_call(torch, fn, warmup=50, iters=100):
+    """Median ms of one call: an event pair recorded around each call, then a
+    synchronisation, after `warmup` calls -- the reference's
+    ``benchmark_fn`` (/root/reference/profile.py:28-47), which its "non-graph
+    incl. launch" tables use.  Host dispatch and the allocation of the
+    output are inside the pair."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    ts = []
+    for _ in range(iters):
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def cpu_threads():
     try:
         from threadpoolctl import threadpool_info
@@ -189,45 +213,55 @@ def host_threads():
     return max(n, 1)
 
 
-def cpu_oracle_numpy(orc, dims, uniform, budget_s=5.0, chunk=65536):
-    """The numpy oracle's forward (fp32, BLAS matmuls) on host cores over a
-    bounded sample: repeated `chunk`-row batches until `budget_s` has elapsed."""
-    x, ws = orc.make_inputs(dims, chunk, seed=7, x_dist="uniform" if uniform else "normal")
-    orc.forward(x[:1024], ws)  # warm the BLAS threads
-    rows = 0
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        orc.forward(x, ws)
-        rows += chunk
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s and reps >= 2:
+def _median_runs(fn, runs, budget_s):
+    """Wall-clock seconds of `runs` calls of `fn` (after one untimed call),
+    stopping early once `budget_s` has elapsed with at least 3 runs done;
+    returns (median, list of run times)."""
+    fn()
+    ts = []
+    t_all = time.perf_counter()
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        if len(ts) >= 3 and time.perf_counter() - t_all >= budget_s:
             break
+    srt = sorted(ts)
+    return srt[len(srt) // 2], ts
+
+
+def cpu_oracle_numpy(orc, x, ws, runs=3, budget_s=10.0):
+    """The numpy oracle's forward (fp32, BLAS matmuls) on the host over the
+    workload's own inputs (the same seeded fp16 values the GPU reads):
+    median of `runs` full passes."""
+    threads = cpu_threads()
+    med, ts = _median_runs(lambda: orc.forward(x, ws), runs, budget_s)
+    m = x.shape[0]
     return {
-        "value": rows / el,
+        "value": m / med,
         "unit": "rows/s",
-        "cores": cpu_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": f"numpy oracle fp32 forward, {reps} x {chunk} rows of the same config in {el:.1f} s "
-        f"(BLAS matmuls threaded, softplus single-threaded numpy)",
+        "sample": f"numpy oracle fp32 forward over all {m} rows of the workload's seed-0 inputs, median of "
+        f"{len(ts)} runs ({', '.join(f'{t:.3f}' for t in ts)} s; BLAS matmuls threaded, softplus "
+        f"single-threaded numpy)",
     }
 
 
-def cpu_eager_baseline(torch, dims, uniform, budget_s=10.0, chunk=65536):
+def cpu_eager_baseline(torch, x_dev, ws_dev, runs=5, budget_s=20.0):
     """The reference's eager path on the host: ``Model.forward``
     (kernel.py:163-171, softplus(x @ w1) -> softplus(. @ w2) -> . @ w3) in
-    PyTorch fp32 on the CPU, over repeated `chunk`-row batches of the
-    workload's shape until `budget_s` has elapsed."""
+    PyTorch fp32 on the CPU, over the workload itself -- all M rows of the
+    same seed-0 inputs the GPU launch reads, upcast to fp32 -- as the median
+    of `runs` full passes (at least 3)."""
     import kernel
 
     threads = host_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        g = torch.Generator().manual_seed(11)
-        x = (torch.rand((chunk, dims[0]), generator=g) * 2 - 1) if uniform else torch.randn((chunk, dims[0]), generator=g)
-        ws = [torch.randn((dims[i], dims[i + 1]), generator=g) / dims[i] ** 0.5 for i in range(len(dims) - 1)]
+        x = x_dev.float().cpu()
+        ws = [w.float().cpu() for w in ws_dev]
         F = torch.nn.functional
         model = kernel.Model()
 
@@ -242,25 +276,19 @@ def cpu_eager_baseline(torch, dims, uniform, budget_s=10.0, chunk=65536):
             return a
 
         with torch.no_grad():
-            run()
-            rows, reps, t0 = 0, 0, time.perf_counter()
-            while True:
-                run()
-                rows += chunk
-                reps += 1
-                el = time.perf_counter() - t0
-                if el >= budget_s and reps >= 2:
-                    break
+            med, ts = _median_runs(run, runs, budget_s)
     finally:
         torch.set_num_threads(prev)
+    m = x.shape[0]
     return {
-        "value": rows / el,
+        "value": m / med,
         "unit": "rows/s",
         "cores": threads,
         "kind": "reference",
         "cpu": cpu_model_name(),
         "sample": f"the reference's eager Model.forward (kernel.py:163-171) in PyTorch fp32 on {threads} host "
-        f"threads, {reps} x {chunk} rows of the same widths in {el:.1f} s",
+        f"threads over all {m} rows of the workload's seed-0 inputs (upcast from fp16), median of {len(ts)} "
+        f"runs ({', '.join(f'{t:.3f}' for t in ts)} s)",
     }
 
 
@@ -309,11 +337,16 @@ def fwd_bench(torch, ops, dims, m, uniform, steps=200, warmup=20, dtype=None):
 def latency_sweep(torch, ops, dims, sizes=(64, 128, 256, 512, 1024, 2048, 4096)):
     """BASELINE configs[1]'s latency sweep: per M, HIP-event time of 200
     back-to-back launches (host dispatch included), the median of one-launch
-    graph replays (/root/reference/profile.py:50-80), and 20-launch graph
-    replays (launch latency shared); plus the replay floor of a one-workgroup
-    kernel (a 16-byte copy) under the same two replay methods.  Buffers are
+    graph replays (/root/reference/profile.py:50-80), 20-launch graph replays
+    (launch latency shared), and the median per-call time of
+    ``kernel._fused_mlp_fwd`` (``.contiguous()``, output allocation and
+    launch inside an event pair, synchronised per call:
+    /root/reference/profile.py:28-47); plus the replay floor of a
+    one-workgroup kernel (a 16-byte copy) under the two replay methods.  Buffers are
     L2/MALL-resident at these sizes (at most 2 MiB): the figures are
     launch-latency-bound, not bandwidth measurements."""
+    import kernel
+
     res = {}
     for m in sizes:
         x, ws = make_device_inputs(torch, dims, m, seed=0, uniform=False)
@@ -323,7 +356,11 @@ def latency_sweep(torch, ops, dims, sizes=(64, 128, 256, 512, 1024, 2048, 4096))
             ev = time_launches(torch, fn, 200, 20)
             g1 = time_graph(torch, fn)
             g20 = time_graph(torch, fn, iters=50, per_graph=20)
+            call = None
+            if len(ws) == 3:  # the drop-in launcher as a reference user calls it
+                call = time_per_call(torch, lambda: kernel._fused_mlp_fwd(x, *ws))
         res[str(m)] = {"event_ms": round(ev, 5), "graph1_ms": round(g1, 5), "graph20_ms_per_launch": round(g20, 5),
+                       "per_call_ms": None if call is None else round(call, 5),
                        "rows_per_s": round(m / (min(ev, g1, g20) * 1e-3), 1),
                        "kernel": ops.fwd_launch_info(dims, m)["kernel"]}
     src = torch.zeros(16, dtype=torch.uint8, device="cuda")
@@ -343,56 +380,6 @@ def sustained(torch, step, ms_hint, seconds=0.6):
     with gc_paused():
         ms = time_launches(torch, step, n, 0)
     return ms, n
-
-
-def timeline_leg(torch, step, m, rows_per_block=32):
-    """Per-XCD view of one persistent launch, from a library built with
-    per-wave timestamps (``make timeline`` -> libmlpmk_timeline.so, loaded
-    through MLPMK_LIBRARY): after ~0.3 s of back-to-back launches, one more
-    launch is recorded.  Per XCD: mean shader clock over the waves' spans
-    (s_memtime cycles / s_memrealtime ticks), when its first and last wave
-    finished and how long the weight staging took, relative to the first
-    wave's start."""
-    import ctypes
-
-    from mlpmk import _lib
-    lib = _lib.get()
-    if not hasattr(lib, "mlpmk_fwd_timeline"):
-        raise SystemExit("bench.py --timeline: the loaded library has no timestamps; build `make -C "
-                         "mlp-megakernel_amd/csrc timeline` and set MLPMK_LIBRARY=mlp-megakernel_amd/libmlpmk_timeline.so")
-    words = 4096 * 8
-    buf = np.zeros(words, np.uint64)
-    fn = lib.mlpmk_fwd_timeline
-    fn.restype, fn.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
-    with gc_paused():
-        ramp_clock(torch, step, 0.3)
-        if fn(buf.ctypes.data, buf.nbytes) != 0:  # clears the records
-            raise SystemExit("mlpmk_fwd_timeline failed")
-        step(0)
-        torch.cuda.synchronize()
-    if fn(buf.ctypes.data, buf.nbytes) != 0:
-        raise SystemExit("mlpmk_fwd_timeline failed")
-    r = buf.reshape(-1, 8)
-    r = r[r[:, 7] == 1].astype(np.float64)
-    t0 = r[:, 0].min()
-    start, staged, end, cyc = r[:, 0] - t0, r[:, 1] - t0, r[:, 2] - t0, r[:, 3]
-    xcc = r[:, 4].astype(int)
-    mhz = 100.0 * cyc / np.maximum(r[:, 2] - r[:, 0], 1)
-    out = {"waves": int(len(r)), "blocks": int(r[:, 6].sum()), "rows": m,
-           "kernel_us": round(end.max() / 100.0, 2), "xcd": {}}
-    for x in sorted(set(xcc)):
-        k = xcc == x
-        out["xcd"][str(x)] = {
-            "waves": int(k.sum()),
-            "blocks": int(r[k, 6].sum()),
-            "mhz": round(float(mhz[k].mean()), 0),
-            "staging_us": round(float((staged[k] - start[k]).mean()) / 100.0, 2),
-            "first_finish_us": round(float(end[k].min()) / 100.0, 2),
-            "last_finish_us": round(float(end[k].max()) / 100.0, 2),
-        }
-    out["mhz_mean"] = round(float(mhz.mean()), 0)
-    out["finish_spread_us"] = round(float(end.max() - end.min()) / 100.0, 2)
-    return out
 
 
 def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, dtype=None):
@@ -565,12 +552,11 @@ def main():
                     help="add the longer training experiments (5-layer step, bf16, stash vs recompute, "
                          "the reference's PyTorch-op backward)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0,
+                    help="seconds after which the CPU legs stop repeating (each still runs at least 3 passes)")
     ap.add_argument("--quick", action="store_true",
                     help="counter-collection runs: parity gate, warm-up and the timed launches only (no clock ramp, "
                          "sustained run, bf16 figure or copy reference)")
-    ap.add_argument("--timeline", action="store_true",
-                    help="per-XCD clock and finish times of one launch (needs libmlpmk_timeline.so via MLPMK_LIBRARY)")
     ap.add_argument("--train-step", type=int, default=None, metavar="M",
                     help="counter-collection runs of the training kernels: only the WN training step at M rows "
                          "(3 layers; 5 with --config 5l128; no headline, no other legs); prints its timing JSON")
@@ -728,8 +714,6 @@ def main():
     }
     if os.environ.get("MLPMK_LIBRARY"):
         result["library"] = os.path.basename(os.environ["MLPMK_LIBRARY"])
-    if args.timeline:
-        result["timeline"] = timeline_leg(torch, step, m)
 
     if not args.no_extra:
         # The other BASELINE configs, each timed here too.
@@ -761,8 +745,9 @@ def main():
                                                   for mt in (4096, 32768, 131072, 1048576)}
 
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_eager_baseline(torch, dims, uniform, budget_s=args.cpu_budget)
-        result["cpu_oracle_numpy"] = cpu_oracle_numpy(orc, dims, uniform, budget_s=args.cpu_budget / 2)
+        result["cpu_baseline"] = cpu_eager_baseline(torch, x0, ws, budget_s=args.cpu_budget)
+        result["cpu_oracle_numpy"] = cpu_oracle_numpy(orc, x0.cpu().numpy(), [w.cpu().numpy() for w in ws],
+                                                      budget_s=args.cpu_budget / 2)
     else:
         result["cpu_baseline"] = None
 

@@ -5,8 +5,7 @@ on machines without the built library; any call then raises ``OSError``
 naming the missing file.  There is no fallback implementation.
 
 ``MLPMK_LIBRARY`` (environment) names another build of the same ABI to load
-instead, e.g. ``libmlpmk_sp2.so`` (``make forms``: the forward built with
-another softplus evaluation, for measurement).
+instead (a build with other compile-time options, for measurement).
 """
 import ctypes
 import os

@@ -1038,25 +1038,9 @@ struct BwdWave {
   }
 };
 
-#ifdef MLPMK_BWD_TIMELINE
-// Measurement build only (make timeline -> libmlpmk_timeline.so): every wave
-// records, in 100 MHz ticks (s_memrealtime), when it started, when the weight
-// staging barrier released it, when its first round ended, when its last
-// round ended (the weight-gradient flush is issued within that round) and
-// when it left the kernel, then its
-// shader-clock cycles over the whole span (s_memtime), XCD and CU ids and its
-// round count.  mlpmk_bwd_timeline copies the records out.
-constexpr int kBwdTimelineWaves = 4096;
-__device__ unsigned long long g_bwd_timeline[kBwdTimelineWaves * 8];
-#endif
 
 template <class N, int NW, bool DX, bool SEG>
 __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
-#ifdef MLPMK_BWD_TIMELINE
-  const unsigned long long tl_t0 = __builtin_amdgcn_s_memrealtime(), tl_c0 = __builtin_amdgcn_s_memtime();
-  unsigned long long tl_t1 = 0, tl_t2 = 0, tl_t3 = 0;
-  unsigned int tl_nr = 0;
-#endif
   using Gm = BwdGeom<N, NW, DX, SEG>;
   static_assert(Gm::valid(), "unsupported backward shape");
   constexpr int R = Gm::R;
@@ -1093,36 +1077,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_kernel(BwdParams p) {
     dgrad_store_all<N, Gm, NW * 64>(sv, wfr);
   }
   __syncthreads();
-#ifdef MLPMK_BWD_TIMELINE
-  tl_t1 = __builtin_amdgcn_s_memrealtime();
-#endif
   for (int64_t rnd = blockIdx.x; rnd < nrounds; rnd += gridDim.x) {
     wv.round();
     wv.row0 += wv.rstep;
-#ifdef MLPMK_BWD_TIMELINE
-    if (tl_nr++ == 0) tl_t2 = __builtin_amdgcn_s_memrealtime();
-#endif
   }
-#ifdef MLPMK_BWD_TIMELINE
-  tl_t3 = __builtin_amdgcn_s_memrealtime();
-#endif
   wv.template flush_all<0>();
-#ifdef MLPMK_BWD_TIMELINE
-  const unsigned long long tl_t4 = __builtin_amdgcn_s_memrealtime(), tl_c4 = __builtin_amdgcn_s_memtime();
-  const int tl_w = (int)blockIdx.x * NW + wid;
-  if (lane == 0 && tl_w < kBwdTimelineWaves) {
-    unsigned long long* r = g_bwd_timeline + tl_w * 8;
-    r[0] = tl_t0;
-    r[1] = tl_t1;
-    r[2] = tl_t2;
-    r[3] = tl_t3;
-    r[4] = tl_t4;
-    r[5] = tl_c4 - tl_c0;
-    r[6] = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) |               // XCC_ID
-           ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4) << 8);  // HW_ID
-    r[7] = tl_nr;
-  }
-#endif
 }
 
 // Sums the per-workgroup weight-gradient partials into dw.  A workgroup owns
@@ -1172,19 +1131,6 @@ __global__ __launch_bounds__(kCombineCols* kCombineGroups) void bwd_combine_kern
 // Host dispatch
 // ---------------------------------------------------------------------------
 
-#ifdef MLPMK_BWD_TIMELINE
-}  // namespace mlpmk
-// Copies the records of the last backward launch (8 x 64-bit words per wave,
-// kBwdTimelineWaves waves) to dst and clears them.  Measurement build only.
-extern "C" int mlpmk_bwd_timeline(void* dst, int64_t bytes) {
-  if (bytes < (int64_t)sizeof(mlpmk::g_bwd_timeline)) return -1;
-  if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(mlpmk::g_bwd_timeline), sizeof(mlpmk::g_bwd_timeline)) != hipSuccess)
-    return -2;
-  static unsigned long long zeros[mlpmk::kBwdTimelineWaves * 8];
-  return hipMemcpyToSymbol(HIP_SYMBOL(mlpmk::g_bwd_timeline), zeros, sizeof(zeros)) == hipSuccess ? 0 : -3;
-}
-namespace mlpmk {
-#endif
 
 typedef Net<128, 128, 128, 128> BNet3L128;
 typedef Net<128, 128, 128, 128, 128, 128> BNet5L128;

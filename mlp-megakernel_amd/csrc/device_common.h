@@ -120,50 +120,13 @@ __host__ __device__ constexpr int outfeat(int mb, int i) {
 // sp2_overflow and then substitute u, which is the reference's threshold
 // branch (kernel.py:108: z for z > 20, where the two agree to fp32 rounding).
 //
-// MLPMK_SOFTPLUS_FORM selects other evaluations of the same function at
-// build time, kept to measure what the softplus costs in the forward (every
-// form is correct; the library is built with form 0, the fastest):
-//   1: max(u, 0) + log2(1 + 2^-|u|)          2 transcendentals + 3 VALU
-//   2: max(u, 0) + y P(y), y = 2^-|u|        1 transcendental  + 8 VALU
-//   3: as 2 with 2^-|u| = ldexp(E(f), -n),   0 transcendentals + 15 VALU
-//      n + f = min(|u|, 64), f in [0, 1)
-// P(y) ~ log2(1 + y) / y on [0, 1] (degree 5, relative error 8.7e-6) and
-// E(f) ~ 2^-f on [0, 1) (degree 4, 2.6e-6) are near-minimax fits in relative
-// error (least squares on Chebyshev nodes, reweighted by the error).  Forms
-// 1-3 never overflow; the maximum propagates NaN.
-#ifndef MLPMK_SOFTPLUS_FORM
-#define MLPMK_SOFTPLUS_FORM 0
-#endif
-__device__ __forceinline__ float sp2_log2_1p_poly(float y) {  // log2(1 + y), y in [0, 1]
-  float p = -0.034564435482025146f;
-  p = __builtin_fmaf(p, y, 0.1463599056005478f);
-  p = __builtin_fmaf(p, y, -0.3033289909362793f);
-  p = __builtin_fmaf(p, y, 0.46928200125694275f);
-  p = __builtin_fmaf(p, y, -0.7204402685165405f);
-  p = __builtin_fmaf(p, y, 1.442683219909668f);
-  return y * p;
-}
-__device__ __forceinline__ float sp2(float u) {
-#if MLPMK_SOFTPLUS_FORM == 0
-  return __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(u));
-#else
-  const float pos = __builtin_elementwise_maximum(u, 0.0f);
-#if MLPMK_SOFTPLUS_FORM == 1
-  return pos + __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(-__builtin_fabsf(u)));
-#elif MLPMK_SOFTPLUS_FORM == 2
-  return pos + sp2_log2_1p_poly(__builtin_amdgcn_exp2f(-__builtin_fabsf(u)));
-#else
-  const float t = __builtin_fminf(__builtin_fabsf(u), 64.0f);
-  const float f = __builtin_amdgcn_fractf(t);
-  float e = 0.0067682890221476555f;
-  e = __builtin_fmaf(e, f, -0.05307658016681671f);
-  e = __builtin_fmaf(e, f, 0.23934273421764374f);
-  e = __builtin_fmaf(e, f, -0.6930305361747742f);
-  e = __builtin_fmaf(e, f, 0.9999974370002747f);
-  return pos + sp2_log2_1p_poly(__builtin_ldexpf(e, -(int)(t - f)));
-#endif
-#endif
-}
+// Other evaluations of the same function were built and timed in this
+// kernel (all correct, all slower at the power-limited clock, because the
+// transcendental unit does not co-issue with other waves' VALU work):
+// max(u, 0) + log2(1 + 2^-|u|) (2 transcendentals + 3 VALU), max(u, 0) +
+// y P(y) with y = 2^-|u| and P a degree-5 fit of log2(1 + y)/y (1 + 8), and
+// the same with 2^-|u| from a range-reduced degree-4 polynomial (0 + 15).
+__device__ __forceinline__ float sp2(float u) { return __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(u)); }
 // Replaces an overflowed sp2 by u (u >= 128); every other value is kept as is.
 __device__ __forceinline__ float sp2_fix(float u, float s) { return u >= 128.0f ? u : s; }
 

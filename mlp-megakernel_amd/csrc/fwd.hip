@@ -2,16 +2,6 @@
 // templates in fwd_kernel.h; fp32 tensors dispatch through fwd_f32.hip).
 #include "fwd_kernel.h"
 
-#ifdef MLPMK_FWD_TIMELINE
-// Copies the records of the last persistent launch (8 x 64-bit words per wave,
-// kTimelineWaves waves) to dst and clears them.  Measurement build only.
-extern "C" int mlpmk_fwd_timeline(void* dst, int64_t bytes) {
-  if (bytes < (int64_t)sizeof(mlpmk::g_timeline)) return -1;
-  if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(mlpmk::g_timeline), sizeof(mlpmk::g_timeline)) != hipSuccess) return -2;
-  static unsigned long long zeros[mlpmk::kTimelineWaves * 8];
-  return hipMemcpyToSymbol(HIP_SYMBOL(mlpmk::g_timeline), zeros, sizeof(zeros)) == hipSuccess ? 0 : -3;
-}
-#endif
 
 // ---------------------------------------------------------------------------
 // Host dispatch

@@ -887,23 +887,9 @@ __device__ __forceinline__ void fwd_block_checked(const FwdParams& p, Chain<N, N
 // tail alone.  Each wave keeps the x rows of its next claimed block in flight
 // while it computes the current one.  D is the number of such blocks in
 // flight; one is enough (deeper rings measured no faster).
-#ifdef MLPMK_FWD_TIMELINE
-// Measurement build only (make timeline -> libmlpmk_timeline.so): every wave
-// of a persistent launch records, in 100 MHz ticks (s_memrealtime), when it
-// started, when the weight staging barrier released it and when it finished,
-// its shader-clock cycles over the same span (s_memtime), its XCD and CU and
-// how many blocks it processed.  mlpmk_fwd_timeline copies the records out.
-constexpr int kTimelineWaves = 4096;
-__device__ unsigned long long g_timeline[kTimelineWaves * 8];
-#endif
 
 template <class N, int NB, bool STASH, int NW, int D>
 __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
-#ifdef MLPMK_FWD_TIMELINE
-  const unsigned long long tl_t0 = __builtin_amdgcn_s_memrealtime(), tl_c0 = __builtin_amdgcn_s_memtime();
-  unsigned long long tl_t1 = 0;
-  unsigned int tl_nb = 0;
-#endif
   static_assert(N::valid(), "unsupported widths");
   static_assert(D >= 1 && D <= 4, "prefetch depth");
   using Plan = LdsPlan<N, NB, NW>;
@@ -952,9 +938,6 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
     stage_weights<N, NW * 64, RF>(p, lds);
   }
   __syncthreads();
-#ifdef MLPMK_FWD_TIMELINE
-  tl_t1 = __builtin_amdgcn_s_memrealtime();
-#endif
 
   i32x4* stage = stage_tiles + (STAGE ? wid * TC : 0);
   // Next block of this workgroup (>= nblk once its share is exhausted).  Without
@@ -990,25 +973,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   for (b = next; b < nblk; b = next) {
     next = claim();
     fwd_block_checked<N, NB, STASH, STAGE, KSM, RF>(p, c, lds_b, lane_off, stage, b, next, lane);
-#ifdef MLPMK_FWD_TIMELINE
-    ++tl_nb;
-#endif
   }
-#ifdef MLPMK_FWD_TIMELINE
-  const unsigned long long tl_t2 = __builtin_amdgcn_s_memrealtime(), tl_c2 = __builtin_amdgcn_s_memtime();
-  const int tl_w = (int)blockIdx.x * NW + wid;
-  if (lane == 0 && tl_w < kTimelineWaves) {
-    unsigned long long* r = g_timeline + tl_w * 8;
-    r[0] = tl_t0;
-    r[1] = tl_t1;
-    r[2] = tl_t2;
-    r[3] = tl_c2 - tl_c0;
-    r[4] = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20);  // XCC_ID
-    r[5] = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);  // HW_ID
-    r[6] = tl_nb + 1;
-    r[7] = 1;
-  }
-#endif
 }
 
 }  // namespace mlpmk

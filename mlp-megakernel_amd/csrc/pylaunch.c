@@ -7,8 +7,12 @@
  * function pointers handed over by `bind` -- the addresses of the library that
  * the ctypes binding loaded, so a build selected with MLPMK_LIBRARY is the one
  * called.  They return the library's status code; argument conversion errors
- * raise.  Built by the package Makefile with gcc against the Python headers;
- * the package uses ctypes when this module is absent.
+ * raise.  The library call itself runs with the GIL released, as ctypes does
+ * it: a launch can block inside HIP (a full launch queue, the first load of a
+ * code object, the device queries of a device's first call), and other Python
+ * threads (data loaders) keep running meanwhile.  Built by the package
+ * Makefile with gcc against the Python headers; the package uses ctypes when
+ * this module is absent.
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -130,8 +134,10 @@ static PyObject* py_fwd(PyObject* self, PyObject* const* args, Py_ssize_t nargs)
   const int64_t M = PyLong_AsLongLong(args[6]);
   void* stream = as_ptr(args[7]);
   ERR_OUT();
-  const int rc = g_fwd(L, dims, dtype, x, (const void* const*)w, out, has_stash ? (float* const*)stash : NULL, M,
-                       stream);
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_fwd(L, dims, dtype, x, (const void* const*)w, out, has_stash ? (float* const*)stash : NULL, M, stream);
+  Py_END_ALLOW_THREADS
   return PyLong_FromLong(rc);
 }
 
@@ -163,12 +169,14 @@ static PyObject* py_bwd(PyObject* self, PyObject* const* args, Py_ssize_t nargs)
   void* stream = as_ptr(args[12]);
   ERR_OUT();
   int rc;
+  Py_BEGIN_ALLOW_THREADS
   if (ws)
     rc = g_bwd_ws(L, dims, dtype, x, (const void* const*)w, (const float* const*)stash, dout, stride, dx,
                   (float* const*)dw, ws, ws_bytes, M, stream);
   else
     rc = g_bwd(L, dims, dtype, x, (const void* const*)w, (const float* const*)stash, dout, stride, dx,
                (float* const*)dw, M, stream);
+  Py_END_ALLOW_THREADS
   return PyLong_FromLong(rc);
 }
 
@@ -187,7 +195,11 @@ static PyObject* py_wn_fwd(PyObject* self, PyObject* const* args, Py_ssize_t nar
   float* inv = (float*)as_ptr(args[6]);
   void* stream = as_ptr(args[7]);
   ERR_OUT();
-  return PyLong_FromLong(g_wn_fwd(L, dims, pd, wd, v, g, w, inv, stream));
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_wn_fwd(L, dims, pd, wd, v, g, w, inv, stream);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(rc);
 }
 
 /* wn_bwd(dims, param_dtype, dw, v, g, inv_norm, dv, dg, stream) -> status */
@@ -206,7 +218,11 @@ static PyObject* py_wn_bwd(PyObject* self, PyObject* const* args, Py_ssize_t nar
   void* dg = as_ptr(args[7]);
   void* stream = as_ptr(args[8]);
   ERR_OUT();
-  return PyLong_FromLong(g_wn_bwd(L, dims, pd, dw, v, g, inv, dv, dg, stream));
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_wn_bwd(L, dims, pd, dw, v, g, inv, dv, dg, stream);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(rc);
 }
 
 static PyMethodDef kMethods[] = {

@@ -226,7 +226,9 @@ def _dout_rows(dout, M, out_w, dtype, dev):
     """``(dout, row_stride)`` as the library reads it: one element broadcast
     everywhere (both strides 0: ``DOUT_SCALAR``), or [M, OUT] rows with unit
     column stride whose row stride (0 for a broadcast row) is a multiple of 8
-    elements; other row strides are copied into padded rows."""
+    elements and whose first element is 16-byte aligned; other row strides
+    and base addresses (a column slice of a wider gradient) are copied into
+    padded rows."""
     if dout.dtype != dtype or dout.device != dev:
         raise TypeError(f"dout must be {dtype} on the same device as x")
     if tuple(dout.shape) != (M, out_w):
@@ -236,9 +238,10 @@ def _dout_rows(dout, M, out_w, dtype, dev):
     if dout.stride(1) != 1:
         raise ValueError(f"dout must be [M, OUT]={M, out_w} with unit column stride")
     row_stride = int(dout.stride(0)) if M > 1 else -(-out_w // 8) * 8
-    if row_stride % 8 != 0:
+    if row_stride % 8 != 0 or dout.data_ptr() % 16 != 0:
         # The library reads dout rows from 16-byte boundaries: an output width
-        # that is not a multiple of 8 gets rows padded to the next multiple.
+        # that is not a multiple of 8, or rows that start off such a boundary,
+        # get a padded copy.
         padded = torch.zeros((M, -(-out_w // 8) * 8), dtype=dtype, device=dev)
         padded[:, :out_w] = dout
         dout, row_stride = padded, padded.shape[1]

@@ -70,6 +70,26 @@ def test_sum_gradient_stays_one_element():
     assert _as_row_broadcast(dense).is_contiguous()
 
 
+def test_misaligned_dout_rows_are_copied():
+    # The gradient of a column slice of torch.cat([a, out, b], 1): unit
+    # column stride, a row stride that is a multiple of 8, but a first
+    # element 4 elements (8 bytes) past a 16-byte boundary.  The library
+    # reads dout rows from 16-byte boundaries, so _dout_rows copies it into
+    # aligned rows instead of passing it through.
+    from mlpmk import ops
+
+    base = torch.randn(6, 136).half()
+    assert base.data_ptr() % 16 == 0
+    g = base[:, 4:132]
+    assert g.stride() == (136, 1) and g.data_ptr() % 16 == 8
+    d, st = ops._dout_rows(g, 6, 128, torch.float16, g.device)
+    assert d.data_ptr() % 16 == 0 and st % 8 == 0 and st >= 128
+    assert torch.equal(d[:, :128], g)
+    aligned = base[:, 8:136]
+    d2, st2 = ops._dout_rows(aligned, 6, 128, torch.float16, aligned.device)
+    assert d2 is aligned and st2 == 136  # an aligned slice goes through as is
+
+
 def test_product_path_refuses_cpu_tensors():
     m = fused_mlp.FusedMLPSoftplus().half()
     with pytest.raises(ValueError, match="GPU"):

@@ -117,3 +117,95 @@ def test_noalloc_rejects_shapes_beyond_its_scratch():
     assert rc == 2 and "scratch" in err, (rc, err)  # MLPMK_ERR_UNSUPPORTED_SHAPE, nothing launched
     torch.cuda.synchronize()
     assert all(int(torch.count_nonzero(d)) == 0 for d in dws) and int(torch.count_nonzero(dx)) == 0
+
+
+# The 64 MiB claim of mlpmk.h: every 2- and 3-layer network mlpmk_bwd_supported
+# accepts needs at most MLPMK_NOALLOC_SCRATCH_BYTES of workspace at any M
+# (the weight-gradient partials are one dW copy per workgroup of a grid
+# capped at the CU count times the occupancy), fp16 and bf16, with and
+# without dx; the 5-layer 128-wide network up to 65,536 rows.
+NOALLOC_BYTES = 64 << 20
+SWEEP_DIMS = [
+    (128, 128, 128, 128), (32, 64, 64, 16), (128, 128, 128), (16, 16, 16), (16, 128, 1),
+    (128, 112, 128, 128), (48, 96, 80, 10), (112, 128, 96, 128), (128, 128, 7),
+]
+
+
+@pytest.mark.parametrize("dims", SWEEP_DIMS)
+def test_two_and_three_layer_workspace_fits_the_scratch_at_any_batch(dims):
+    assert ops.bwd_supported(list(dims))
+    for dt in (torch.float16, torch.bfloat16):
+        for with_dx in (False, True):
+            sizes = [ops.bwd_workspace_bytes(dims, m, with_dx, dtype=dt)
+                     for m in (1, 4096, 16384, 65536, 131072, 1 << 20, 1 << 24, (1 << 31) - 1)]
+            assert max(sizes) <= NOALLOC_BYTES, (dims, dt, with_dx, sizes)
+
+
+def test_five_layer_workspace_fits_up_to_65536_rows():
+    for with_dx in (False, True):
+        assert ops.bwd_workspace_bytes((128,) * 6, 65536, with_dx) <= NOALLOC_BYTES
+        assert ops.bwd_workspace_bytes((128,) * 6, 262144, with_dx) > NOALLOC_BYTES
+
+
+# The first mlpmk_bwd_noalloc call of a process made inside a HIP graph
+# capture (the scratch array's address is looked up on that call), then the
+# graph replayed with fresh inputs and each replay checked against the
+# oracle.  Runs in a child process so that the call really is the first.
+_CAPTURE_SCRIPT = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+import numpy as np, torch
+import _mlpmk  # noqa: F401
+from mlpmk import _lib, ops
+from oracle import mlp_oracle as orc
+
+dims, m = (128, 128, 128, 128), 16384
+lib = _lib.get()
+x0, ws = orc.make_inputs(dims, m, seed=41)
+wd = [torch.from_numpy(w).cuda() for w in ws]
+xd = torch.from_numpy(x0).cuda()
+hs = [torch.empty((m, 128), dtype=torch.float32, device="cuda") for _ in range(2)]
+out = torch.empty((m, 128), dtype=torch.float16, device="cuda")
+dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
+dout = torch.ones((1, 128), dtype=torch.float16, device="cuda")
+pd, k1 = _lib.int_array(list(dims))
+pw, k2 = _lib.ptr_array([w.data_ptr() for w in wd])
+ph, k3 = _lib.ptr_array([h.data_ptr() for h in hs])
+pg, k4 = _lib.ptr_array([d.data_ptr() for d in dws])
+s = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+ops.fwd_into(xd, wd, out, hs)  # forward kernels loaded outside the capture
+torch.cuda.synchronize()
+with torch.cuda.graph(g, stream=s):
+    for d in dws:
+        d.zero_()
+    ops.fwd_into(xd, wd, out, hs)
+    rc = lib.mlpmk_bwd_noalloc(3, pd, _lib.DTYPE_F16, xd.data_ptr(), pw, ph, dout.data_ptr(), 0, None, pg, m,
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.mlpmk_last_error().decode()
+torch.cuda.synchronize()
+for rep in range(3):
+    x, _ = orc.make_inputs(dims, m, seed=100 + rep)
+    xd.copy_(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    rdws, _ = orc.backward(x, ws, ref_h, np.ones((m, 128), np.float32), need_dx=False)
+    for i in range(3):
+        got = dws[i].cpu().numpy().astype(np.float64)
+        r = rdws[i].astype(np.float64)
+        worst = np.max(np.abs(got - r) - (2e-2 * np.abs(r) + 2e-3 * np.abs(r).max()))
+        frob = np.linalg.norm(got - r) / np.linalg.norm(r)
+        assert worst <= 0 and frob < 1e-2, (rep, i, worst, frob)
+print("capture ok")
+'''
+
+
+def test_first_noalloc_call_inside_a_graph_capture():
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "capture ok" in r.stdout, r.stdout[-2000:] + r.stderr[-4000:]
