@@ -42,12 +42,14 @@ typedef enum mlpmk_status {
 } mlpmk_status;
 
 /* Element types.  The forward (mlpmk_fwd) takes fp16, bf16 or fp32 tensors
- * (x, w and out all of that type); the backward (mlpmk_bwd*) fp16 or bf16
- * tensors (x, w, dout, dx; fp32 ones are rejected with
- * MLPMK_ERR_UNSUPPORTED_SHAPE).  Accumulation, the stash and the weight
- * gradients are fp32 either way.  The weight-norm parameters may be fp32,
- * fp16 or bf16.  The reference's kernels take their element type as the
- * INPUT_DTYPE constexpr (/root/reference/mlp_fused.md:159-166). */
+ * (x, w and out all of that type), and so does the backward (mlpmk_bwd_ws /
+ * _noalloc: x, w, dout, dx).  Accumulation, the stash and the weight
+ * gradients are fp32 either way.  fp32 tensors run with every MFMA operand
+ * split into bf16 hi + lo (products hi*hi + hi*lo + lo*hi): fp32's exponent
+ * range and a ~16-bit significand, where the reference's TF32 tl.dot
+ * operands keep 10 bits; widths up to 128.  The weight-norm parameters may
+ * be fp32, fp16 or bf16.  The reference's kernels take their element type as
+ * the INPUT_DTYPE constexpr (/root/reference/mlp_fused.md:159-166). */
 enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1, MLPMK_DTYPE_BF16 = 2 };
 
 /* dout_row_stride of the backward entry points for a dL/dout that is one
@@ -80,10 +82,19 @@ const char* mlpmk_last_error(void);
  */
 int mlpmk_fwd_supported(int num_layers, const int* dims);
 
-/* 1 if the backward kernel exists for (num_layers, dims), else 0.  Host only.
- * The shapes of mlpmk_fwd_supported with every width at most 128 (wider
- * networks train through the library-GEMM fallback, mlpmk_sigmoid_h_mul). */
+/* 1 if a backward kernel exists for (num_layers, dims) with 16-bit tensors,
+ * else 0.  Host only.  The shapes of mlpmk_fwd_supported with every width at
+ * most 128, and those with widths up to 256 (input and hidden multiples of
+ * 16) whose output width is a multiple of 8 (the two-pass backward; other
+ * wide networks train through the library-GEMM fallback,
+ * mlpmk_sigmoid_h_mul). */
 int mlpmk_bwd_supported(int num_layers, const int* dims);
+
+/* mlpmk_bwd_supported for tensors of `dtype` (MLPMK_DTYPE_*): fp32 tensors
+ * take networks of 2..5 layers with every width at most 128 (input and
+ * hidden multiples of 16, output a multiple of 8).  Host only.  Since ABI
+ * version 202. */
+int mlpmk_bwd_supported_dtype(int num_layers, const int* dims, int dtype);
 
 /*
  * 1 if mlpmk_bwd / mlpmk_bwd_ws accept stash[num_layers-2] == NULL for
@@ -112,10 +123,10 @@ int mlpmk_bwd_recompute_supported(int num_layers, const int* dims);
  *   dtype  MLPMK_DTYPE_F16, MLPMK_DTYPE_BF16 or MLPMK_DTYPE_F32: element
  *          type of x, w and out (bf16: bf16 MFMA operands, hidden
  *          activations rounded to bf16 between layers, as the reference's
- *          casts to INPUT_DTYPE do; fp32: x, the scaled weights and the
- *          hidden activations rounded to fp16 MFMA operands -- the 10-bit
- *          mantissa of the reference's TF32 tl.dot operands, with fp16's
- *          exponent range -- and out written in fp32 from the accumulators)
+ *          casts to INPUT_DTYPE do; fp32: x, the weights and the hidden
+ *          activations split into bf16 hi/lo operand pairs -- fp32's
+ *          exponent range, a ~16-bit significand -- and out written in fp32
+ *          from the accumulators; widths up to 128)
  *   x      [M, dims[0]]            dtype, device
  *   w[l]   [dims[l], dims[l+1]]    dtype, device, l = 0 .. num_layers-1
  *   out    [M, dims[num_layers]]   dtype, device (written)
@@ -149,14 +160,18 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
 /*
  * Backward megakernel (one launch): data gradients with MFMA, weight gradients
  * as split-K partials reduced in LDS and then added with global fp32 atomics
- * by every workgroup.  mlpmk_bwd_ws below is the faster form.
+ * by every workgroup.  mlpmk_bwd_ws below is the faster form, and the only
+ * one for fp32 tensors and widths above 128 (their two-pass backward hands
+ * dz between its passes through the workspace): here those return
+ * MLPMK_ERR_INVALID_ARG without touching the device.
  *
  * Replaces the fused backward of the reference's `FusedMLPSoftplus` autograd
  * function (/root/reference/mlp_fused.md:88-112, README.md:32) -- the file that
  * held it (fused_mlp.py, README.md:18) is not in the reference snapshot.
  *
- *   dtype            MLPMK_DTYPE_F16 or MLPMK_DTYPE_BF16: element type of x,
- *                    w, dout and dx
+ *   dtype            MLPMK_DTYPE_F16, MLPMK_DTYPE_BF16 or MLPMK_DTYPE_F32
+ *                    (mlpmk_bwd_ws / _noalloc only): element type of x, w,
+ *                    dout and dx
  *   x                [M, dims[0]] dtype
  *   w[l]             as in mlpmk_fwd
  *   stash[l]         h_{l+1} [M, dims[l+1]] fp32, as written by mlpmk_fwd;
@@ -166,9 +181,9 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
  *   dout             dL/dout, dtype, row l at dout + l * dout_row_stride
  *                    elements; dout_row_stride = 0 broadcasts one row,
  *                    MLPMK_DOUT_SCALAR one element to every row and column
- *                    (the expanded gradient of loss = out.sum()), otherwise
- *                    a multiple of 8 (16-byte rows) not below the output
- *                    width
+ *                    (the expanded gradient of loss = out.sum(); aligned to
+ *                    its element size), otherwise a multiple of 8 not below
+ *                    the output width
  *   dx               NULL, or [M, dims[0]] dtype (written)
  *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
  *                    caller zeroes them for a fresh gradient
@@ -182,15 +197,20 @@ int mlpmk_bwd(int num_layers, const int* dims, int dtype, const void* x, const v
 
 /*
  * mlpmk_bwd with a caller-provided device workspace (same arguments and
- * results; replaces the same reference interface).  Each workgroup of the
- * backward megakernel stores its weight-gradient partial sums in the
- * workspace with plain stores, and a second kernel on the same stream sums
- * them into dw (+=, one thread per element, no atomics) instead of every
- * workgroup adding its partials with fp32 atomics: device-wide fp32 atomics
- * run at ~270 M elements/s, and that flush cost ~45-65 us at M = 131072
- * (256 workgroups x 49152 dW elements).  Grids below 64 workgroups (small M)
- * keep the atomic flush, which is then cheaper, and leave the partial-sum
- * part of the workspace untouched.
+ * results; replaces the same reference interface).  Two forms run behind it:
+ *   - the one-pass megakernel (16-bit tensors, widths up to 128, batches
+ *     above 16,384 rows, and every recomputing call): each workgroup stores
+ *     its weight-gradient partial sums in the workspace with plain stores,
+ *     and a second kernel on the same stream sums them into dw (+=, one
+ *     thread per element, in a fixed order) instead of every workgroup
+ *     adding a whole dW with fp32 atomics (~45-65 us at M = 131072: 256
+ *     workgroups x 49152 elements from few CUs each);
+ *   - the two-pass backward (fp32 tensors, widths above 128, and 16-bit
+ *     batches up to 16,384 rows): a data-gradient kernel over 32-row blocks
+ *     of the whole chip writes every dz_l into the workspace, then a
+ *     weight-gradient kernel whose workgroups own 64 x 64 blocks of one dW_l
+ *     and a chunk of rows adds its tiles to dw with fp32 atomics (summation
+ *     order not fixed).
  * Networks of 4 and 5 layers run as two launches (all their dgrad weights
  * and exchange tiles do not fit one workgroup's 160 KiB of LDS): layers
  * L-1..S, whose fp16 gradient of h_S goes through the first M * 256 bytes
@@ -219,10 +239,13 @@ int mlpmk_bwd_ws(int num_layers, const int* dims, int dtype, const void* x, cons
  * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree.
  *   - Shapes whose workspace (mlpmk_bwd_workspace_size) exceeds
  *     MLPMK_NOALLOC_SCRATCH_BYTES return MLPMK_ERR_UNSUPPORTED_SHAPE before
- *     anything is launched: every 3-layer and 2-layer network at any M (the
- *     partials take at most 48 MiB on MI355X), 4- and 5-layer networks up to
- *     the M whose dz hand-over (M x 256 bytes) still fits (M = 65,536 for the
- *     5-layer 128-wide network).
+ *     anything is launched.  What fits: every 3-layer and 2-layer network with
+ *     16-bit tensors and widths up to 128 at any M (the partials take at most
+ *     48 MiB on MI355X); 4- and 5-layer ones up to the M whose dz hand-over
+ *     (M x 256 bytes) still fits (M = 65,536 for the 5-layer 128-wide
+ *     network); fp32 tensors and widths above 128 up to the M whose
+ *     two-pass dz blocks (M x the hidden widths x the element size) fit
+ *     (M = 65,536 for the 3-layer 128-wide network in fp32).
  *   - Every call on a device shares that device's array, and calls that
  *     overlap on one device (two streams) race; calls in one stream order are
  *     safe.  The array keeps the last call's contents; nothing needs to start
@@ -235,10 +258,12 @@ int mlpmk_bwd_noalloc(int num_layers, const int* dims, int dtype, const void* x,
                       float* const* dw, int64_t M, void* stream);
 
 /*
- * Bytes of workspace mlpmk_bwd_ws needs on the current device: one fp32 copy
- * of all dW blocks per workgroup of the backward grid, plus for the 5-layer
- * network the dz block of the hand-over between its two launches (0 when
- * M == 0).
+ * Bytes of workspace mlpmk_bwd_ws needs on the current device: for the
+ * one-pass megakernel one fp32 copy of all dW blocks per workgroup of the
+ * backward grid, plus for 4- and 5-layer networks the dz block of the
+ * hand-over between their two launches; for the two-pass backward the dz of
+ * every hidden layer ([M, width], element size of dtype); the larger where
+ * a call at this M may take either (0 when M == 0).
  */
 int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t M, int with_dx, int64_t* bytes);
 
@@ -249,7 +274,7 @@ int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t
  * from the snapshot).  v and g live in two contiguous blocks, layer after layer
  * (v_all / g_all, mlp_fused.md:478-480):
  *   param_dtype  MLPMK_DTYPE_F32, _F16 or _BF16: element type of v and g
- *   w_dtype      MLPMK_DTYPE_F16 or _BF16: element type of w_out
+ *   w_dtype      MLPMK_DTYPE_F16, _BF16 or _F32: element type of w_out
  *   v      sum_l dims[l]*dims[l+1] elements of param_dtype, layer l = [dims[l], dims[l+1]]
  *   g      sum_l dims[l+1] elements of param_dtype
  *   w_out  same element layout as v, w_dtype (written)

@@ -37,10 +37,10 @@ _POLICY = {
     (32, 64, 64, 16): (2, 2, 64, 16),
 }
 _GENERIC_POLICY = (0, 0, 32, 8)  # runtime-width kernels: no split kernel, at most 8 waves
-# fp32 tensors (fwd_f32.hip): the persistent kernel only, 32-row blocks, at
-# most this many waves (4 where 8 would spill: the 3-layer runtime-width kernel).
-_POLICY_F32 = {(128, 128, 128, 128): 8, (32, 64, 64, 16): 8, (128, 128, 128, 128, 128, 128): 8}
-_GENERIC_WAVES_F32 = {2: 8, 3: 4, 4: 8, 5: 4}
+# fp32 tensors (fwd_x3.hip): the feature-split kernel at every M, 32-row
+# blocks, 4 waves (one per 32 output features of a 128-wide layer; the
+# runtime-width kernels are compiled at width 128).
+_F32_WAVES = 4
 
 
 def __getattr__(name):
@@ -53,10 +53,7 @@ def _mirror_policy(M, dims, num_cus, fp32=False):
     if max(dims) > 128:  # streamed-weight kernel (fwd_wide.hip): 8 waves, 32-row blocks, any M
         return 32, 8
     if fp32:
-        max_waves = _POLICY_F32.get(tuple(dims)) or _GENERIC_WAVES_F32[len(dims) - 1]
-        if max_waves > 4 and -(-M // 32) <= 4 * num_cus:
-            return 32, 4
-        return 32, max_waves
+        return 32, _F32_WAVES
     split_per_cu, split_waves, bm, max_waves = _POLICY.get(tuple(dims), _GENERIC_POLICY)
     if -(-M // 32) <= split_per_cu * num_cus:
         return 32, split_waves
@@ -89,9 +86,8 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
     With ``num_cus`` None and a GPU present the answer comes from the library
     (``mlpmk_fwd_launch_info``); otherwise from the mirror above with
     ``num_cus`` CUs (MI355X's 256 by default).  ``fp32`` inputs (fp32 x, W
-    and out; fp16 MFMA operands) always take the persistent kernel, with at
-    most 8 waves per workgroup (4 up to 4 blocks per CU, and for the 3-layer
-    runtime-width kernel).
+    and out; bf16 hi/lo split MFMA operands) always take their feature-split
+    kernel: 32-row blocks, 4 waves.
     """
     dims = (K1, N1, N2, N3)
     if num_cus is None and torch.cuda.is_available():

@@ -26,6 +26,7 @@ SIGNATURES = {
     "mlpmk_fwd_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_recompute_supported": (c_int, [c_int, P_INT]),
+    "mlpmk_bwd_supported_dtype": (c_int, [c_int, P_INT, c_int]),
     "mlpmk_fwd": (c_int, [c_int, P_INT, c_int, c_void_p, P_VOIDP, c_void_p, P_VOIDP, c_int64, c_void_p]),
     "mlpmk_fwd_launch_info": (c_int, [c_int, P_INT, c_int, c_int64, c_int, P_INT]),
     "mlpmk_bwd": (

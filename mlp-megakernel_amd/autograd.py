@@ -18,6 +18,10 @@ Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
   The reference casts to fp16 (``cast_inputs=torch.float16``); here the
   tensors take the autocast dtype, so ``torch.autocast(dtype=torch.bfloat16)``
   runs the bf16 kernels and fp16 autocast the fp16 ones (``kernel_dtype``).
+  Outside autocast the tensors keep their own type, as the reference's
+  INPUT_DTYPE kernels do (mlp_fused.md:159-166): fp32 parameters and an fp32
+  ``x`` run the fp32-tensor kernels (bf16 hi/lo split operands: fp32's
+  exponent range) and return an fp32 ``out``.
 * inference: ``fused_mlp`` / ``fused_mlp_wn`` (and the modules) call the plain
   forward, without the fp32 stash, whenever autograd will not need it -- grad
   disabled (``torch.no_grad`` / ``inference_mode``) or nothing requiring grad.
@@ -65,18 +69,20 @@ def _backward_impl():
 _bwd_shapes = {}
 
 
-def _fused_bwd_supported(dims):
-    ok = _bwd_shapes.get(dims)
+def _fused_bwd_supported(dims, dtype=torch.float16):
+    key = (dims, dtype)
+    ok = _bwd_shapes.get(key)
     if ok is None:
-        ok = _bwd_shapes[dims] = ops.bwd_supported(list(dims))
+        ok = _bwd_shapes[key] = ops.bwd_supported(list(dims), dtype)
     return ok
 
 
 def _run_bwd(x, weights, hs, dout, dws, dx):
-    # Shapes without a fused backward (widths above 128) take the fallback:
+    # Shapes without a fused backward (output widths that are not a multiple
+    # of 8 above 128, or fp32 ones not a multiple of 8) take the fallback:
     # the reference's own route for shapes its fused kernel does not cover.
     dims = tuple([int(x.shape[1])] + [int(w.shape[1]) for w in weights])
-    if _backward_impl() == "fallback" or not _fused_bwd_supported(dims):
+    if _backward_impl() == "fallback" or not _fused_bwd_supported(dims, x.dtype):
         from . import fallback
 
         fallback.bwd(x, weights, hs, dout, dws, dx)
@@ -84,8 +90,10 @@ def _run_bwd(x, weights, hs, dout, dws, dx):
         ops.bwd(x, weights, hs, dout, dws, dx)
 
 
-def _use_recompute(dims, m, need_dx):
-    if RECOMPUTE == "never" or _backward_impl() == "fallback" or not _fused_bwd_supported(tuple(dims)):
+def _use_recompute(dims, m, need_dx, dtype=torch.float16):
+    if RECOMPUTE == "never" or _backward_impl() == "fallback" or not _fused_bwd_supported(tuple(dims), dtype):
+        return False
+    if dtype == torch.float32:  # (the recomputing kernels are 16-bit ones)
         return False
     if RECOMPUTE not in ("auto", "always"):
         raise ValueError(f"RECOMPUTE must be 'auto', 'always' or 'never', got {RECOMPUTE!r}")
@@ -98,14 +106,19 @@ def _use_recompute(dims, m, need_dx):
     return m >= (RECOMPUTE_MIN_ROWS_5L if len(dims) == 6 else RECOMPUTE_MIN_ROWS)
 
 
-def kernel_dtype(x):
+def kernel_dtype(x, dims=None):
     """Element type the megakernels run in for input ``x``: the autocast dtype
-    when autocast is on (fp16 unless it is bf16), else bf16 for a bf16 ``x``
-    and fp16 for anything else (the reference's modules are fp16,
-    README.md:24-34)."""
+    when autocast is on (fp16 unless it is bf16); else ``x``'s own type --
+    bf16, fp16, or fp32 where the fp32-tensor kernels take the network
+    (every width at most 128; wider networks run fp32 ``x`` in fp16) -- and
+    fp16 for anything else."""
     if torch.is_autocast_enabled("cuda"):
         return torch.bfloat16 if torch.get_autocast_dtype("cuda") == torch.bfloat16 else torch.float16
-    return torch.bfloat16 if x.dtype == torch.bfloat16 else torch.float16
+    if x.dtype == torch.bfloat16:
+        return torch.bfloat16
+    if x.dtype == torch.float32 and (dims is None or max(dims) <= 128):
+        return torch.float32
+    return torch.float16
 
 
 def _needs_graph(*tensors):
@@ -138,12 +151,12 @@ class FusedMLPFunction(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, x, *weights):
-        dt = kernel_dtype(x)
+        dims = (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights)
+        dt = kernel_dtype(x, dims)
         x = x.to(dt).contiguous()
         weights = [w.to(dt).contiguous() for w in weights]
         if any(ctx.needs_input_grad):
-            dims = (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights)
-            rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0])
+            rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0], dt)
             out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
             ctx.save_for_backward(x, *weights, *[h for h in hs if h is not None])
             ctx.dims = dims
@@ -164,11 +177,11 @@ class FusedMLPFunction(torch.autograd.Function):
         dout = _as_row_broadcast(dout.to(x.dtype))
         dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        if _backward_impl() == "fused" and _fused_bwd_supported(dims):
+        if _backward_impl() == "fused" and _fused_bwd_supported(dims, x.dtype):
             # x, the weights and the stash were checked by the forward.
             M = int(x.shape[0])
             dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, x.device)
-            ops._bwd_raw(x.device, dims, ops._elem_code(x.dtype), x.data_ptr(), [w.data_ptr() for w in weights],
+            ops._bwd_raw(x.device, dims, ops._fwd_code(x.dtype), x.data_ptr(), [w.data_ptr() for w in weights],
                          [h.data_ptr() if h is not None else None for h in hs], dout.data_ptr(), row_stride,
                          dx.data_ptr() if dx is not None else None, [d.data_ptr() for d in dws], M)
         else:
@@ -191,8 +204,8 @@ class FusedMLPWNFunction(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, x, v_all, g_all, dims):
-        x = x.to(kernel_dtype(x)).contiguous()
         dims = tuple(int(d) for d in dims)
+        x = x.to(kernel_dtype(x, dims)).contiguous()
         nw, ng, woff = _layout(dims)
         dev = x.device
         if dev.type != "cuda":
@@ -206,17 +219,17 @@ class FusedMLPWNFunction(torch.autograd.Function):
             raise TypeError("v_all and g_all must share a dtype and x's device")
         if v_all.numel() != nw or g_all.numel() != ng:
             raise ValueError("weight-norm block sizes do not match dims")
-        code = ops._elem_code(x.dtype)
+        code = ops._fwd_code(x.dtype)
         w_all = torch.empty(nw, dtype=x.dtype, device=dev)  # the megakernels' element type
         inv_all = torch.empty(ng, dtype=torch.float32, device=dev)
         ops._wn_fwd_raw(dev, dims, pcode, code, v_all.data_ptr(), g_all.data_ptr(), w_all.data_ptr(),
                         inv_all.data_ptr())
-        wb = w_all.data_ptr()
-        w_ptrs = [wb + 2 * o for o in woff]
+        wb, es = w_all.data_ptr(), w_all.element_size()
+        w_ptrs = [wb + es * o for o in woff]
         M = int(x.shape[0])
         out = torch.empty((M, dims[-1]), dtype=x.dtype, device=dev)
         if any(ctx.needs_input_grad):
-            rc = _use_recompute(dims, M, ctx.needs_input_grad[0])
+            rc = _use_recompute(dims, M, ctx.needs_input_grad[0], x.dtype)
             hs = [torch.empty((M, d), dtype=torch.float32, device=dev) for d in dims[1:-1]]
             if rc:
                 hs[-1] = None
@@ -242,10 +255,10 @@ class FusedMLPWNFunction(torch.autograd.Function):
         dout = _as_row_broadcast(dout.to(x.dtype))
         dw_all = torch.zeros(nw, dtype=torch.float32, device=dev)
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        if _backward_impl() == "fused" and _fused_bwd_supported(dims):
+        if _backward_impl() == "fused" and _fused_bwd_supported(dims, x.dtype):
             dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, dev)
-            wb, gb = w_all.data_ptr(), dw_all.data_ptr()
-            ops._bwd_raw(dev, dims, ops._elem_code(x.dtype), x.data_ptr(), [wb + 2 * o for o in woff],
+            wb, gb, es = w_all.data_ptr(), dw_all.data_ptr(), w_all.element_size()
+            ops._bwd_raw(dev, dims, ops._fwd_code(x.dtype), x.data_ptr(), [wb + es * o for o in woff],
                          [h.data_ptr() if h is not None else None for h in hs], dout.data_ptr(), row_stride,
                          dx.data_ptr() if dx is not None else None, [gb + 4 * o for o in woff], M)
         else:
@@ -291,7 +304,7 @@ def fused_mlp(x, *weights):
     launch."""
     if _needs_graph(x, *weights):
         return FusedMLPFunction.apply(x, *weights)
-    dt = kernel_dtype(x)
+    dt = kernel_dtype(x, (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights))
     return ops.fwd(x.to(dt).contiguous(), [w.to(dt).contiguous() for w in weights])
 
 
@@ -301,7 +314,7 @@ def fused_mlp_wn(x, v_all, g_all, dims):
     dims = tuple(int(d) for d in dims)
     if _needs_graph(x, v_all, g_all):
         return FusedMLPWNFunction.apply(x, v_all, g_all, dims)
-    x = x.to(kernel_dtype(x)).contiguous()
+    x = x.to(kernel_dtype(x, dims)).contiguous()
     w_all = torch.empty(sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1)), dtype=x.dtype, device=x.device)
     inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=x.device)
     ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)

@@ -15,9 +15,10 @@ namespace mlpmk {
 bool fwd_supported_dims(int L, const int* dims);
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, int dtype, hipStream_t st, LaunchInfo* info);
 bool bwd_supported_dims(int L, const int* dims);
+bool bwd_supported_dtype(int L, const int* dims, int dtype);
 bool bwd_recompute_supported(int L, const int* dims);
-int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st);
-int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, bool bf, int64_t* bytes);
+int bwd_dispatch(int L, const int* dims, const BwdParams& p, int dtype, hipStream_t st);
+int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int dtype, int64_t* bytes);
 int scratch_workspace(void** ptr, int64_t* bytes);
 int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* v, const void* g, void* w_out,
                     float* inv_norm, hipStream_t st);
@@ -78,17 +79,14 @@ int kernel_occupancy(const void* kernel, int threads, int* wgs_per_cu) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Element format of the 16-bit tensors of the megakernels.
-static int check_elem_dtype(int dtype) {
-  if (dtype == MLPMK_DTYPE_F16 || dtype == MLPMK_DTYPE_BF16) return MLPMK_OK;
-  if (dtype == MLPMK_DTYPE_F32)
-    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE,
-                "dtype=fp32: the megakernels take fp16 or bf16 tensors (fp32 accumulation); cast first");
-  return fail(MLPMK_ERR_INVALID_ARG, "dtype=%d (1 = fp16, 2 = bf16)", dtype);
+// Element format of the backward's x, w, dout and dx.
+static int check_bwd_dtype(int dtype) {
+  if (dtype == MLPMK_DTYPE_F16 || dtype == MLPMK_DTYPE_BF16 || dtype == MLPMK_DTYPE_F32) return MLPMK_OK;
+  return fail(MLPMK_ERR_INVALID_ARG, "dtype=%d (0 = fp32, 1 = fp16, 2 = bf16)", dtype);
 }
 
 // Element format of the forward's x, W and out: fp32 tensors are taken too
-// (fp16 MFMA operands, fp32 output rows).
+// (bf16 hi/lo split MFMA operands, fp32 rows).
 static int check_fwd_dtype(int dtype) {
   if (dtype == MLPMK_DTYPE_F16 || dtype == MLPMK_DTYPE_BF16 || dtype == MLPMK_DTYPE_F32) return MLPMK_OK;
   return fail(MLPMK_ERR_INVALID_ARG, "dtype=%d (0 = fp32, 1 = fp16, 2 = bf16)", dtype);
@@ -115,7 +113,7 @@ using namespace mlpmk;
 
 extern "C" {
 
-int mlpmk_version(void) { return 201; }  // 2.01: MLPMK_DOUT_SCALAR
+int mlpmk_version(void) { return 202; }  // 2.02: fp32 backward, mlpmk_bwd_supported_dtype, fp32 W from weight norm
 
 const char* mlpmk_status_string(int status) {
   switch (status) {
@@ -139,6 +137,12 @@ int mlpmk_fwd_supported(int num_layers, const int* dims) {
 int mlpmk_bwd_supported(int num_layers, const int* dims) {
   if (!dims || num_layers < 2 || num_layers > kMaxLayersHost) return 0;
   return bwd_supported_dims(num_layers, dims) ? 1 : 0;
+}
+
+int mlpmk_bwd_supported_dtype(int num_layers, const int* dims, int dtype) {
+  if (!dims || num_layers < 2 || num_layers > kMaxLayersHost) return 0;
+  if (dtype != MLPMK_DTYPE_F16 && dtype != MLPMK_DTYPE_BF16 && dtype != MLPMK_DTYPE_F32) return 0;
+  return bwd_supported_dtype(num_layers, dims, dtype) ? 1 : 0;
 }
 
 int mlpmk_bwd_recompute_supported(int num_layers, const int* dims) {
@@ -215,7 +219,7 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
                       bool use_scratch = false) {
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
-  if ((rc = check_elem_dtype(dtype))) return rc;
+  if ((rc = check_bwd_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   const bool dout_scalar = dout_row_stride == MLPMK_DOUT_SCALAR;
   if (dout_row_stride < 0 && !dout_scalar)
@@ -223,8 +227,9 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
                 (long long)dout_row_stride, (int)MLPMK_DOUT_SCALAR);
   if (!w || !dw) return fail(MLPMK_ERR_INVALID_ARG, "w or dw is NULL");
   if (num_layers > 1 && !stash) return fail(MLPMK_ERR_INVALID_ARG, "stash is NULL");
-  if (!bwd_supported_dims(num_layers, dims))
-    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+  if (!bwd_supported_dtype(num_layers, dims, dtype))
+    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths%s",
+                dtype == MLPMK_DTYPE_F32 ? " with fp32 tensors (widths up to 128, output width a multiple of 8)" : "");
   const int out_w = dims[num_layers];
   if (dout_row_stride > 0 && dout_row_stride < out_w)
     return fail(MLPMK_ERR_INVALID_ARG, "dout_row_stride=%lld is below the output width %d",
@@ -246,8 +251,9 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
   if ((rc = check_ptr(x, "x"))) return rc;
   if (dout_scalar) {
     if (!dout) return fail(MLPMK_ERR_INVALID_ARG, "dout is NULL");
-    if (reinterpret_cast<uintptr_t>(dout) & 1u)
-      return fail(MLPMK_ERR_MISALIGNED, "dout=%p is not 2-byte aligned", dout);
+    const uintptr_t al = dtype == MLPMK_DTYPE_F32 ? 3u : 1u;
+    if (reinterpret_cast<uintptr_t>(dout) & al)
+      return fail(MLPMK_ERR_MISALIGNED, "dout=%p is not %d-byte aligned", dout, (int)al + 1);
   } else if ((rc = check_ptr(dout, "dout"))) {
     return rc;
   }
@@ -270,8 +276,7 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
   if (workspace) {
     if ((rc = check_ptr(workspace, "workspace"))) return rc;
     int64_t need = 0;
-    if ((rc = bwd_workspace_bytes(num_layers, dims, M, dx != nullptr, dtype == MLPMK_DTYPE_BF16, &need)))
-      return rc;
+    if ((rc = bwd_workspace_bytes(num_layers, dims, M, dx != nullptr, dtype, &need))) return rc;
     if (use_scratch && need > workspace_bytes)
       return fail(MLPMK_ERR_UNSUPPORTED_SHAPE,
                   "M=%lld needs %lld bytes of workspace; mlpmk_bwd_noalloc's scratch holds %lld "
@@ -282,7 +287,7 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
                   (long long)workspace_bytes, (long long)need);
     p.part = static_cast<float*>(workspace);
   }
-  return bwd_dispatch(num_layers, dims, p, dtype == MLPMK_DTYPE_BF16, static_cast<hipStream_t>(stream));
+  return bwd_dispatch(num_layers, dims, p, dtype, static_cast<hipStream_t>(stream));
 }
 
 int mlpmk_bwd(int num_layers, const int* dims, int dtype, const void* x, const void* const* w,
@@ -315,12 +320,12 @@ int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t
   *bytes = 0;
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
-  if ((rc = check_elem_dtype(dtype))) return rc;
+  if ((rc = check_bwd_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
-  if (!bwd_supported_dims(num_layers, dims))
-    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
+  if (!bwd_supported_dtype(num_layers, dims, dtype))
+    return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths and dtype");
   if (M == 0) return MLPMK_OK;
-  return bwd_workspace_bytes(num_layers, dims, M, with_dx != 0, dtype == MLPMK_DTYPE_BF16, bytes);
+  return bwd_workspace_bytes(num_layers, dims, M, with_dx != 0, dtype, bytes);
 }
 
 static int check_wn(int num_layers, const int* dims, int dtype) {
@@ -336,8 +341,8 @@ int mlpmk_wn_fwd(int num_layers, const int* dims, int param_dtype, int w_dtype, 
   g_last_error[0] = 0;
   int rc = check_wn(num_layers, dims, param_dtype);
   if (rc) return rc;
-  if (w_dtype != MLPMK_DTYPE_F16 && w_dtype != MLPMK_DTYPE_BF16)
-    return fail(MLPMK_ERR_INVALID_ARG, "w_dtype=%d (1 = fp16, 2 = bf16)", w_dtype);
+  if (w_dtype != MLPMK_DTYPE_F16 && w_dtype != MLPMK_DTYPE_BF16 && w_dtype != MLPMK_DTYPE_F32)
+    return fail(MLPMK_ERR_INVALID_ARG, "w_dtype=%d (0 = fp32, 1 = fp16, 2 = bf16)", w_dtype);
   if ((rc = check_ptr(v, "v")) || (rc = check_ptr(g, "g")) || (rc = check_ptr(w_out, "w_out")) ||
       (rc = check_ptr(inv_norm, "inv_norm")))
     return rc;

@@ -1368,8 +1368,48 @@ static int bwd_workspace_t(int L, const int* dims, int64_t M, bool dx, int64_t* 
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
 }
 
-int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, bool bf, int64_t* bytes) {
-  return bf ? bwd_workspace_t<true>(L, dims, M, dx, bytes) : bwd_workspace_t<false>(L, dims, M, dx, bytes);
+bool tp_supported(int L, const int* dims, int dtype);
+int tp_workspace_bytes(int L, const int* dims, int dtype, int64_t M, int64_t* bytes);
+int tp_dispatch(int L, const int* dims, int dtype, const BwdParams& bp, void* ws, hipStream_t st);
+
+static bool fused_supported(int L, const int* dims) {
+  return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims);
+}
+
+// Batches up to this many rows take the two-pass backward (bwd_tp.hip) where
+// both it and the one-pass megakernel exist: at a few thousand rows the
+// megakernel runs one 128-row round per workgroup on M / 128 CUs.
+#ifndef MLPMK_TP_MAX_ROWS
+#define MLPMK_TP_MAX_ROWS 16384
+#endif
+
+// Which backward runs: 0 the one-pass megakernel, 1 the two-pass backward,
+// -1 neither (an error).  fp32 tensors and widths above 128 have only the
+// two-pass kernels; the recomputing backward (last stash entry NULL) only
+// the one-pass ones.
+static int bwd_path(int L, const int* dims, int dtype, int64_t M, bool recompute) {
+  const bool tp = tp_supported(L, dims, dtype);
+  const bool fused = dtype != MLPMK_DTYPE_F32 && fused_supported(L, dims);
+  if (recompute) return fused ? 0 : -1;
+  if (tp && (!fused || M <= MLPMK_TP_MAX_ROWS)) return 1;
+  return fused ? 0 : -1;
+}
+
+int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int dtype, int64_t* bytes) {
+  const bool bf = dtype == MLPMK_DTYPE_BF16;
+  int64_t fused = 0, two = 0;
+  if (bwd_path(L, dims, dtype, M, false) == 1) {
+    int rc = tp_workspace_bytes(L, dims, dtype, M, &two);
+    if (rc != MLPMK_OK) return rc;
+  }
+  // The one-pass kernels (also for a recomputing call at a two-pass batch
+  // size: whether the last stash entry is NULL is decided per call).
+  if (dtype != MLPMK_DTYPE_F32 && fused_supported(L, dims)) {
+    int rc = bf ? bwd_workspace_t<true>(L, dims, M, dx, &fused) : bwd_workspace_t<false>(L, dims, M, dx, &fused);
+    if (rc != MLPMK_OK) return rc;
+  }
+  *bytes = fused > two ? fused : two;
+  return MLPMK_OK;
 }
 
 // Library-owned workspace of mlpmk_bwd_noalloc, for callers that cannot
@@ -1408,7 +1448,15 @@ int scratch_workspace(void** ptr, int64_t* bytes) {
   return MLPMK_OK;
 }
 
-bool bwd_supported_dims(int L, const int* dims) { return bwd_exact_shape(L, dims) || bwd_generic_dims(L, dims); }
+bool bwd_supported_dims(int L, const int* dims) {
+  return fused_supported(L, dims) || tp_supported(L, dims, MLPMK_DTYPE_F16);
+}
+
+// fp32 tensors: the two-pass backward's shapes (widths up to 128).
+bool bwd_supported_dtype(int L, const int* dims, int dtype) {
+  if (dtype == MLPMK_DTYPE_F32) return tp_supported(L, dims, dtype);
+  return bwd_supported_dims(L, dims);
+}
 
 // The 3- and 5-layer 128-wide networks also run in recompute mode: with a
 // NULL stash entry for h_{L-1} (the forward then does not write it) the
@@ -1444,8 +1492,19 @@ static int bwd_dispatch_t(int L, const int* dims, const BwdParams& p, hipStream_
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths");
 }
 
-int bwd_dispatch(int L, const int* dims, const BwdParams& p, bool bf, hipStream_t st) {
-  return bf ? bwd_dispatch_t<true>(L, dims, p, st) : bwd_dispatch_t<false>(L, dims, p, st);
+int bwd_dispatch(int L, const int* dims, const BwdParams& p, int dtype, hipStream_t st) {
+  const bool recompute = L > 2 && !p.stash[L - 2];
+  int path = bwd_path(L, dims, dtype, p.M, recompute);
+  // The two-pass backward hands dz between its passes through the
+  // workspace: without one (mlpmk_bwd) the one-pass kernels run if they can.
+  if (path == 1 && !p.part) path = (dtype != MLPMK_DTYPE_F32 && fused_supported(L, dims)) ? 0 : -2;
+  if (path == 1) return tp_dispatch(L, dims, dtype, p, p.part, st);
+  if (path == -2)
+    return fail(MLPMK_ERR_INVALID_ARG,
+                "this backward (fp32 tensors or widths above 128) hands dz between two passes through the "
+                "workspace: use mlpmk_bwd_ws");
+  if (path < 0) return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no backward kernel for these widths and dtype");
+  return dtype == MLPMK_DTYPE_BF16 ? bwd_dispatch_t<true>(L, dims, p, st) : bwd_dispatch_t<false>(L, dims, p, st);
 }
 
 }  // namespace mlpmk

@@ -44,3 +44,25 @@ struct BwdParams {
 };
 
 }  // namespace mlpmk
+
+namespace mlpmk {
+
+// Launch parameters of the two-pass backward (bwd_tp.hip).  Tensors are
+// 16-bit (fp16 / bf16 payloads) or fp32 as the launch's element mode says;
+// pointers are untyped here.
+struct TpParams {
+  const void* x;
+  const void* w[kMaxLayersHost];
+  const float* stash[kMaxLayersHost];  // stash[l] = h_{l+1}, fp32 [M, d[l+1]]
+  const void* dout;                    // dL/dout; row r at dout + r * dout_stride
+  int64_t dout_stride;                 // elements; 0 broadcasts row 0, -1 element 0
+  void* dx;                            // nullable
+  float* dw[kMaxLayersHost];           // fp32 [d[l], d[l+1]], accumulated into (fp32 atomics)
+  void* dz[kMaxLayersHost];            // dz_l, l = 0 .. L-2: [M, d[l+1]] in the workspace
+  int64_t M;
+  int64_t chunk_rows;                  // rows per weight-gradient chunk
+  int dims[kMaxLayersHost + 1];
+};
+
+}  // namespace mlpmk
+

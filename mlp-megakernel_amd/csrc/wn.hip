@@ -57,7 +57,7 @@ __device__ __forceinline__ float wn_colsum(float part, float (&red)[kWnRowGroups
 // loop over chunks.
 constexpr int kWnRegRows = 16;
 
-// P: parameter type (float, fp16 or bf16); O: element type of W (fp16 or bf16).
+// P: parameter type (float, fp16 or bf16); O: element type of W (fp16, bf16 or fp32).
 template <class P, class O>
 __global__ __launch_bounds__(kWnThreads) void wn_fwd_kernel(WnLayout lay, const P* __restrict__ v,
                                                             const P* __restrict__ g, O* __restrict__ w,
@@ -179,6 +179,8 @@ static void launch_wn_fwd_p(const WnLayout& lay, int w_dtype, const void* v, con
                             float* inv_norm, hipStream_t st) {
   if (w_dtype == MLPMK_DTYPE_BF16)
     launch_wn_fwd<P, __bf16>(lay, v, g, w_out, inv_norm, st);
+  else if (w_dtype == MLPMK_DTYPE_F32)
+    launch_wn_fwd<P, float>(lay, v, g, w_out, inv_norm, st);
   else
     launch_wn_fwd<P, f16>(lay, v, g, w_out, inv_norm, st);
 }

@@ -63,13 +63,16 @@ def bwd(x, weights, hs, dout, dws, dx=None):
     dt = x.dtype
     dz16 = dout.to(dt).contiguous() if dout.stride(0) != 0 else dout[:1].to(dt).expand_as(dout).contiguous()
     dz32 = dz16.float()
+    f32 = dt == torch.float32  # fp32 tensors: every GEMM in fp32
     for l in range(L - 1, -1, -1):
         need_dh = l > 0 or dx is not None
         if need_dh:
             dh = dz16 @ weights[l].t().contiguous()  # data gradient: 16-bit GEMM, fp32 accumulation
         a = hs[l - 1] if l > 0 else x.float()
         dws[l].add_(a.t() @ dz32)  # weight gradient: fp32 GEMM, right after (interleaved)
-        if l > 0:
+        if l > 0 and f32:
+            dz32 = dz16 = sigmoid_h_mul(hs[l - 1], dh.contiguous())
+        elif l > 0:
             dz32, dz16 = sigmoid_h_mul(hs[l - 1], dh.contiguous(), dz16_dtype=dt)
         elif dx is not None:
             dx.copy_(dh)

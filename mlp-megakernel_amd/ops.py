@@ -49,10 +49,14 @@ def fwd_supported(dims):
     return bool(lib.mlpmk_fwd_supported(len(dims) - 1, p))
 
 
-def bwd_supported(dims):
+def bwd_supported(dims, dtype=None):
+    """True if a backward kernel takes ``dims`` (for tensors of ``dtype``;
+    default: 16-bit tensors, ``mlpmk_bwd_supported``)."""
     lib = _lib.get()
     p, _keep = _lib.int_array(dims)
-    return bool(lib.mlpmk_bwd_supported(len(dims) - 1, p))
+    if dtype is None:
+        return bool(lib.mlpmk_bwd_supported(len(dims) - 1, p))
+    return bool(lib.mlpmk_bwd_supported_dtype(len(dims) - 1, p, _fwd_code(dtype)))
 
 
 def bwd_recompute_supported(dims):
@@ -75,8 +79,8 @@ def _elem_code(dtype, name="x"):
 
 
 def _fwd_code(dtype, name="x"):
-    """Element type of the forward's x, weights and out: fp16, bf16, or fp32
-    (fp32 tensors run with fp16 MFMA operands and write fp32 rows)."""
+    """Element type of x, weights, out (and dout, dx): fp16, bf16, or fp32
+    (fp32 tensors run with bf16 hi/lo split MFMA operands and fp32 rows)."""
     if dtype == torch.float32:
         return _lib.DTYPE_F32
     code = _ELEM.get(dtype)
@@ -254,9 +258,9 @@ def fwd_into(x, weights, out, stash=None):
     ``x`` [M, D] fp16, bf16 or fp32, ``weights`` list of [in, out] and
     ``out`` [M, OUT] of x's dtype, ``stash`` list of L-1 fp32 [M, H_l] tensors
     (an entry may be None: that activation is not written) or None.  All
-    contiguous on one CUDA (HIP) device.  fp32 tensors run with fp16 MFMA
-    operands (the 10-bit mantissa of TF32, fp16's exponent range) and fp32
-    accumulation, softplus and output rows.
+    contiguous on one CUDA (HIP) device.  fp32 tensors run with bf16 hi/lo
+    split MFMA operands (fp32's exponent range, a ~16-bit significand) and
+    fp32 accumulation, softplus and output rows.
     """
     dev = x.device
     if dev.type != "cuda":
@@ -339,7 +343,7 @@ def bwd_workspace_bytes(dims, M, with_dx, device=None, dtype=torch.float16):
     """Bytes of workspace ``mlpmk_bwd_ws`` needs on ``device`` (default: the
     current device) for tensors of ``dtype``; cached per device, shape and M."""
     idx = _cur_device() if device is None or device.index is None else device.index
-    return _workspace_bytes(idx, tuple(int(d) for d in dims), int(M), bool(with_dx), _elem_code(dtype))
+    return _workspace_bytes(idx, tuple(int(d) for d in dims), int(M), bool(with_dx), _fwd_code(dtype))
 
 
 def _workspace_bytes(idx, dims, M, with_dx, code):
@@ -360,7 +364,9 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     """Backward megakernel: accumulates fp32 weight gradients into ``dws``
     (callers zero them first) and writes ``dx`` if given.
 
-    ``dout`` is [M, OUT] fp16 with unit column stride; a row stride of 0
+    ``x``, the weights, ``dout`` and ``dx`` are fp16, bf16 or fp32 (fp32
+    tensors run with bf16 hi/lo split operands: fp32's exponent range).
+    ``dout`` is [M, OUT] of x's dtype with unit column stride; a row stride of 0
     (``t.expand(M, OUT)`` of one row) is passed through as a broadcast, and
     so is one element expanded over both dimensions (what ``loss =
     out.sum()`` hands back: ``MLPMK_DOUT_SCALAR``, no copy).
@@ -372,7 +378,7 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     """
     dev = x.device
     xd = x.dtype
-    code = _elem_code(xd)
+    code = _fwd_code(xd)
     if not _ok(x, xd, dev):
         _require(x, "x", xd, dev)
     for i, w in enumerate(weights):
@@ -421,7 +427,7 @@ def wn_fwd(dims, v_all, g_all, w_all, inv_all):
     dt = _param_dtype(v_all)
     _require(v_all, "v_all", v_all.dtype, dev)
     _require(g_all, "g_all", v_all.dtype, dev)
-    wcode = _elem_code(w_all.dtype, "w_all")
+    wcode = _fwd_code(w_all.dtype, "w_all")
     _require(w_all, "w_all", w_all.dtype, dev)
     _require(inv_all, "inv_all", torch.float32, dev)
     nw = sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1))

@@ -50,10 +50,11 @@ def test_version_and_status_strings():
      ((128, 64, 128, 128), True, True), ((32, 128, 3), True, True), ((16, 48, 80, 112, 7), True, True),
      ((128,) * 5, True, True), ((64, 128, 128, 1), True, True),
      # streamed-weight forward: widths up to 256 (multiples of 16, any output
-     # width up to 256); their backward is the library-GEMM fallback, not the
-     # fused kernel
-     ((128, 256, 128), True, False), ((128, 256, 256, 128), True, False), ((256, 64, 200), True, False),
-     ((128, 128, 129), True, False), ((16, 256, 256, 256, 256, 256), True, False),
+     # width up to 256); the two-pass backward takes them when the output
+     # width is a multiple of 8 (else the modules train through the
+     # library-GEMM fallback)
+     ((128, 256, 128), True, True), ((128, 256, 256, 128), True, True), ((256, 64, 200), True, True),
+     ((128, 128, 129), True, False), ((16, 256, 256, 256, 256, 256), True, True), ((128, 256, 132), True, False),
      ((128, 128), False, False), ((100, 128, 128, 128), False, False), ((128, 136, 128, 128), False, False),
      ((128, 272, 128), False, False), ((128, 128, 257), False, False), ((128, 248, 128), False, False),
      ((128,) * 7, False, False)],
@@ -112,7 +113,9 @@ def test_bwd_validation_codes():
     assert call(m=-1) == INVALID
     assert call(stride=-2) == INVALID  # negative, and not MLPMK_DOUT_SCALAR
     assert call(dw=None) == INVALID
-    assert call(dtype=0) == UNSUPPORTED
+    # fp32 tensors run the two-pass backward, which hands dz between its
+    # passes through the workspace: mlpmk_bwd (none) refuses them
+    assert call(dtype=0) == INVALID and b"mlpmk_bwd_ws" in lib.mlpmk_last_error()
     assert call(dtype=3) == INVALID
     if ops.bwd_supported(d):
         assert call(stride=64) == INVALID  # below the output width
@@ -179,7 +182,7 @@ def test_wn_and_copy_validation_codes():
     lib = _lib.get()
     pd, _k = _lib.int_array([128, 128, 128, 128])
     assert lib.mlpmk_wn_fwd(3, pd, 7, 1, A, A, A, A, None) == INVALID  # bad dtype
-    assert lib.mlpmk_wn_fwd(3, pd, 0, 0, A, A, A, A, None) == INVALID  # W must be fp16 or bf16
+    assert lib.mlpmk_wn_fwd(3, pd, 0, 3, A, A, A, A, None) == INVALID  # W is fp32, fp16 or bf16
     assert b"w_dtype" in lib.mlpmk_last_error()
     assert lib.mlpmk_wn_fwd(3, pd, 0, 1, A, None, A, A, None) == INVALID
     assert lib.mlpmk_wn_bwd(3, pd, 1, A, A, A, A, A + 2, A, None) == MISALIGNED
@@ -215,11 +218,10 @@ def test_drop_in_modules_import_without_gpu():
     assert cfg(40000, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 4)
     assert cfg(4194304, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 16)
     assert cfg(4096, 128, 128, 128, 128, num_cus=8) == (32, 128, 16, 16, 16, 12)
-    # fp32 tensors: the persistent kernel only, 4 waves up to 4 blocks per CU,
-    # then 8 (4 for the 3-layer runtime-width kernel)
+    # fp32 tensors: their feature-split kernel at every M (32-row blocks, 4 waves)
     assert cfg(4096, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 4)
-    assert cfg(1048576, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 8)
-    assert cfg(4194304, 32, 64, 64, 16, fp32=True) == (32, 16, 16, 16, 16, 8)
+    assert cfg(1048576, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 4)
+    assert cfg(4194304, 32, 64, 64, 16, fp32=True) == (32, 16, 16, 16, 16, 4)
     assert cfg(1048576, 64, 64, 64, 64, fp32=True) == (32, 64, 16, 16, 16, 4)
     assert callable(kernel._fused_mlp_fwd) and kernel.Model and kernel.ModelNew
 

@@ -1,6 +1,8 @@
 """Hidden widths above 128 (up to 256): the streamed-weight forward
-(``fwd_wide.hip``) against the CPU oracle, and training of the drop-in modules
-at H = 256 through the library-GEMM fallback backward.
+(``fwd_wide.hip``) and the two-pass backward (``bwd_tp.hip``: data gradients
+with streamed fragments, weight gradients by 64 x 64 blocks) against the CPU
+oracle, and training of the drop-in modules at H = 256 (output widths that
+are not a multiple of 8 train through the library-GEMM fallback).
 
 The reference's kernel compiles for any hidden width (constexpr tile loops,
 /root/reference/kernel.py:60-123; its modules take H, README.md:62,68) and
@@ -145,10 +147,14 @@ def _check_grad(got, ref, what):
     assert worst <= 0 and frob < 1e-2, f"{what}: worst excess {worst:.3g}, rel frob {frob:.3g}"
 
 
-@pytest.mark.parametrize("H,n_layers", [(256, 3), (192, 5)])
-def test_module_with_wide_hidden_trains(H, n_layers):
+@pytest.mark.parametrize("H,n_layers,out_f", [(256, 3, 128), (192, 5, 128), (256, 3, 100)])
+def test_module_with_wide_hidden_trains(H, n_layers, out_f):
+    # (out_features 100, not a multiple of 8: the library-GEMM fallback backward)
+    from mlpmk import autograd as mag
+
     torch.manual_seed(3)
-    model = fused_mlp.FusedMLPSoftplus(D=128, H=H, out_features=128, n_layers=n_layers).cuda().half()
+    model = fused_mlp.FusedMLPSoftplus(D=128, H=H, out_features=out_f, n_layers=n_layers).cuda().half()
+    assert mag._fused_bwd_supported(tuple(model.dims)) == (out_f % 8 == 0)
     x = torch.randn(4096, 128, device="cuda").half().requires_grad_(True)
     out = model(x)
     out.sum().backward()
@@ -185,3 +191,69 @@ def test_weight_norm_module_with_wide_hidden_trains():
     dv, dg = zip(*[orc.wn_backward(dws[i], vs[i], gs[i]) for i in range(len(vs))])
     _check_grad(model.v_all.grad.cpu().numpy(), np.concatenate([d.reshape(-1) for d in dv]), "dv")
     _check_grad(model.g_all.grad.cpu().numpy(), np.concatenate(dg), "dg")
+
+
+# The two-pass backward at widths above 128, through the C ABI (ops.bwd ->
+# mlpmk_bwd_ws), against the oracle's closed-form backward on the oracle's
+# own hidden activations (rounded to fp16 as the kernels' operands are).
+def _check_dw(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max()
+    worst = np.max(np.abs(got - ref) - (2e-2 * np.abs(ref) + 2e-3 * scale))
+    frob = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert worst <= 0 and frob < 1e-2, f"{what}: worst excess {worst:.3g} (scale {scale:.3g}), rel frob {frob:.3g}"
+
+
+@pytest.mark.parametrize("dims,m,with_dx,dout_mode", [
+    ((128, 256, 256, 128), 4096, True, "scalar"),
+    ((128, 256, 256, 128), 4096, False, "dense"),
+    ((128, 256, 256, 128), 131072, False, "scalar"),
+    ((128, 256, 256, 128), 131072, True, "dense"),
+    ((256, 256, 256, 256), 8192, True, "dense"),
+    ((128, 192, 256, 64), 4096, True, "row"),
+    ((256, 64, 200), 999, True, "dense"),
+    ((128, 256, 256, 256, 256, 128), 4096, True, "scalar"),
+    ((96, 208, 160, 256, 48), 2048, True, "dense"),
+])
+def test_wide_two_pass_backward_matches_oracle(dims, m, with_dx, dout_mode):
+    assert ops.bwd_supported(list(dims))
+    x, ws = orc.make_inputs(dims, m, seed=m + len(dims))
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    rng = np.random.default_rng(m)
+    if dout_mode == "scalar":
+        dnp = np.full((m, dims[-1]), 0.5, np.float32)
+        dout = torch.full((), 0.5, dtype=torch.float16, device="cuda").expand(m, dims[-1])
+    elif dout_mode == "row":
+        row = rng.standard_normal(dims[-1]).astype(np.float16)
+        dnp = np.broadcast_to(row.astype(np.float32), (m, dims[-1]))
+        dout = torch.from_numpy(row).cuda().reshape(1, -1).expand(m, dims[-1])
+    else:
+        d16 = rng.standard_normal((m, dims[-1])).astype(np.float16)
+        dnp = d16.astype(np.float32)
+        dout = torch.from_numpy(d16).cuda()
+    dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(len(dims) - 1)]
+    dx = torch.empty_like(xd) if with_dx else None
+    ops.bwd(xd, wd, hs, dout, dws, dx)
+    torch.cuda.synchronize()
+    _, ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=True)
+    rdws, rdx = orc.backward(x, ws, ref_h, dnp, need_dx=with_dx)
+    for i in range(len(dws)):
+        _check_dw(dws[i].cpu().numpy(), rdws[i], f"{dims} M={m} dW{i + 1}")
+    if with_dx:
+        _check(dx.float().cpu().numpy(), rdx, f"{dims} M={m} dx")
+
+
+def test_wide_backward_needs_the_workspace():
+    # The two-pass backward hands dz between its passes through the
+    # workspace: mlpmk_bwd (none) refuses widths above 128.
+    dims = (128, 256, 128)
+    x, ws = orc.make_inputs(dims, 256, seed=1)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    _, hs = ops.fwd(xd, wd, stash=True)
+    dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(2)]
+    with pytest.raises(ops.MlpmkError, match="mlpmk_bwd_ws"):
+        ops.bwd(xd, wd, hs, torch.ones((256, 128), dtype=torch.float16, device="cuda"), dws, workspace=False)

@@ -3,9 +3,11 @@ place of a caller workspace) through the C ABI, against ``mlpmk_bwd_ws`` on
 the same inputs and against the CPU oracle.
 
 Two calls in a row share the device's scratch array, the second with a
-smaller batch; both must match the workspace entry point bit for bit (with
-grids of 64+ workgroups both sum the partials in one fixed order) and the
-oracle to the weight-gradient tolerance of the other backward tests.  A
+smaller batch; both must match the workspace entry point -- bit for bit
+where the one-pass megakernel runs (its partials are summed in one fixed
+order), to fp32 summation order where the two-pass backward does (up to
+16,384 rows: fp32 atomics) -- and the oracle to the weight-gradient
+tolerance of the other backward tests.  A
 shape whose workspace exceeds the array is rejected before any launch.
 """
 import ctypes
@@ -99,7 +101,10 @@ def test_noalloc_matches_workspace_entry_on_two_calls(dims, m1, m2, with_dx, rec
         got_dws, got_dx = _grads("noalloc", dims, xd, wd, hs, dout, with_dx)
         ref_dws, ref_dx = _grads("ws", dims, xd, wd, hs, dout, with_dx)
         for i, (a, b) in enumerate(zip(got_dws, ref_dws)):
-            assert torch.equal(a, b), f"call {call} (M={m}): dW{i + 1} differs from mlpmk_bwd_ws"
+            if m > 16384:
+                assert torch.equal(a, b), f"call {call} (M={m}): dW{i + 1} differs from mlpmk_bwd_ws"
+            else:  # two-pass backward: fp32 atomics, any summation order
+                assert torch.allclose(a, b, rtol=1e-5, atol=1e-6 * float(b.abs().max())), f"call {call}: dW{i + 1}"
         if with_dx:
             assert torch.equal(got_dx, ref_dx), f"call {call} (M={m}): dx differs from mlpmk_bwd_ws"
         _check_oracle(dims, x, ws, hs, got_dws, got_dx, with_dx)
