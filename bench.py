@@ -382,12 +382,14 @@ def sustained(torch, step, ms_hint, seconds=0.6):
     return ms, n
 
 
-def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, dtype=None):
+def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, dtype=None, hidden=128):
     """One training step of BASELINE config 5 through the drop-in module:
     weight norm + forward megakernel (fp32 stash), loss = out.sum(), backward
     megakernel + weight-norm backward, x without grad.  Timed with HIP events
     around `steps` back-to-back autograd steps (Python dispatch included), and
-    around `steps` replays of the whole step captured as one HIP graph."""
+    around `steps` replays of the whole step captured as one HIP graph.
+    ``dtype`` is x's type (fp32 x with the module's fp32 parameters runs the
+    fp32-tensor kernels); ``hidden`` the hidden width H."""
     import fused_mlp
     from mlpmk import autograd as mag
 
@@ -395,18 +397,19 @@ def train_step_bench(torch, m, steps=50, warmup=10, n_layers=3, recompute=None, 
     if recompute is not None:
         mag.RECOMPUTE = recompute
     try:
-        return _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype or torch.float16)
+        return _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype or torch.float16, hidden)
     finally:
         mag.RECOMPUTE = policy
 
 
-def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
+def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype, hidden=128):
     from mlpmk import autograd as mag
 
     torch.manual_seed(0)
-    model = fused_mlp.FusedMLPSoftplusWN(n_layers=n_layers).cuda()
+    model = fused_mlp.FusedMLPSoftplusWN(H=hidden, n_layers=n_layers).cuda()
     dims = tuple(model.dims)
-    rc = mag._use_recompute(dims, m, False)
+    kdt = mag.kernel_dtype(torch.empty(0, dtype=dtype), dims)
+    rc = mag._use_recompute(dims, m, False, kdt)
     # Steps rotate over nx inputs (up to 256 MB of x, at most 8 buffers) so
     # that x is not re-read from the Infinity Cache; the stash a step's
     # forward writes is read back by the same step's backward, as in training.
@@ -444,9 +447,11 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
     # per row: x + out + stash written in the forward; dout, stash, x read
     # back (no dx).  Flops: forward 2*sum(in*out), dgrad of layers 1.., wgrad
     # (+ the recomputed layer).
-    nstash = n_layers - 1 - (1 if rc else 0)
-    nbytes = 256 + 256 + 512 * nstash + 256 + 512 * nstash + 256
-    flop = 32768 * (3 * n_layers - 1 + (1 if rc else 0))
+    es = torch.empty((), dtype=kdt).element_size()
+    stash_w = sum(dims[1:-1]) - (dims[-2] if rc else 0)
+    nbytes = es * dims[0] + es * dims[-1] + 4 * stash_w + es * dims[-1] + 4 * stash_w + es * dims[0]
+    lflop = [2 * dims[i] * dims[i + 1] for i in range(n_layers)]
+    flop = sum(lflop) + sum(lflop[1:]) + sum(lflop) + (lflop[-2] if rc else 0)  # fwd, dgrad (no dx), wgrad
     return {
         "ms_per_step": round(ms, 5),
         "rows_per_s": m / (ms * 1e-3),
@@ -459,7 +464,8 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype):
                     "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..3, then 2..0) + wn_bwd",
         "x_buffers": nx,
         "recompute_h_last": rc,
-        "dtype": str(dtype).replace("torch.", ""),
+        "dims": list(dims),
+        "dtype": str(kdt).replace("torch.", ""),
     }
 
 
@@ -722,13 +728,19 @@ def main():
             "5l128 M=65536": fwd_bench(torch, ops, CONFIG_DIMS["5l128"], 65536, False),
             "5l128 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["5l128"], 1048576, False),
             "narrow M=4194304": fwd_bench(torch, ops, CONFIG_DIMS["narrow"], 4194304, True),
-            # fp32 tensors (fp16 MFMA operands, fp32 rows: twice the bytes)
+            # fp32 tensors (bf16 hi/lo split operands, fp32 rows: twice the bytes)
             "3l128 fp32 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["3l128"], 1048576, False, dtype=torch.float32),
             # hidden width 256: weights streamed through LDS (fwd_wide.hip)
             "3l256 M=1048576": fwd_bench(torch, ops, CONFIG_DIMS["3l256"], 1048576, False),
         }
         result["latency_sweep"] = latency_sweep(torch, ops, CONFIG_DIMS["3l128"])
         result["training"] = {str(mt): train_step_bench(torch, mt) for mt in (4096, 16384, 131072)}
+        # fp32 tensors (bf16 hi/lo split operands) and hidden width 256 (the
+        # two-pass backward at every M), same step
+        result["training_fp32"] = {str(mt): train_step_bench(torch, mt, steps=20, warmup=5, dtype=torch.float32)
+                                   for mt in (4096, 131072)}
+        result["training_h256"] = {str(mt): train_step_bench(torch, mt, steps=20, warmup=5, hidden=256)
+                                   for mt in (4096, 131072)}
 
     if args.train:
         result["training_5l"] = {str(mt): train_step_bench(torch, mt, n_layers=5) for mt in (65536, 131072)}

@@ -171,14 +171,6 @@ __device__ __forceinline__ f16 scaled_weight(f16 w, float sc) {
   asm volatile("" : "+v"(t));
   return f32_to_elem<BF>(t);
 }
-// An fp32 weight: w * sc rounded to fp32, then once to the 16-bit operand.
-template <bool BF = false>
-__device__ __forceinline__ f16 scaled_weight(float w, float sc) {
-  float t = w * sc;
-  asm volatile("" : "+v"(t));
-  return f32_to_elem<BF>(t);
-}
-
 template <bool BF = false>
 __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, float a4, float a5,
                                        float a6, float a7) {
@@ -240,7 +232,6 @@ struct Net {
   static constexpr bool gen = false;  // widths fixed at compile time
   static constexpr bool rc = false;   // backward: h_{L-1} read from the stash (see Recompute in bwd.hip)
   static constexpr bool bf = false;   // 16-bit tensors are fp16 (see BF16)
-  static constexpr bool io32 = false; // x, W and out are 16-bit tensors (see F32IO)
   static constexpr int L = sizeof...(Ds) - 1;
   static constexpr int d[sizeof...(Ds)] = {Ds...};
   // K-steps (16 input features each) and 32-row output blocks of layer l.
@@ -286,15 +277,6 @@ struct Gen : Base {
 template <class Base>
 struct BF16 : Base {
   static constexpr bool bf = true;
-};
-// The same network with fp32 tensors x, W and out (forward): x rows and
-// weights are rounded to fp16 MFMA operands in the kernel (the 10-bit
-// mantissa of the reference's TF32 tl.dot operands, fp16's exponent range),
-// accumulation and softplus stay fp32, and out is stored in fp32 straight
-// from the accumulators.
-template <class Base>
-struct F32IO : Base {
-  static constexpr bool io32 = true;
 };
 template <bool B, class N>
 struct ElemNet {

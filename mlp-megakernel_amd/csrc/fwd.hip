@@ -1,5 +1,5 @@
 // Forward megakernel host dispatch for fp16 and bf16 tensors (the kernels are
-// templates in fwd_kernel.h; fp32 tensors dispatch through fwd_f32.hip).
+// templates in fwd_kernel.h; fp32 tensors dispatch through fwd_x3.hip).
 #include "fwd_kernel.h"
 
 

@@ -1,7 +1,6 @@
 #pragma once
 // Forward megakernel for gfx950 (MI355X): kernel templates and their launch
-// templates, shared by the fp16/bf16 dispatch (fwd.hip) and the fp32-tensor
-// dispatch (fwd_f32.hip).
+// templates for 16-bit (fp16 / bf16) tensors, dispatched by fwd.hip.
 //
 // Replaces the reference's Triton `_fused_mlp_recompute` (/root/reference/kernel.py:60-123)
 // and its training-forward variant with stored activations
@@ -30,7 +29,6 @@
 //  * Each layer is software-pipelined by 32-feature output block: the MFMA
 //    chain of block mb+1 is issued ahead of block mb's activation, so the
 //    matrix core and the VALU work concurrently within one wave.
-#include <type_traits>
 
 #include "device_common.h"
 #include "params.h"
@@ -68,9 +66,7 @@ __device__ __forceinline__ f16x8 weight_fragment(const FwdParams& p, int l, int 
   f16x8 v;
   if (of < Nout) {
     const int k0 = 16 * s + 8 * g;
-    // fp32 weights (F32IO) are rounded once from w * scale, like fp16 ones.
-    typedef typename std::conditional<N::io32, float, f16>::type WT;
-    const WT* src = reinterpret_cast<const WT*>(p.w[l]) + (int64_t)k0 * Nout + of;
+    const f16* src = p.w[l] + (int64_t)k0 * Nout + of;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (N::gen)
@@ -167,9 +163,7 @@ __device__ __forceinline__ void stage_store_any(f16x8* lds, const f16x8 (&r)[8],
 template <class N, int NT, int RF>
 __device__ __forceinline__ void stage_weights(const FwdParams& p, f16x8* lds) {
   constexpr int TOTAL = StageTasks<N>::total();
-  // fp32 weights (F32IO) take the column gathers: their task rows would need
-  // twice the registers, and the staging is once per workgroup.
-  if constexpr (TOTAL >= NT && !N::gen && !N::io32) {
+  if constexpr (TOTAL >= NT && !N::gen) {
     constexpr int TPT = (TOTAL + NT - 1) / NT;
     f16x8 r[TPT][8];
 #pragma unroll
@@ -217,7 +211,7 @@ struct SplitStaging {
     return o;
   }
   static constexpr int kGather = kTasks ? 1 : kSlotOff(N::L);
-  static_assert(!N::gen && !N::io32, "runtime-width and fp32-tensor networks stage in one phase");
+  static_assert(!N::gen, "runtime-width networks stage in one phase");
   f16x8 r[TPT][8];   // task rows (kTasks)
   f16x8 g[kGather];  // raw gathered fragment lanes, unscaled (!kTasks)
 
@@ -323,7 +317,7 @@ struct LdsPlan {
   static constexpr int kTileChunks = 32 * NB * kRowChunks;
   static constexpr int wbytes = N::nfrag() * 1024;
   static constexpr bool stage =
-      !N::gen && !N::io32 && N::d[N::L] % 64 == 0 && wbytes + NW * kTileChunks * 16 + 16 <= kLds;
+      !N::gen && N::d[N::L] % 64 == 0 && wbytes + NW * kTileChunks * 16 + 16 <= kLds;
   static constexpr int stage_bytes = stage ? NW * kTileChunks * 16 : 0;
   static constexpr int reg_frags = wbytes + stage_bytes + 16 <= kLds ? 0 : 1;
   static constexpr bool claim = wbytes - reg_frags * 1024 + stage_bytes + 16 <= kLds;
@@ -355,9 +349,8 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
   BlockIO io;
 #pragma unroll
   for (int l = 0; l <= N::L; ++l) io.dl[l] = N::gen ? p.dims[l] : N::d[l];
-  constexpr uint32_t E = N::io32 ? 4u : 2u;  // bytes per element of x and out
-  io.x = make_rsrc(reinterpret_cast<const char*>(p.x) + row0 * io.dl[0] * E, rows * io.dl[0] * E);
-  io.out = make_rsrc(reinterpret_cast<const char*>(p.out) + row0 * io.dl[N::L] * E, rows * io.dl[N::L] * E);
+  io.x = make_rsrc(p.x + row0 * io.dl[0], rows * io.dl[0] * 2u);
+  io.out = make_rsrc(p.out + row0 * io.dl[N::L], rows * io.dl[N::L] * 2u);
   if constexpr (STASH) {
     io.stash_on = 0;
 #pragma unroll
@@ -370,25 +363,9 @@ __device__ __forceinline__ BlockIO block_io(const FwdParams& p, int64_t row0) {
   return io;
 }
 
-// Eight fp32 x values (one K-step piece of a row) of an F32IO network, as
-// loaded; converted to the fp16 operand only where the MFMA reads them.
-struct X32 {
-  i32x4 a, b;
-};
-// Register type of one K-step piece of an x row.
-template <bool IO32>
-struct XPiece {
-  typedef i32x4 type;
-};
-template <>
-struct XPiece<true> {
-  typedef X32 type;
-};
-
 // Rows of x as raw dwords: kept as i32x4 until the MFMA reads them, because an
 // f16x8 destination makes the compiler re-pack the halves right after the load
-// (v_bfi copies), which waits for the load at the point of issue.  fp32 rows
-// (X32) are two 16-byte loads per piece.
+// (v_bfi copies), which waits for the load at the point of issue.
 // For a runtime-width network rows are D wide (a multiple of 16): K-steps
 // past D (a wave-uniform test) are zero without a load.
 template <int KS, int NB, bool GEN = false>
@@ -403,25 +380,9 @@ __device__ __forceinline__ void load_rows(i32x4 (&xa)[KS][NB], rsrc_t xr, int n,
         xa[s][nb] = __builtin_amdgcn_raw_buffer_load_b128(xr, ((nb * 32 + n) * D + 16 * s + 8 * g) * 2, 0, 0);
     }
 }
-template <int KS, int NB, bool GEN = false>
-__device__ __forceinline__ void load_rows(X32 (&xa)[KS][NB], rsrc_t xr, int n, int g, int D = KS * 16) {
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      if (GEN && 16 * s >= D) {
-        xa[s][nb] = X32{};
-      } else {
-        const int off = ((nb * 32 + n) * D + 16 * s + 8 * g) * 4;
-        xa[s][nb].a = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
-        xa[s][nb].b = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
-      }
-    }
-}
-
 // x rows of the 32*NB-row block starting at row0 (Gen networks: true width).
 template <class N, int NB>
-__device__ __forceinline__ void load_block_x(typename XPiece<N::io32>::type (&xa)[N::ks(0)][NB], const FwdParams& p,
+__device__ __forceinline__ void load_block_x(i32x4 (&xa)[N::ks(0)][NB], const FwdParams& p,
                                              int64_t row0, int lane) {
   load_rows<N::ks(0), NB, N::gen>(xa, block_io<N, false, 32 * NB>(p, row0).x, lane & 31, lane >> 5,
                                   N::gen ? p.dims[0] : N::d[0]);
@@ -429,11 +390,6 @@ __device__ __forceinline__ void load_block_x(typename XPiece<N::io32>::type (&xa
 
 __device__ __forceinline__ f16x8 as_f16x8(f16x8 v) { return v; }
 __device__ __forceinline__ f16x8 as_f16x8(i32x4 v) { return __builtin_bit_cast(f16x8, v); }
-// fp32 x -> fp16 operand (RNE, as the fp16 tensors' producers round).
-__device__ __forceinline__ f16x8 as_f16x8(const X32& v) {
-  const f32x4 a = __builtin_bit_cast(f32x4, v.a), b = __builtin_bit_cast(f32x4, v.b);
-  return pack8<false>(a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]);
-}
 
 // Steps of one row block: step t is output block mb(t) (32 features) of
 // layer layer(t), layers in order.
@@ -600,39 +556,7 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const uint32_t elem = (uint32_t)((nb * 32 + n) * Nout + 32 * mb + 8 * g);
-    if constexpr (LAST && N::io32) {
-      // fp32 output rows (F32IO) straight from the accumulators: piece q =
-      // registers 4q .. 4q+3 = features c + 16 (q >> 1) + 4 (q & 1) + [0..3],
-      // one 16-byte store each, default cache policy so that L2 merges the
-      // pieces of a row's lines (as for the stash); for a runtime output
-      // width the piece that straddles it, and every piece when rows are not
-      // 16-byte aligned (width not a multiple of 4), is stored element by
-      // element.
-      const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
-      const int OW = N::gen ? io.dl[N::L] : Nout;
-      const int c = 32 * mb + 8 * g;
-      const uint32_t e = (uint32_t)((nb * 32 + n) * OW + c);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int df = 16 * (q >> 1) + 4 * (q & 1);
-        if ((!N::gen || OW % 4 == 0) && c + df + 4 <= OW) {
-          buf_store16<kStashStore>((f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}, io.out, (e + df) * 4);
-        } else if constexpr (N::gen) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            // Each element through an empty asm into a VGPR of its own:
-            // taken straight from the accumulator tuple, the 4-byte store
-            // builtin was given element 0 every time (as with the 2-byte
-            // stores of the 16-bit path).
-            float t = v[4 * q + j];
-            asm volatile("" : "+v"(t));
-            if (c + df + j < OW)
-              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, t), io.out, (int)((e + df + j) * 4), 0,
-                                                    kStashStore);
-          }
-        }
-      }
-    } else if constexpr (LAST && STAGE) {
+    if constexpr (LAST && STAGE) {
       const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
       const int row = nb * 32 + n;
       const int c = 4 * (mb & 1) + g;  // chunk within the staged 128-byte row segment
@@ -771,7 +695,7 @@ __device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane
 template <class N, int NB, int KSM>
 struct Chain {
   static constexpr int KS0 = N::ks(0);
-  typename XPiece<N::io32>::type xa[KS0][NB];  // x rows of the block (refilled with the next block's)
+  i32x4 xa[KS0][NB];             // x rows of the block (refilled with the next block's)
   f16x8 b0[KSM][NB], b1[KSM][NB];  // hidden activations, ping-pong between layers
   f32x16 acc[2][NB];             // accumulators of the current and the next step
   Frags<KSM> fr;                 // fragments of the next chain to issue

@@ -12,19 +12,30 @@
 // backward (bwd_tp.hip) uses the same operands, so a training step keeps
 // fp32's range end to end.
 //
-// Mapping: the feature split of fwd_split.hip.  A workgroup of NWV waves
-// (one per 32-feature output block of the widest layer, one per SIMD) runs
-// 32-row blocks, persistent over the batch; wave w computes output features
-// [32w, 32w + 32) of every layer in the transposed orientation (MFMA M =
-// features, N = rows, K = input features), its A fragments (hi and lo) held
-// in registers for the whole kernel where they fit (up to 3 layers) and
-// read from L2 per block otherwise.  Layers hand their activations to the
-// next as B operands through two LDS tiles [32 rows][features] (hi, lo).
+// Mapping: the feature split of fwd_split.hip, in the transposed
+// orientation (MFMA M = features, N = rows, K = input features): 32-row
+// blocks, persistent over the batch; wave w of a layer's group computes
+// output features [32w, 32w + 32) of that layer, its A fragments (hi and
+// lo) resident in AGPRs, which the MFMA reads directly.  Layers hand their
+// activations on as B operands through LDS tiles [32 rows][features] (hi,
+// lo).
+//
+// 2 and 3 layers (fwd_x3p_kernel): a two-stage layer pipeline.  Stage A
+// (NWV waves) runs layer 0 of block t while stage B (NWV more waves, one
+// per SIMD beside an A wave) runs layer 1 of block t - 1 and layer 2 of
+// block t - 2; every hand-over crosses the one barrier of a step, so the
+// two waves of a SIMD overlap one's softplus and x conversion with the
+// other's MFMA chains.  A single wave per SIMD running all layers waits out
+// every chain, barrier and softplus in turn: 3.1x slower at 3 x 128.
+// 4 and 5 layers (fwd_x3_kernel, whose fragments need the whole register
+// file): one wave per output block runs every layer of a block in turn.
 //
 // Softplus in base 2: u = z log2(e), softplus(z) = ln2 * sp2(u) with sp2(u)
 // = log2(1 + 2^u), and u itself where 2^u overflows (u >= 128, z > 88.7; the
-// reference's threshold branch, kernel.py:108, gives z there too).  The
-// fp32 stash (training) holds softplus(z) as the backward reads it.
+// reference's threshold branch, kernel.py:108, gives z there too).  The two
+// scales are folded into the first and last layers' weights (fscale), so a
+// hidden activation is one exp2 and one log2.  The fp32 stash (training)
+// holds softplus(z) as the backward reads it.
 #include "device_common.h"
 #include "host_common.h"
 #include "params.h"
@@ -54,8 +65,15 @@ struct FxGeo {
       while (m < N::d[l]) m *= 2;
     return m;
   }
+  static constexpr int pow2_32(int v) {
+    int m = 32;
+    while (m < v) m *= 2;
+    return m;
+  }
   static constexpr int NWV = nwv(), KSM = ksm(), TW = tw(), CH = TW / 8;
-  static constexpr bool RES = L <= 3;  // fragments resident in registers
+  static constexpr int CHX = pow2_32(N::d[0]) / 8;  // chunks of 8 features per x-tile row
+  static constexpr bool PIPE = L <= 3;  // the two-stage pipeline
+  static constexpr int THREADS = (PIPE ? 2 : 1) * NWV * 64;
   static constexpr bool valid() {
     for (int i = 0; i < L; ++i)
       if (N::d[i] > 128 || N::d[i] % 16 != 0) return false;
@@ -63,24 +81,44 @@ struct FxGeo {
   }
 };
 
+// Scale folded into W_l: log2 e on the first layer, ln 2 on the last.  The
+// first layer's sums then come out as u = z log2 e, hidden layers carry
+// g = sp2(u) = softplus(z) / ln 2 into unscaled weights (the ln 2 of one
+// layer and the log2 e of the next cancel), and the last layer's ln 2 turns
+// its g inputs back into h.
 template <class N>
-struct FxWave {
+__device__ __forceinline__ float fscale(int l) {
+  return (l == 0 ? kLog2e : 1.0f) * (l == N::L - 1 ? kLn2 : 1.0f);
+}
+
+// One exchange tile: [hi, lo][32 rows * CH chunks of 8 features].
+template <int CH>
+using XTile = f16x8[2][32 * CH];
+
+// What a wave of either kernel does with one block of one layer.  w is the
+// wave's output block (features [32w, 32w + 32)).
+template <class N, bool STASH>
+struct FxOps {
   using G = FxGeo<N>;
   static constexpr int L = N::L, CH = G::CH, EM = EM_F32;
   const FwdParams& p;
-  f16x8 (*tile)[2][32 * CH];  // [2][hi, lo][32 * CH]
-  int lane, n, g, w;
-  int par = 0;
-  Opnd fr[G::RES ? L : 1][G::KSM];  // this wave's A fragments (output block w)
-  Opnd B[G::KSM];                   // B operands of the current layer: row n
+  int n, g, w;
 
-  __device__ __forceinline__ bool owns(int l) const { return 32 * w < dimw<N>(p, l + 1); }
+  // Whether this wave has output features in layer l (always, for fixed
+  // networks whose every layer has NWV output blocks).
+  template <int l>
+  __device__ __forceinline__ bool owns() const {
+    if constexpr (!N::gen && G::blocks(l) == G::NWV) return true;
+    return 32 * w < dimw<N>(p, l + 1);
+  }
 
-  // Fragment (block w, K-step s) of layer l: lane (i, g) holds
-  // W_l[16s + 8g + j][outfeat(w, i)], j = 0..7 -- for fixed (s, g, j) the 32
-  // lanes of a half-wave read 32 consecutive columns of one row (128 bytes).
-  // Rows past the true input width read zeros through the resource; columns
-  // past the true output width are masked.
+  // Fragment (block w, K-step s) of layer l, scaled: lane (i, g) holds
+  // fscale(l) * W_l[16s + 8g + j][outfeat(w, i)], j = 0..7 -- for fixed
+  // (s, g, j) the 32 lanes of a half-wave read 32 consecutive columns of one
+  // row (128 bytes).  Rows past the true input width read zeros through the
+  // resource; columns past the true output width are masked.  The fragments
+  // are then pinned to AGPRs: left to itself the allocator parks them there
+  // and copies them back to VGPRs before every MFMA.
   template <int l>
   __device__ __forceinline__ void load_frags(Opnd (&f)[G::KSM]) const {
     const int K = dimw<N>(p, l), Nout = dimw<N>(p, l + 1);
@@ -93,28 +131,60 @@ struct FxWave {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int row = 16 * s + 8 * g + j;
-        v[j] = ok ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (row * Nout + col) * 4, 0, 0))
+        v[j] = ok ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (row * Nout + col) * 4, 0, 0)) *
+                        fscale<N>(l)
                   : 0.0f;
       }
       f[s] = make_op<EM>(v);
-    }
-  }
-  template <int l = 0>
-  __device__ __forceinline__ void load_all_frags() {
-    if constexpr (l < L) {
-      if (owns(l)) load_frags<l>(fr[l]);
-      load_all_frags<l + 1>();
+      asm volatile("" : "+a"(f[s].h), "+a"(f[s].l));
     }
   }
 
-  // x rows from row0 as B operands: lane (n, g), K-step s: x[row n][16s + 8g + 0..7].
-  __device__ __forceinline__ void load_x(int64_t row0) {
+  // x rows from row0, as loaded (lane (n, g), K-step s: x[row n][16s + 8g +
+  // 0..7]).  Past the batch the resource is empty and the rows read as zeros.
+  __device__ __forceinline__ void load_x(f32x4 (&xr)[G::ks(0)][2], int64_t row0) const {
     const int D = dimw<N>(p, 0);
     const rsrc_t r = make_rsrc(reinterpret_cast<const float*>(p.x) + row0 * D, rows_at(p.M, row0, 32) * D * 4u);
 #pragma unroll
     for (int s = 0; s < G::ks(0); ++s) {
-      B[s] = load_op<EM>(r, (uint32_t)(n * D + 16 * s + 8 * g));
-      if (N::gen && 16 * s + 8 * g >= D) B[s] = Opnd{f16x8{}, f16x8{}};
+      const uint32_t e = (uint32_t)(n * D + 16 * s + 8 * g) * 4;
+      xr[s][0] = buf_load16<f32x4>(r, e);
+      xr[s][1] = buf_load16<f32x4>(r, e + 16);
+    }
+  }
+  // Loaded x rows as split B operands of layer 0.
+  __device__ __forceinline__ void x_operands(const f32x4 (&xr)[G::ks(0)][2], Opnd (&X)[G::KSM]) const {
+    const int D = dimw<N>(p, 0);
+#pragma unroll
+    for (int s = 0; s < G::ks(0); ++s) {
+      const float v[8] = {xr[s][0][0], xr[s][0][1], xr[s][0][2], xr[s][0][3],
+                          xr[s][1][0], xr[s][1][1], xr[s][1][2], xr[s][1][3]};
+      X[s] = make_op<EM>(v);
+      if (N::gen && 16 * s + 8 * g >= D) X[s] = Opnd{f16x8{}, f16x8{}};
+    }
+  }
+
+  // Layer 0's B operands (row n) from an x tile (CHX chunks per row).
+  __device__ __forceinline__ void read_xtile(const XTile<G::CHX>& t, Opnd (&X)[G::KSM]) const {
+    const int D = dimw<N>(p, 0);
+#pragma unroll
+    for (int s = 0; s < G::ks(0); ++s) {
+      X[s].h = t[0][slot<G::CHX>(n, 2 * s + g)];
+      X[s].l = t[1][slot<G::CHX>(n, 2 * s + g)];
+      if (N::gen && 16 * s + 8 * g >= D) X[s] = Opnd{f16x8{}, f16x8{}};
+    }
+  }
+
+  // Layer l's B operands (row n) from a tile holding layer l's input.
+  template <int l>
+  __device__ __forceinline__ void read_tile(const XTile<CH>& t, Opnd (&B)[G::KSM]) const {
+    const int Wd = dimw<N>(p, l);
+#pragma unroll
+    for (int s = 0; s < G::ks(l); ++s) {
+      B[s].h = t[0][slot<CH>(n, 2 * s + g)];
+      B[s].l = t[1][slot<CH>(n, 2 * s + g)];
+      // (past the true width the tile holds stale values: zero operands)
+      if (N::gen && 16 * s + 8 * g >= Wd) B[s] = Opnd{f16x8{}, f16x8{}};
     }
   }
 
@@ -139,87 +209,214 @@ struct FxWave {
       }
   }
 
-  // Layer l of one 32-row block: B holds the layer's input rows.  Owning
-  // waves compute their 32 output features; hidden layers hand the whole
-  // activation on through the tile.
+  // Layer l of one 32-row block for an owning wave: the MFMA chain over the
+  // layer's K-steps, then either the hidden activation (g = softplus(z) /
+  // ln 2 into tile `out`, h into the stash) or the output rows.
   template <int l>
-  __device__ __forceinline__ void layer(int64_t row0) {
-    if (owns(l)) {
-      f32x16 acc = {}, acc2 = {};  // two chains: even and odd K-steps
-      if constexpr (G::RES) {
+  __device__ __forceinline__ void compute(const Opnd (&f)[G::KSM], const Opnd (&in)[G::KSM], int64_t row0,
+                                          XTile<CH>& out) const {
+    f32x16 acc = {};
 #pragma unroll
-        for (int s = 0; s < G::ks(l); ++s) {
-          if (s & 1)
-            acc2 = mma<EM>(fr[l][s], B[s], acc2);
-          else
-            acc = mma<EM>(fr[l][s], B[s], acc);
-        }
-      } else {
-        Opnd f[G::KSM];
-        load_frags<l>(f);
-#pragma unroll
-        for (int s = 0; s < G::ks(l); ++s) {
-          if (s & 1)
-            acc2 = mma<EM>(f[s], B[s], acc2);
-          else
-            acc = mma<EM>(f[s], B[s], acc);
-        }
-      }
-      acc += acc2;
-      float v[16];
-      if constexpr (l + 1 < L) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float u = acc[j] * kLog2e;
-          v[j] = sp2_fix(u, sp2(u)) * kLn2;
-        }
-        if (p.stash[l]) store_row16(p.stash[l], dimw<N>(p, l + 1), row0, v);
-        const Opnd lo = make_op<EM>(*reinterpret_cast<const float(*)[8]>(v));
-        const Opnd hi = make_op<EM>(*reinterpret_cast<const float(*)[8]>(v + 8));
-        tile[par][0][slot<CH>(n, 4 * w + g)] = lo.h;
-        tile[par][0][slot<CH>(n, 4 * w + 2 + g)] = hi.h;
-        tile[par][1][slot<CH>(n, 4 * w + g)] = lo.l;
-        tile[par][1][slot<CH>(n, 4 * w + 2 + g)] = hi.l;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = acc[j];
-        store_row16(reinterpret_cast<float*>(p.out), dimw<N>(p, L), row0, v);
-      }
-    }
+    for (int s = 0; s < G::ks(l); ++s) acc = mma<EM>(f[s], in[s], acc);
+    float v[16];
     if constexpr (l + 1 < L) {
-      __syncthreads();  // the whole hidden activation of these rows is in the tile
-      const int Wd = dimw<N>(p, l + 1);
 #pragma unroll
-      for (int s = 0; s < G::ks(l + 1); ++s) {
-        B[s].h = tile[par][0][slot<CH>(n, 2 * s + g)];
-        B[s].l = tile[par][1][slot<CH>(n, 2 * s + g)];
-        // (past the true width the tile holds stale values: zero operands)
-        if (N::gen && 16 * s + 8 * g >= Wd) B[s] = Opnd{f16x8{}, f16x8{}};
+      for (int j = 0; j < 16; ++j) v[j] = sp2_fix(acc[j], sp2(acc[j]));
+      if constexpr (STASH) {
+        if (p.stash[l]) {
+          float h[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) h[j] = v[j] * kLn2;
+          store_row16(p.stash[l], dimw<N>(p, l + 1), row0, h);
+        }
       }
-      // The next hand-over writes the other tile: this one is read until
-      // every wave has passed the next barrier.
-      par ^= 1;
-      layer<l + 1>(row0);
+      const Opnd lo = make_op_nonneg(*reinterpret_cast<const float(*)[8]>(v));
+      const Opnd hi = make_op_nonneg(*reinterpret_cast<const float(*)[8]>(v + 8));
+      out[0][slot<CH>(n, 4 * w + g)] = lo.h;
+      out[0][slot<CH>(n, 4 * w + 2 + g)] = hi.h;
+      out[1][slot<CH>(n, 4 * w + g)] = lo.l;
+      out[1][slot<CH>(n, 4 * w + 2 + g)] = hi.l;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = acc[j];
+      store_row16(reinterpret_cast<float*>(p.out), dimw<N>(p, L), row0, v);
     }
   }
 };
 
-template <class N>
-__global__ __launch_bounds__((FxGeo<N>::NWV * 64)) void fwd_x3_kernel(FwdParams p) {
+// ---------------------------------------------------------------------------
+// 2 and 3 layers: the two-stage pipeline.  Step t: stage A computes layer 0
+// of the WG's block t into t0[t & 1]; stage B computes layer 1 of block t - 1
+// (from t0[(t - 1) & 1]; into t1[(t - 1) & 1] with 3 layers) and, with 3
+// layers, layer 2 of block t - 2 (from t1[(t - 2) & 1]).  A tile written in
+// step t is read in step t + 1 and written again in step t + 2, so the one
+// barrier ending each step orders every hand-over.  Both stages run
+// nb + L - 1 steps (nb = the WG's blocks), every wave the same barriers.
+//
+// x reaches stage A through LDS as well: in step t every wave of the WG
+// splits its 8-value piece of block t + 1 (loaded in step t - 1) into the
+// x tile xt[(t + 1) & 1] and issues the loads of its piece of block t + 2.
+// Each row of x is then loaded once and split once per workgroup, where
+// every stage-A wave loading and splitting the whole block itself costs 4x
+// the VALU work and L2 reads.
+// ---------------------------------------------------------------------------
+template <class N, bool STASH>
+struct XPiece {
   using G = FxGeo<N>;
-  static_assert(G::valid(), "fp32-tensor forward shape");
-  __shared__ f16x8 tile[2][2][32 * G::CH];
-  const int lane = threadIdx.x & 63;
-  FxWave<N> wv{p, tile, lane, lane & 31, lane >> 5, __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))};
-  const int64_t nblk = (p.M + 31) / 32;
-  for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
-    const int64_t row0 = b * 32;
-    wv.load_x(row0);
-    if constexpr (G::RES) {
-      if (b == blockIdx.x) wv.template load_all_frags<>();
-    }
-    wv.template layer<0>(row0);
+  static_assert(G::THREADS == 32 * 16, "one 8-value x piece per thread of the workgroup");
+  const FwdParams& p;
+  int row, chunk;  // this thread's piece of a block: row, 8-value chunk
+  f32x4 raw[2];
+
+  // Loads of the piece of block row0 (rows past the batch read zeros;
+  // chunks past the true width are never read unmasked).
+  __device__ __forceinline__ void load(int64_t row0) {
+    const int D = dimw<N>(p, 0);
+    const rsrc_t r = make_rsrc(reinterpret_cast<const float*>(p.x) + row0 * D, rows_at(p.M, row0, 32) * D * 4u);
+    const uint32_t e = (uint32_t)(row * D + 8 * chunk) * 4;
+    raw[0] = buf_load16<f32x4>(r, e);
+    raw[1] = buf_load16<f32x4>(r, e + 16);
   }
+  // The loaded piece, split, into an x tile.
+  __device__ __forceinline__ void store(XTile<G::CHX>& t) const {
+    if (8 * chunk >= 8 * G::CHX) return;
+    const float v[8] = {raw[0][0], raw[0][1], raw[0][2], raw[0][3], raw[1][0], raw[1][1], raw[1][2], raw[1][3]};
+    const Opnd o = make_op<EM_F32>(v);
+    t[0][slot<G::CHX>(row, chunk)] = o.h;
+    t[1][slot<G::CHX>(row, chunk)] = o.l;
+  }
+};
+
+template <class N, bool STASH>
+__global__ __launch_bounds__(FxGeo<N>::THREADS) void fwd_x3p_kernel(FwdParams p) {
+  using G = FxGeo<N>;
+  constexpr int L = N::L, CH = G::CH;
+  static_assert(G::valid() && G::PIPE, "fp32-tensor pipelined forward shape");
+  __shared__ XTile<CH> t0[2], t1[L == 3 ? 2 : 1];
+  __shared__ XTile<G::CHX> xt[2];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const FxOps<N, STASH> op{p, lane & 31, lane >> 5, wave % G::NWV};
+  const int64_t nblk = (p.M + 31) / 32, stride = gridDim.x, b0 = blockIdx.x;
+  const int64_t nb = (nblk - b0 + stride - 1) / stride;  // >= 1: the grid never exceeds the block count
+  const int64_t steps = nb + L - 1;
+  // x piece of this thread: 16 chunks of 8 values per row (x widths <= 128)
+  XPiece<N, STASH> xp{p, (int)(threadIdx.x >> 4), (int)(threadIdx.x & 15), {}};
+  auto rows_of = [&](int64_t t) { return (b0 + t * stride) * 32; };
+  xp.load(rows_of(0));
+  xp.store(xt[0]);
+  xp.load(rows_of(1));
+  __syncthreads();
+  if (wave < G::NWV) {
+    // Stage A: layer 0.
+    Opnd f[G::KSM], X[G::KSM];
+    const bool own = op.template owns<0>();
+    if (own) op.template load_frags<0>(f);
+    for (int64_t t = 0; t < steps; ++t) {
+      if (t + 1 < nb) {
+        xp.store(xt[(t + 1) & 1]);
+        xp.load(rows_of(t + 2));
+      }
+      if (t < nb && own) {
+        op.read_xtile(xt[t & 1], X);
+        op.template compute<0>(f, X, rows_of(t), t0[t & 1]);
+      }
+      __syncthreads();
+    }
+  } else {
+    // Stage B: layers 1 and (3 layers) 2.
+    Opnd f1[G::KSM], f2[G::KSM], B[G::KSM];
+    const bool own1 = op.template owns<1>();
+    bool own2 = false;
+    if (own1) op.template load_frags<1>(f1);
+    if constexpr (L == 3) {
+      own2 = op.template owns<2>();
+      if (own2) op.template load_frags<2>(f2);
+    }
+    for (int64_t t = 0; t < steps; ++t) {
+      if (t + 1 < nb) {
+        xp.store(xt[(t + 1) & 1]);
+        xp.load(rows_of(t + 2));
+      }
+      if (t >= 1 && t - 1 < nb) {
+        op.template read_tile<1>(t0[(t - 1) & 1], B);
+        if (own1) op.template compute<1>(f1, B, rows_of(t - 1), t1[(t - 1) & 1]);
+      }
+      if constexpr (L == 3) {
+        if (t >= 2 && t - 2 < nb) {
+          op.template read_tile<2>(t1[t & 1], B);  // (t - 2) & 1 == t & 1
+          if (own2) op.template compute<2>(f2, B, rows_of(t - 2), t1[0]);  // (last layer: no tile written)
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4 and 5 layers: one wave per output block runs every layer of a block in
+// turn (NWV waves), its fragments of all layers resident.  The x loads of
+// block b + 2 are issued once block b + 1's rows have become operands
+// (between block b's first two layers), so each has a whole block's time to
+// arrive.
+// ---------------------------------------------------------------------------
+template <class N, bool STASH>
+struct FxWave {
+  using G = FxGeo<N>;
+  static constexpr int L = N::L, CH = G::CH;
+  FxOps<N, STASH> op;
+  XTile<CH>* tile;  // [2]
+  int par = 0;
+  Opnd fr[L][G::KSM];  // this wave's A fragments (output block w)
+  Opnd X[G::KSM];      // layer 0's B operands: x row n of the current block
+  Opnd B[G::KSM];      // B operands of a hidden layer: row n
+  f32x4 xr[G::ks(0)][2];
+
+  template <int l = 0>
+  __device__ __forceinline__ void load_all_frags() {
+    if constexpr (l < L) {
+      if (op.template owns<l>()) op.template load_frags<l>(fr[l]);
+      load_all_frags<l + 1>();
+    }
+  }
+
+  template <int l>
+  __device__ __forceinline__ void layer(int64_t row0, int64_t ahead) {
+    if (op.template owns<l>()) {
+      if constexpr (l == 0)
+        op.template compute<0>(fr[0], X, row0, tile[par]);
+      else
+        op.template compute<l>(fr[l], B, row0, tile[par]);
+    }
+    if constexpr (l + 1 < L) {
+      __syncthreads();  // the whole hidden activation of these rows is in the tile
+      op.template read_tile<l + 1>(tile[par], B);
+      if constexpr (l == 0) {
+        op.x_operands(xr, X);
+        op.load_x(xr, ahead);
+      }
+      // The next hand-over writes the other tile: this one is read until
+      // every wave has passed the next barrier.
+      par ^= 1;
+      layer<l + 1>(row0, ahead);
+    }
+  }
+};
+
+template <class N, bool STASH>
+__global__ __launch_bounds__(FxGeo<N>::THREADS) void fwd_x3_kernel(FwdParams p) {
+  using G = FxGeo<N>;
+  static_assert(G::valid() && !G::PIPE, "fp32-tensor forward shape");
+  __shared__ XTile<G::CH> tile[2];
+  const int lane = threadIdx.x & 63;
+  FxWave<N, STASH> wv{{p, lane & 31, lane >> 5, __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))}, tile};
+  const int64_t nblk = (p.M + 31) / 32, stride = gridDim.x;
+  // (the grid never exceeds the block count: every workgroup has a block)
+  wv.op.load_x(wv.xr, (int64_t)blockIdx.x * 32);
+  wv.load_all_frags();
+  wv.op.x_operands(wv.xr, wv.X);
+  wv.op.load_x(wv.xr, ((int64_t)blockIdx.x + stride) * 32);
+  for (int64_t b = blockIdx.x; b < nblk; b += stride) wv.template layer<0>(b * 32, (b + 2 * stride) * 32);
 }
 
 }  // namespace tp
@@ -230,33 +427,43 @@ __global__ __launch_bounds__((FxGeo<N>::NWV * 64)) void fwd_x3_kernel(FwdParams 
 
 namespace {
 
+template <class N, bool STASH>
+constexpr const void* x3_kernel() {
+  if constexpr (tp::FxGeo<N>::PIPE)
+    return reinterpret_cast<const void*>(&tp::fwd_x3p_kernel<N, STASH>);
+  else
+    return reinterpret_cast<const void*>(&tp::fwd_x3_kernel<N, STASH>);
+}
+
 template <class N>
-int launch_x3(const FwdParams& p, hipStream_t st, LaunchInfo* info) {
+int launch_x3(const FwdParams& p, bool stash, hipStream_t st, LaunchInfo* info) {
   using G = tp::FxGeo<N>;
   constexpr int kMaxDev = 64;
-  static int occ_cache[kMaxDev];  // benign race: the value is idempotent
+  static int occ_cache[2][kMaxDev];  // [stash][device]; benign race: the value is idempotent
+  const void* kern = stash ? x3_kernel<N, true>() : x3_kernel<N, false>();
   int cus = 0;
   int rc = current_device_cus(&cus);
   if (rc != MLPMK_OK) return rc;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  int occ = (dev >= 0 && dev < kMaxDev) ? occ_cache[dev] : 0;
+  int occ = (dev >= 0 && dev < kMaxDev) ? occ_cache[stash][dev] : 0;
   if (occ <= 0) {
-    rc = kernel_occupancy(reinterpret_cast<const void*>(&tp::fwd_x3_kernel<N>), G::NWV * 64, &occ);
+    rc = kernel_occupancy(kern, G::THREADS, &occ);
     if (rc != MLPMK_OK) return rc;
-    if (dev >= 0 && dev < kMaxDev) occ_cache[dev] = occ;
+    if (dev >= 0 && dev < kMaxDev) occ_cache[stash][dev] = occ;
   }
   const int64_t nblk = (p.M + 31) / 32;
   const int64_t cap = (int64_t)cus * occ;
   const int grid = (int)(nblk < cap ? nblk : cap);
   if (info) {
-    *info = LaunchInfo{MLPMK_KERNEL_FEATURE_SPLIT, 32, G::NWV, grid, occ};
+    *info = LaunchInfo{MLPMK_KERNEL_FEATURE_SPLIT, 32, G::THREADS / 64, grid, occ};
     return MLPMK_OK;
   }
   (void)hipGetLastError();
-  hipLaunchKernelGGL((tp::fwd_x3_kernel<N>), dim3(grid), dim3(G::NWV * 64), 0, st, p);
-  e = hipGetLastError();
+  void* args[] = {const_cast<FwdParams*>(&p)};
+  e = hipLaunchKernel(kern, dim3(grid), dim3(G::THREADS), args, 0, st);
+  if (e == hipSuccess) e = hipGetLastError();
   return e == hipSuccess ? MLPMK_OK : hip_fail(e, "fp32 forward kernel launch");
 }
 
@@ -265,18 +472,17 @@ int launch_x3(const FwdParams& p, hipStream_t st, LaunchInfo* info) {
 bool fwd_generic_dims(int L, const int* dims);
 
 // fp32 tensors: every shape of the 128-wide kernels (the three compiled
-// ones and the runtime-width networks of 2..5 layers).  The stash flag needs
-// no separate kernel: NULL stash entries are simply not written.
+// ones and the runtime-width networks of 2..5 layers).  With the stash
+// flag, non-NULL stash entries are written.
 int fwd_dispatch_f32(int L, const int* dims, const FwdParams& p, bool stash, hipStream_t st, LaunchInfo* info) {
-  (void)stash;
   if (L == 3 && dims[0] == 128 && dims[1] == 128 && dims[2] == 128 && dims[3] == 128)
-    return launch_x3<Net<128, 128, 128, 128>>(p, st, info);
+    return launch_x3<Net<128, 128, 128, 128>>(p, stash, st, info);
   if (fwd_generic_dims(L, dims)) {  // (includes 5 x 128 and 32-64-64-16)
     switch (L) {
-      case 2: return launch_x3<Gen<Net<128, 128, 128>>>(p, st, info);
-      case 3: return launch_x3<Gen<Net<128, 128, 128, 128>>>(p, st, info);
-      case 4: return launch_x3<Gen<Net<128, 128, 128, 128, 128>>>(p, st, info);
-      default: return launch_x3<Gen<Net<128, 128, 128, 128, 128, 128>>>(p, st, info);
+      case 2: return launch_x3<Gen<Net<128, 128, 128>>>(p, stash, st, info);
+      case 3: return launch_x3<Gen<Net<128, 128, 128, 128>>>(p, stash, st, info);
+      case 4: return launch_x3<Gen<Net<128, 128, 128, 128, 128>>>(p, stash, st, info);
+      default: return launch_x3<Gen<Net<128, 128, 128, 128, 128, 128>>>(p, stash, st, info);
     }
   }
   return fail(MLPMK_ERR_UNSUPPORTED_SHAPE, "no fp32-tensor forward kernel for these widths (all at most 128)");

@@ -50,6 +50,28 @@ __device__ __forceinline__ Opnd make_op(const float (&v)[8]) {
   return o;
 }
 
+// bf16 hi + lo of 8 values that are >= 0, +inf or NaN (softplus outputs):
+// hi = the upper half of each value's bits (truncation), lo = v - hi >= 0
+// rounded to bf16.  The same ~16-bit significand as make_op at four VALU
+// operations per value instead of five: max(v - hi, 0) turns the NaN of
+// inf - inf into lo = 0 (maxNum), so inf stays inf.
+__device__ __forceinline__ Opnd make_op_nonneg(const float (&v)[8]) {
+  uint32_t hp[4];
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v[j]);
+    r[j] = __builtin_fmaxf(v[j] - __builtin_bit_cast(float, bits & 0xffff0000u), 0.0f);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    hp[j] = (__builtin_bit_cast(uint32_t, v[2 * j + 1]) & 0xffff0000u) | (__builtin_bit_cast(uint32_t, v[2 * j]) >> 16);
+  Opnd o;
+  o.h = __builtin_bit_cast(f16x8, (i32x4){(int)hp[0], (int)hp[1], (int)hp[2], (int)hp[3]});
+  o.l = pack8<true>(r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]);
+  return o;
+}
+
 template <int EM>
 __device__ __forceinline__ f32x16 mma(const Opnd& a, const Opnd& b, f32x16 c) {
   if constexpr (EM == EM_F32) {

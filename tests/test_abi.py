@@ -84,7 +84,7 @@ def test_fwd_validation_codes():
     assert _fwd(d, stash=(A, A + 4)) == MISALIGNED
     assert b"stash[1]" in lib.mlpmk_last_error()
     assert lib.mlpmk_fwd(3, None, 1, A, None, A, None, 1, None) == INVALID
-    # element types: fp16 (1), bf16 (2) and fp32 (0, fp16 MFMA operands); others are invalid
+    # element types: fp16 (1), bf16 (2) and fp32 (0, bf16 hi/lo split operands); others are invalid
     assert _fwd(d, dtype=7) == INVALID
     assert _fwd(d, dtype=0, m=0) == OK
     assert _fwd(d, dtype=2, m=0) == OK
