@@ -72,8 +72,8 @@ struct FxGeo {
   }
   static constexpr int NWV = nwv(), KSM = ksm(), TW = tw(), CH = TW / 8;
   static constexpr int CHX = pow2_32(N::d[0]) / 8;  // chunks of 8 features per x-tile row
-  static constexpr bool PIPE = L <= 3;  // the two-stage pipeline
-  static constexpr int THREADS = (PIPE ? 2 : 1) * NWV * 64;
+  static constexpr bool PIPE = L <= 3;  // the layer pipeline: one wave group per layer
+  static constexpr int THREADS = (PIPE ? L : 1) * NWV * 64;
   static constexpr bool valid() {
     for (int i = 0; i < L; ++i)
       if (N::d[i] > 128 || N::d[i] % 16 != 0) return false;
@@ -245,41 +245,43 @@ struct FxOps {
 };
 
 // ---------------------------------------------------------------------------
-// 2 and 3 layers: the two-stage pipeline.  Step t: stage A computes layer 0
-// of the WG's block t into t0[t & 1]; stage B computes layer 1 of block t - 1
-// (from t0[(t - 1) & 1]; into t1[(t - 1) & 1] with 3 layers) and, with 3
-// layers, layer 2 of block t - 2 (from t1[(t - 2) & 1]).  A tile written in
-// step t is read in step t + 1 and written again in step t + 2, so the one
-// barrier ending each step orders every hand-over.  Both stages run
-// nb + L - 1 steps (nb = the WG's blocks), every wave the same barriers.
+// 2 and 3 layers: the layer pipeline.  L groups of NWV waves, group r
+// computing layer r (one wave of each group per SIMD); in step t group r
+// runs layer r of the WG's block t - r, reading its input from tile
+// tl[r - 1][(t - r) & 1] (group 0: the x tile) and writing its hidden
+// activation into tl[r][(t - r) & 1].  A tile written in step t is read in
+// step t + 1 and written again in step t + 2, so the one barrier ending each
+// step orders every hand-over.  Every group runs nb + L - 1 steps (nb = the
+// WG's blocks), every wave the same barriers.
 //
-// x reaches stage A through LDS as well: in step t every wave of the WG
-// splits its 8-value piece of block t + 1 (loaded in step t - 1) into the
-// x tile xt[(t + 1) & 1] and issues the loads of its piece of block t + 2.
-// Each row of x is then loaded once and split once per workgroup, where
-// every stage-A wave loading and splitting the whole block itself costs 4x
-// the VALU work and L2 reads.
+// x reaches group 0 through LDS as well: in step t the WG's threads split
+// their 8-value pieces of block t + 1 (loaded in step t - 1) into the x tile
+// xt[(t + 1) & 1] and issue the loads of their pieces of block t + 2.  Each
+// row of x is then loaded once and split once per workgroup, where every
+// layer-0 wave loading and splitting the whole block itself costs 4x the
+// VALU work and L2 reads.
 // ---------------------------------------------------------------------------
-template <class N, bool STASH>
+template <class N>
 struct XPiece {
   using G = FxGeo<N>;
-  static_assert(G::THREADS == 32 * 16, "one 8-value x piece per thread of the workgroup");
+  static_assert(G::THREADS >= 32 * 16, "every 8-value x piece of a block has a thread");
   const FwdParams& p;
-  int row, chunk;  // this thread's piece of a block: row, 8-value chunk
+  int row, chunk;  // this thread's piece of a block: row, 8-value chunk (row >= 32: none)
   f32x4 raw[2];
 
   // Loads of the piece of block row0 (rows past the batch read zeros;
   // chunks past the true width are never read unmasked).
   __device__ __forceinline__ void load(int64_t row0) {
     const int D = dimw<N>(p, 0);
-    const rsrc_t r = make_rsrc(reinterpret_cast<const float*>(p.x) + row0 * D, rows_at(p.M, row0, 32) * D * 4u);
-    const uint32_t e = (uint32_t)(row * D + 8 * chunk) * 4;
+    const rsrc_t r = make_rsrc(reinterpret_cast<const float*>(p.x) + row0 * D,
+                               row < 32 ? rows_at(p.M, row0, 32) * D * 4u : 0u);
+    const uint32_t e = (uint32_t)((row & 31) * D + 8 * chunk) * 4;
     raw[0] = buf_load16<f32x4>(r, e);
     raw[1] = buf_load16<f32x4>(r, e + 16);
   }
   // The loaded piece, split, into an x tile.
   __device__ __forceinline__ void store(XTile<G::CHX>& t) const {
-    if (8 * chunk >= 8 * G::CHX) return;
+    if (row >= 32 || chunk >= G::CHX) return;
     const float v[8] = {raw[0][0], raw[0][1], raw[0][2], raw[0][3], raw[1][0], raw[1][1], raw[1][2], raw[1][3]};
     const Opnd o = make_op<EM_F32>(v);
     t[0][slot<G::CHX>(row, chunk)] = o.h;
@@ -287,70 +289,58 @@ struct XPiece {
   }
 };
 
+// Group r of the layer pipeline (see above).
+template <int r, class N, bool STASH>
+__device__ __forceinline__ void x3p_group(const FxOps<N, STASH>& op, XPiece<N>& xp, XTile<FxGeo<N>::CH> (*tl)[2],
+                                          XTile<FxGeo<N>::CHX>* xt, int64_t b0, int64_t stride, int64_t nb) {
+  using G = FxGeo<N>;
+  constexpr int L = N::L;
+  Opnd f[G::KSM], in[G::KSM];
+  const bool own = op.template owns<r>();
+  if (own) op.template load_frags<r>(f);
+  const int64_t steps = nb + L - 1;
+  for (int64_t t = 0; t < steps; ++t) {
+    if (t + 1 < nb) {
+      xp.store(xt[(t + 1) & 1]);
+      xp.load((b0 + (t + 2) * stride) * 32);
+    }
+    if (t >= r && t - r < nb) {
+      const int64_t b = t - r;
+      if constexpr (r == 0)
+        op.read_xtile(xt[b & 1], in);
+      else
+        op.template read_tile<r>(tl[r - 1][b & 1], in);
+      if (own) op.template compute<r>(f, in, (b0 + b * stride) * 32, tl[r < L - 1 ? r : 0][b & 1]);
+    }
+    __syncthreads();
+  }
+}
+
 template <class N, bool STASH>
 __global__ __launch_bounds__(FxGeo<N>::THREADS) void fwd_x3p_kernel(FwdParams p) {
   using G = FxGeo<N>;
   constexpr int L = N::L, CH = G::CH;
   static_assert(G::valid() && G::PIPE, "fp32-tensor pipelined forward shape");
-  __shared__ XTile<CH> t0[2], t1[L == 3 ? 2 : 1];
+  __shared__ XTile<CH> tl[L - 1][2];
   __shared__ XTile<G::CHX> xt[2];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const FxOps<N, STASH> op{p, lane & 31, lane >> 5, wave % G::NWV};
   const int64_t nblk = (p.M + 31) / 32, stride = gridDim.x, b0 = blockIdx.x;
   const int64_t nb = (nblk - b0 + stride - 1) / stride;  // >= 1: the grid never exceeds the block count
-  const int64_t steps = nb + L - 1;
   // x piece of this thread: 16 chunks of 8 values per row (x widths <= 128)
-  XPiece<N, STASH> xp{p, (int)(threadIdx.x >> 4), (int)(threadIdx.x & 15), {}};
-  auto rows_of = [&](int64_t t) { return (b0 + t * stride) * 32; };
-  xp.load(rows_of(0));
+  XPiece<N> xp{p, (int)(threadIdx.x >> 4), (int)(threadIdx.x & 15), {}};
+  xp.load(b0 * 32);
   xp.store(xt[0]);
-  xp.load(rows_of(1));
+  xp.load((b0 + stride) * 32);
   __syncthreads();
-  if (wave < G::NWV) {
-    // Stage A: layer 0.
-    Opnd f[G::KSM], X[G::KSM];
-    const bool own = op.template owns<0>();
-    if (own) op.template load_frags<0>(f);
-    for (int64_t t = 0; t < steps; ++t) {
-      if (t + 1 < nb) {
-        xp.store(xt[(t + 1) & 1]);
-        xp.load(rows_of(t + 2));
-      }
-      if (t < nb && own) {
-        op.read_xtile(xt[t & 1], X);
-        op.template compute<0>(f, X, rows_of(t), t0[t & 1]);
-      }
-      __syncthreads();
-    }
-  } else {
-    // Stage B: layers 1 and (3 layers) 2.
-    Opnd f1[G::KSM], f2[G::KSM], B[G::KSM];
-    const bool own1 = op.template owns<1>();
-    bool own2 = false;
-    if (own1) op.template load_frags<1>(f1);
-    if constexpr (L == 3) {
-      own2 = op.template owns<2>();
-      if (own2) op.template load_frags<2>(f2);
-    }
-    for (int64_t t = 0; t < steps; ++t) {
-      if (t + 1 < nb) {
-        xp.store(xt[(t + 1) & 1]);
-        xp.load(rows_of(t + 2));
-      }
-      if (t >= 1 && t - 1 < nb) {
-        op.template read_tile<1>(t0[(t - 1) & 1], B);
-        if (own1) op.template compute<1>(f1, B, rows_of(t - 1), t1[(t - 1) & 1]);
-      }
-      if constexpr (L == 3) {
-        if (t >= 2 && t - 2 < nb) {
-          op.template read_tile<2>(t1[t & 1], B);  // (t - 2) & 1 == t & 1
-          if (own2) op.template compute<2>(f2, B, rows_of(t - 2), t1[0]);  // (last layer: no tile written)
-        }
-      }
-      __syncthreads();
-    }
-  }
+  const int r = wave / G::NWV;
+  if (r == 0)
+    x3p_group<0>(op, xp, tl, xt, b0, stride, nb);
+  else if (L == 2 || r == 1)
+    x3p_group<1>(op, xp, tl, xt, b0, stride, nb);
+  else
+    x3p_group<L - 1>(op, xp, tl, xt, b0, stride, nb);
 }
 
 // ---------------------------------------------------------------------------
