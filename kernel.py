@@ -37,10 +37,16 @@ _POLICY = {
     (32, 64, 64, 16): (2, 2, 64, 16),
 }
 _GENERIC_POLICY = (0, 0, 32, 8)  # runtime-width kernels: no split kernel, at most 8 waves
-# fp32 tensors (fwd_x3.hip): the feature-split kernel at every M, 32-row
-# blocks, 4 waves (one per 32 output features of a 128-wide layer; the
-# runtime-width kernels are compiled at width 128).
-_F32_WAVES = 4
+# fp32 tensors (fwd_x3.hip): the feature-split kernels at every M, 32-row
+# blocks; 4 waves per layer (one per 32 output features of a 128-wide layer;
+# the runtime-width kernels are compiled at width 128), one wave group per
+# layer for 2 and 3 layers (the layer pipeline), one group running every
+# layer for 4 and 5.
+_F32_WAVES_PER_LAYER = 4
+
+
+def _f32_waves(n_layers):
+    return _F32_WAVES_PER_LAYER * (n_layers if n_layers <= 3 else 1)
 
 
 def __getattr__(name):
@@ -53,7 +59,7 @@ def _mirror_policy(M, dims, num_cus, fp32=False):
     if max(dims) > 128:  # streamed-weight kernel (fwd_wide.hip): 8 waves, 32-row blocks, any M
         return 32, 8
     if fp32:
-        return 32, _F32_WAVES
+        return 32, _f32_waves(len(dims) - 1)
     split_per_cu, split_waves, bm, max_waves = _POLICY.get(tuple(dims), _GENERIC_POLICY)
     if -(-M // 32) <= split_per_cu * num_cus:
         return 32, split_waves

@@ -218,11 +218,13 @@ def test_drop_in_modules_import_without_gpu():
     assert cfg(40000, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 4)
     assert cfg(4194304, 32, 64, 64, 16) == (64, 16, 16, 16, 16, 16)
     assert cfg(4096, 128, 128, 128, 128, num_cus=8) == (32, 128, 16, 16, 16, 12)
-    # fp32 tensors: their feature-split kernel at every M (32-row blocks, 4 waves)
-    assert cfg(4096, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 4)
-    assert cfg(1048576, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 4)
-    assert cfg(4194304, 32, 64, 64, 16, fp32=True) == (32, 16, 16, 16, 16, 4)
-    assert cfg(1048576, 64, 64, 64, 64, fp32=True) == (32, 64, 16, 16, 16, 4)
+    # fp32 tensors: their layer pipeline at every M (32-row blocks, 4 waves per
+    # layer of the 3-layer network)
+    assert cfg(4096, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 12)
+    assert cfg(1048576, 128, 128, 128, 128, fp32=True) == (32, 128, 16, 16, 16, 12)
+    assert cfg(4194304, 32, 64, 64, 16, fp32=True) == (32, 16, 16, 16, 16, 12)
+    assert cfg(1048576, 64, 64, 64, 64, fp32=True) == (32, 64, 16, 16, 16, 12)
+    assert kernel._mirror_policy(4096, (128,) * 6, 256, fp32=True) == (32, 4)  # 5 layers: one group
     assert callable(kernel._fused_mlp_fwd) and kernel.Model and kernel.ModelNew
 
 
