@@ -566,6 +566,10 @@ def main():
     ap.add_argument("--train-step", type=int, default=None, metavar="M",
                     help="counter-collection runs of the training kernels: only the WN training step at M rows "
                          "(3 layers; 5 with --config 5l128; no headline, no other legs); prints its timing JSON")
+    ap.add_argument("--train-dtype", choices=("fp16", "bf16", "fp32"), default="fp16",
+                    help="with --train-step: x's type (fp32 runs the fp32-tensor kernels)")
+    ap.add_argument("--train-hidden", type=int, default=128,
+                    help="with --train-step: the hidden width H (256: the streamed-weight kernels)")
     ap.add_argument("--sweep", action="store_true",
                     help="only the small-batch latency sweep of --config (M = 64 .. 4096; kernel-trace runs); "
                          "prints its JSON")
@@ -596,9 +600,10 @@ def main():
 
     if args.train_step:
         n_layers = 5 if args.config == "5l128" else 3
+        tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.train_dtype]
         print(json.dumps({"training_step": {str(args.train_step): train_step_bench(
-            torch, args.train_step, steps=args.steps, warmup=args.warmup, n_layers=n_layers)},
-                          "layers": n_layers}))
+            torch, args.train_step, steps=args.steps, warmup=args.warmup, n_layers=n_layers, dtype=tdt,
+            hidden=args.train_hidden)}, "layers": n_layers}))
         return
 
     dims = CONFIG_DIMS[args.config]

@@ -110,6 +110,7 @@ struct DgWave {
   Opnd fr[RES ? L : 1][G::KSM];       // this wave's A fragments (output block w)
   Opnd B[G::KSM];                     // B operands of the current layer: dz_l of row n
   float h[L][16];                     // h_l of this wave's 16 features of row n (l >= 1)
+  float hn[RES ? L : 1][16];          // RES: the same for the workgroup's next block, in flight
 
   __device__ __forceinline__ bool owns(int l) const { return 32 * w < dimw<N>(p, l); }
 
@@ -172,17 +173,27 @@ struct DgWave {
 
   // h_l for this wave's 16 features of row n (features 32w + 8g + [0..7]
   // and 32w + 16 + 8g + [0..7]), fp32.  With RES every stash layer's are
-  // issued at once at the start of a block; otherwise each layer's with its
-  // fragments.
+  // issued at once, a block ahead (into hn, which becomes h when that block
+  // starts: the loads of block b + grid are in flight while block b
+  // computes); otherwise each layer's with its fragments.  Past the batch the
+  // resource is empty and the loads return zeros.
   template <int l = 1>
-  __device__ __forceinline__ void load_h(int64_t row0) {
+  __device__ __forceinline__ void load_h(int64_t row0, float (&dst)[L][16]) {
     if constexpr (l < L) {
-      load_h_one<l>(row0);
-      load_h<l + 1>(row0);
+      load_h_one<l>(row0, dst);
+      load_h<l + 1>(row0, dst);
+    }
+  }
+  __device__ __forceinline__ void take_next_h() {
+    if constexpr (RES) {
+#pragma unroll
+      for (int l = 1; l < L; ++l)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) h[l][j] = hn[l][j];
     }
   }
   template <int l>
-  __device__ __forceinline__ void load_h_one(int64_t row0) {
+  __device__ __forceinline__ void load_h_one(int64_t row0, float (&dst)[L][16]) {
     {
       const int HW = dimw<N>(p, l);
       const rsrc_t r = make_rsrc(p.stash[l - 1] + row0 * HW, owns(l) ? rows_at(p.M, row0, 32) * HW * 4u : 0u);
@@ -191,10 +202,10 @@ struct DgWave {
       const f32x4 c = buf_load16<f32x4>(r, e + 64), d = buf_load16<f32x4>(r, e + 80);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        h[l][j] = a[j];
-        h[l][4 + j] = b[j];
-        h[l][8 + j] = c[j];
-        h[l][12 + j] = d[j];
+        dst[l][j] = a[j];
+        dst[l][4 + j] = b[j];
+        dst[l][8 + j] = c[j];
+        dst[l][12 + j] = d[j];
       }
     }
   }
@@ -231,7 +242,7 @@ struct DgWave {
         } else {
           Opnd f[G::KSM];
           load_frags<l>(f);
-          if constexpr (l >= 1) load_h_one<l>(row0);
+          if constexpr (l >= 1) load_h_one<l>(row0, h);
 #pragma unroll
           for (int s = 0; s < G::ks(l); ++s) {
             if (s & 1)
@@ -292,11 +303,15 @@ __global__ __launch_bounds__((DgGeo<N, DX>::NWV * 64)) void tp_dgrad_kernel(TpPa
   const int lane = threadIdx.x & 63;
   W wv{p, tile, lane, lane & 31, lane >> 5, __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))};
   const int64_t nblk = (p.M + 31) / 32;
+  if constexpr (RES) {
+    wv.template load_h<>((int64_t)blockIdx.x * 32, wv.hn);  // (from HBM: the longest wait first)
+    wv.template load_all_frags<>();                          // (L2 hits after the first workgroup)
+  }
   for (int64_t b = blockIdx.x; b < nblk; b += gridDim.x) {
     const int64_t row0 = b * 32;
-    if constexpr (RES) wv.template load_h<>(row0);  // (from HBM: the longest wait first)
     if constexpr (RES) {
-      if (b == blockIdx.x) wv.template load_all_frags<>();  // (L2 hits after the first workgroup)
+      wv.take_next_h();
+      wv.template load_h<>(row0 + 32 * (int64_t)gridDim.x, wv.hn);
     }
     wv.load_dout(row0);
     wv.template layer<N::L - 1>(row0);
