@@ -56,8 +56,8 @@ def __getattr__(name):
 
 
 def _mirror_policy(M, dims, num_cus, fp32=False):
-    if max(dims) > 128:  # streamed-weight kernel (fwd_wide.hip): 8 waves, 32-row blocks, any M
-        return 32, 8
+    if max(dims) > 128:  # streamed-weight kernel (fwd_wide.hip): 32-row blocks, 8 waves from 256 rounds
+        return 32, (4 if M < 256 * num_cus else 8)
     if fp32:
         return 32, _f32_waves(len(dims) - 1)
     split_per_cu, split_waves, bm, max_waves = _POLICY.get(tuple(dims), _GENERIC_POLICY)

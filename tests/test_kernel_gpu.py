@@ -92,8 +92,12 @@ def test_launcher_runs_on_the_current_stream_without_sync():
     assert ok, err
 
 
-@pytest.mark.parametrize("fp32", [False, True])
-@pytest.mark.parametrize("dims", [(128,) * 4, (32, 64, 64, 16), (64, 64, 64, 64), (128, 128, 128, 10), (64, 128, 32, 16)])
+_MIRROR_DIMS = [(128,) * 4, (32, 64, 64, 16), (64, 64, 64, 64), (128, 128, 128, 10), (64, 128, 32, 16),
+                (128, 256, 256, 128)]
+
+
+# (fp32 tensors run widths up to 128: no fp32 case for the wide network)
+@pytest.mark.parametrize("dims,fp32", [(d, f) for d in _MIRROR_DIMS for f in (False, True) if not (f and max(d) > 128)])
 def test_pick_config_mirror_matches_the_library_launch(dims, fp32):
     # The Python mirror of the launch policy (used without a device) against
     # the library's own answer from the code path that launches

@@ -54,9 +54,11 @@ def test_wide_forward_matches_oracle(dims, m):
     _check(out.float().cpu().numpy(), orc.forward(x, ws, round_hidden=True), f"{dims} M={m}")
     info = ops.fwd_launch_info(dims, m)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    assert info == {"kernel": "persistent", "rows_per_block": 32, "waves": 8,
-                    "grid": min(-(-m // 256), cus), "wgs_per_cu": 1}
-    assert kernel._mirror_policy(m, dims, cus) == (32, 8)
+    # rounds of 8 waves (256 rows) from 256 x CUs rows, of 4 waves below
+    nw = 8 if m >= 256 * cus else 4
+    assert info == {"kernel": "persistent", "rows_per_block": 32, "waves": nw,
+                    "grid": min(-(-m // (32 * nw)), cus), "wgs_per_cu": 1}
+    assert kernel._mirror_policy(m, dims, cus) == (32, nw)
 
 
 def test_wide_forward_at_one_million_rows_sampled():
@@ -123,7 +125,7 @@ def test_wide_launcher_matches_model():
     out = kernel._fused_mlp_fwd(xd, *wd)
     eager = kernel.Model()(xd.float(), *[w.float() for w in wd])
     _check(out.float().cpu().numpy(), eager.cpu().numpy(), "vs eager Model")
-    assert kernel._pick_config(m, *dims)[::5] == (32, 8)
+    assert kernel._pick_config(m, *dims)[::5] == (32, 4)  # 4-wave rounds below 256 x CUs rows
 
 
 def _torch_ref(x16, ws16):
