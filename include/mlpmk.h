@@ -59,6 +59,16 @@ enum { MLPMK_DTYPE_F32 = 0, MLPMK_DTYPE_F16 = 1, MLPMK_DTYPE_BF16 = 2 };
  * the copy that would materialise a broadcast row.  Since ABI version 201. */
 enum { MLPMK_DOUT_SCALAR = -1 };
 
+/* Flag OR-ed into the dtype argument of mlpmk_bwd / _ws / _noalloc: dw is
+ * written (=) instead of accumulated into (+=), so its prior contents do not
+ * matter and the caller needs no zero-fill launch before a fresh gradient.
+ * The reference's backward produces dW fresh for each step (its autograd
+ * function returns the gradients, /root/reference/mlp_fused.md:88-112); the
+ * accumulating default is kept for callers that sum several backwards.
+ * With M = 0 the written gradient is zero (one clearing launch).  Since ABI
+ * version 203. */
+enum { MLPMK_BWD_WRITE_DW = 0x100 };
+
 /* Library ABI version (major * 100 + minor). */
 int mlpmk_version(void);
 
@@ -186,7 +196,8 @@ int mlpmk_fwd_launch_info(int num_layers, const int* dims, int dtype, int64_t M,
  *                    the output width
  *   dx               NULL, or [M, dims[0]] dtype (written)
  *   dw[l]            [dims[l], dims[l+1]] fp32, ACCUMULATED into (+=); the
- *                    caller zeroes them for a fresh gradient
+ *                    caller zeroes them for a fresh gradient, or passes
+ *                    dtype | MLPMK_BWD_WRITE_DW to have them written (=)
  * Networks of 4 and 5 layers are supported through mlpmk_bwd_ws only (they
  * hand dz between two launches through the workspace); here they return
  * MLPMK_ERR_INVALID_ARG without touching the device.

@@ -61,6 +61,7 @@ STATUS = {
     5: "MLPMK_ERR_NO_DEVICE",
 }
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+BWD_WRITE_DW = 0x100  # MLPMK_BWD_WRITE_DW: OR-ed into the backward's dtype, dW written instead of accumulated
 
 _lock = threading.Lock()
 _lib = None

@@ -35,7 +35,7 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import _lib, ops
 
 # Activation recomputation policy: "auto" recomputes h_{L-1} where that makes
 # the training step faster (MI355X, stash -> recompute; the weight-norm
@@ -175,16 +175,19 @@ class FusedMLPFunction(torch.autograd.Function):
         if ctx.recompute:
             hs.append(None)  # h_{L-1}: recomputed by the backward kernel
         dout = _as_row_broadcast(dout.to(x.dtype))
-        dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
         if _backward_impl() == "fused" and _fused_bwd_supported(dims, x.dtype):
-            # x, the weights and the stash were checked by the forward.
+            # x, the weights and the stash were checked by the forward.  The
+            # library writes dW (MLPMK_BWD_WRITE_DW): no zero-fill launch.
+            dws = [torch.empty(w.shape, dtype=torch.float32, device=w.device) for w in weights]
             M = int(x.shape[0])
             dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, x.device)
-            ops._bwd_raw(x.device, dims, ops._fwd_code(x.dtype), x.data_ptr(), [w.data_ptr() for w in weights],
-                         [h.data_ptr() if h is not None else None for h in hs], dout.data_ptr(), row_stride,
-                         dx.data_ptr() if dx is not None else None, [d.data_ptr() for d in dws], M)
+            ops._bwd_raw(x.device, dims, ops._fwd_code(x.dtype) | _lib.BWD_WRITE_DW, x.data_ptr(),
+                         [w.data_ptr() for w in weights], [h.data_ptr() if h is not None else None for h in hs],
+                         dout.data_ptr(), row_stride, dx.data_ptr() if dx is not None else None,
+                         [d.data_ptr() for d in dws], M)
         else:
+            dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
             _run_bwd(x, weights, hs, dout, dws, dx)
         return (dx, *[d if need else None for d, need in zip(dws, ctx.needs_input_grad[1:])])
 
@@ -253,15 +256,18 @@ class FusedMLPWNFunction(torch.autograd.Function):
         dev = x.device
         M = int(x.shape[0])
         dout = _as_row_broadcast(dout.to(x.dtype))
-        dw_all = torch.zeros(nw, dtype=torch.float32, device=dev)
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
         if _backward_impl() == "fused" and _fused_bwd_supported(dims, x.dtype):
+            # dW written by the library (MLPMK_BWD_WRITE_DW): no zero-fill launch.
+            dw_all = torch.empty(nw, dtype=torch.float32, device=dev)
             dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, dev)
             wb, gb, es = w_all.data_ptr(), dw_all.data_ptr(), w_all.element_size()
-            ops._bwd_raw(dev, dims, ops._fwd_code(x.dtype), x.data_ptr(), [wb + es * o for o in woff],
-                         [h.data_ptr() if h is not None else None for h in hs], dout.data_ptr(), row_stride,
-                         dx.data_ptr() if dx is not None else None, [gb + 4 * o for o in woff], M)
+            ops._bwd_raw(dev, dims, ops._fwd_code(x.dtype) | _lib.BWD_WRITE_DW, x.data_ptr(),
+                         [wb + es * o for o in woff], [h.data_ptr() if h is not None else None for h in hs],
+                         dout.data_ptr(), row_stride, dx.data_ptr() if dx is not None else None,
+                         [gb + 4 * o for o in woff], M)
         else:
+            dw_all = torch.zeros(nw, dtype=torch.float32, device=dev)
             _run_bwd(x, _split(w_all, dims), hs, dout, _split(dw_all, dims), dx)
         dv = dg = None
         if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:

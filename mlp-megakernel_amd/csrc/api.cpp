@@ -18,6 +18,7 @@ bool bwd_supported_dims(int L, const int* dims);
 bool bwd_supported_dtype(int L, const int* dims, int dtype);
 bool bwd_recompute_supported(int L, const int* dims);
 int bwd_dispatch(int L, const int* dims, const BwdParams& p, int dtype, hipStream_t st);
+int bwd_clear_dw(int L, const int* dims, float* const* dw, hipStream_t st);
 int bwd_workspace_bytes(int L, const int* dims, int64_t M, bool dx, int dtype, int64_t* bytes);
 int scratch_workspace(void** ptr, int64_t* bytes);
 int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* v, const void* g, void* w_out,
@@ -113,7 +114,7 @@ using namespace mlpmk;
 
 extern "C" {
 
-int mlpmk_version(void) { return 202; }  // 2.02: fp32 backward, mlpmk_bwd_supported_dtype, fp32 W from weight norm
+int mlpmk_version(void) { return 203; }  // 2.03: MLPMK_BWD_WRITE_DW (2.02: fp32 backward, mlpmk_bwd_supported_dtype)
 
 const char* mlpmk_status_string(int status) {
   switch (status) {
@@ -219,6 +220,8 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
                       bool use_scratch = false) {
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
+  const bool write_dw = (dtype & MLPMK_BWD_WRITE_DW) != 0;
+  dtype &= ~MLPMK_BWD_WRITE_DW;
   if ((rc = check_bwd_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   const bool dout_scalar = dout_row_stride == MLPMK_DOUT_SCALAR;
@@ -238,6 +241,7 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
     return fail(MLPMK_ERR_MISALIGNED, "dout_row_stride=%lld is not a multiple of 8 elements",
                 (long long)dout_row_stride);
   BwdParams p = {};
+  p.write_dw = write_dw;
   for (int l = 0; l < num_layers; ++l) {
     char name[16];
     snprintf(name, sizeof(name), "w[%d]", l);
@@ -247,7 +251,8 @@ static int bwd_common(int num_layers, const int* dims, int dtype, const void* x,
     p.w[l] = static_cast<const _Float16*>(w[l]);
     p.dw[l] = dw[l];
   }
-  if (M == 0) return MLPMK_OK;
+  // No rows: nothing to accumulate, or (written) the gradient is zero.
+  if (M == 0) return write_dw ? bwd_clear_dw(num_layers, dims, dw, static_cast<hipStream_t>(stream)) : MLPMK_OK;
   if ((rc = check_ptr(x, "x"))) return rc;
   if (dout_scalar) {
     if (!dout) return fail(MLPMK_ERR_INVALID_ARG, "dout is NULL");
@@ -320,6 +325,7 @@ int mlpmk_bwd_workspace_size(int num_layers, const int* dims, int dtype, int64_t
   *bytes = 0;
   int rc = check_dims(num_layers, dims);
   if (rc) return rc;
+  dtype &= ~MLPMK_BWD_WRITE_DW;  // (the same workspace either way)
   if ((rc = check_bwd_dtype(dtype))) return rc;
   if (M < 0) return fail(MLPMK_ERR_INVALID_ARG, "M=%lld is negative", (long long)M);
   if (!bwd_supported_dtype(num_layers, dims, dtype))

@@ -1099,7 +1099,8 @@ struct CombineLayout {
 };
 
 __global__ __launch_bounds__(kCombineCols* kCombineGroups) void bwd_combine_kernel(const float* __restrict__ part,
-                                                                                   int G, CombineLayout lay) {
+                                                                                   int G, CombineLayout lay,
+                                                                                   int write) {
   __shared__ float red[kCombineGroups][kCombineCols];
   const int c = threadIdx.x % kCombineCols, q = threadIdx.x / kCombineCols;
   const int64_t e = (int64_t)blockIdx.x * kCombineCols + c;
@@ -1124,7 +1125,20 @@ __global__ __launch_bounds__(kCombineCols* kCombineGroups) void bwd_combine_kern
   for (int i = 1; i < kMaxLayersHost; ++i)
     if (i < lay.L && e >= lay.off[i]) l = i;
   float* d = lay.dw[l] + (e - lay.off[l]);
-  *d += sum;
+  *d = write ? sum : *d + sum;  // MLPMK_BWD_WRITE_DW: written, else accumulated
+}
+
+// Clears the dW blocks of a launch whose workgroups add their partial sums
+// with atomics straight into dw, when dw is to be written (=).
+__global__ __launch_bounds__(256) void bwd_zero_dw_kernel(CombineLayout lay) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < lay.nelem;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    int l = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxLayersHost; ++i)
+      if (i < lay.L && e >= lay.off[i]) l = i;
+    lay.dw[l][e - lay.off[l]] = 0.0f;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1143,6 +1157,23 @@ static bool bdims_match(int L, const int* dims) {
   for (int i = 0; i <= L; ++i)
     if (dims[i] != N::d[i]) return false;
   return true;
+}
+
+// An empty batch with MLPMK_BWD_WRITE_DW: the gradient of no rows, dW = 0.
+int bwd_clear_dw(int L, const int* dims, float* const* dw, hipStream_t st) {
+  CombineLayout lay = {};
+  lay.L = L;
+  int64_t o = 0;
+  for (int l = 0; l < L; ++l) {
+    lay.off[l] = o;
+    o += (int64_t)dims[l] * dims[l + 1];
+    lay.dw[l] = dw[l];
+  }
+  lay.off[L] = lay.nelem = o;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(bwd_zero_dw_kernel, dim3((unsigned)((lay.nelem + 255) / 256)), dim3(256), 0, st, lay);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MLPMK_OK : hip_fail(e, "dW clear kernel launch");
 }
 
 // Grid of the persistent backward: one workgroup per round of R rows, at
@@ -1183,15 +1214,11 @@ static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
   if (rc != MLPMK_OK) return rc;
   BwdParams p = p_in;
   if (grid < kPartialMinGrid) p.part = nullptr;
-  (void)hipGetLastError();
-  hipLaunchKernelGGL((bwd_kernel<N, NW, DX, SEG>), dim3(grid), dim3(NW * 64), 0, st, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "bwd kernel launch");
-  if (p.part) {
-    // The dW blocks back to back with the layers' true widths (the same
-    // offsets flush_tile writes the partials at).
-    CombineLayout lay = {};
-    lay.L = N::L;
+  // The dW blocks back to back with the layers' true widths (the same
+  // offsets flush_tile writes the partials at).
+  CombineLayout lay = {};
+  lay.L = N::L;
+  {
     int64_t o = 0;
     for (int l = 0; l < N::L; ++l) {
       lay.off[l] = o;
@@ -1199,8 +1226,20 @@ static int launch_bwd(const BwdParams& p_in, hipStream_t st) {
       lay.dw[l] = p.dw[l];
     }
     lay.off[N::L] = lay.nelem = o;
+  }
+  (void)hipGetLastError();
+  hipError_t e = hipSuccess;
+  if (p.write_dw && !p.part) {  // atomics straight into dw: clear it first
+    hipLaunchKernelGGL(bwd_zero_dw_kernel, dim3((unsigned)((lay.nelem + 255) / 256)), dim3(256), 0, st, lay);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "dW clear kernel launch");
+  }
+  hipLaunchKernelGGL((bwd_kernel<N, NW, DX, SEG>), dim3(grid), dim3(NW * 64), 0, st, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bwd kernel launch");
+  if (p.part) {
     hipLaunchKernelGGL(bwd_combine_kernel, dim3((unsigned)((lay.nelem + kCombineCols - 1) / kCombineCols)),
-                       dim3(kCombineCols * kCombineGroups), 0, st, p.part, grid, lay);
+                       dim3(kCombineCols * kCombineGroups), 0, st, p.part, grid, lay, p.write_dw);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "bwd combine kernel launch");
   }
@@ -1291,6 +1330,7 @@ static int launch_bwd_split(const BwdParams& p, int L, hipStream_t st) {
   a.dx = dzs;
   a.M = p.M;
   a.part = part;
+  a.write_dw = p.write_dw;
   int rc = launch_bwd<TOP, bwd_waves<TOP, true, true>(), true, true>(a, st);
   if (rc != MLPMK_OK) return rc;
   BwdParams b = {};
@@ -1306,6 +1346,7 @@ static int launch_bwd_split(const BwdParams& p, int L, hipStream_t st) {
   b.dx = p.dx;
   b.M = p.M;
   b.part = part;
+  b.write_dw = p.write_dw;
   return launch_bwd_any<BOT>(b, st);
 }
 

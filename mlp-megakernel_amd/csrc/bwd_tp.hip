@@ -303,6 +303,20 @@ __global__ __launch_bounds__((DgGeo<N, DX>::NWV * 64)) void tp_dgrad_kernel(TpPa
   const int lane = threadIdx.x & 63;
   W wv{p, tile, lane, lane & 31, lane >> 5, __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))};
   const int64_t nblk = (p.M + 31) / 32;
+  if (p.zero_dw) {
+    // Written (=) rather than accumulated dW: cleared here, before the
+    // weight-gradient pass adds its tiles (the next launch on the stream).
+    // Every layer's d[l] * d[l+1] is a multiple of 128 (widths multiples of
+    // 16, the output width of 8) and dw is 16-byte aligned.
+    const int64_t nthr = (int64_t)gridDim.x * blockDim.x;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+#pragma unroll
+    for (int l = 0; l < N::L; ++l) {
+      const int64_t n4 = (int64_t)dimw<N>(p, l) * dimw<N>(p, l + 1) / 4;
+      f32x4* const d = reinterpret_cast<f32x4*>(p.dw[l]);
+      for (int64_t i = tid; i < n4; i += nthr) d[i] = f32x4{};
+    }
+  }
   if constexpr (RES) {
     wv.template load_h<>((int64_t)blockIdx.x * 32, wv.hn);  // (from HBM: the longest wait first)
     wv.template load_all_frags<>();                          // (L2 hits after the first workgroup)
@@ -762,6 +776,7 @@ int tp_dispatch(int L, const int* dims, int dtype, const BwdParams& bp, void* ws
   p.dout_stride = bp.dout_stride;
   p.dx = bp.dx;
   p.M = bp.M;
+  p.zero_dw = bp.write_dw;
   for (int l = 0; l <= L; ++l) p.dims[l] = dims[l];
   const int es = dtype == MLPMK_DTYPE_F32 ? 4 : 2;
   char* c = static_cast<char*>(ws);

@@ -30,6 +30,8 @@ struct BwdParams {
   _Float16* dx;                        // nullable
   float* dw[kMaxLayersHost];           // fp32 [d[l], d[l+1]], accumulated with atomics
   int64_t M;
+  // Nonzero: dw is written (=), not accumulated into (MLPMK_BWD_WRITE_DW).
+  int write_dw;
   // Null: every workgroup adds its weight-gradient partial sums to dw with
   // fp32 atomics.  Otherwise workgroup b stores them, laid out like the dW
   // blocks back to back, at part + b * (sum_l d[l] * d[l+1]), and a second
@@ -61,6 +63,9 @@ struct TpParams {
   void* dz[kMaxLayersHost];            // dz_l, l = 0 .. L-2: [M, d[l+1]] in the workspace
   int64_t M;
   int64_t chunk_rows;                  // rows per weight-gradient chunk
+  // Nonzero: the data-gradient pass clears dw before the weight-gradient
+  // pass adds to it (MLPMK_BWD_WRITE_DW).
+  int zero_dw;
   int dims[kMaxLayersHost + 1];
 };
 

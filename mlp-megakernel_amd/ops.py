@@ -360,9 +360,11 @@ def _workspace_bytes(idx, dims, M, with_dx, code):
     return n
 
 
-def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
+def bwd(x, weights, stash, dout, dws, dx=None, workspace=True, accumulate=True):
     """Backward megakernel: accumulates fp32 weight gradients into ``dws``
-    (callers zero them first) and writes ``dx`` if given.
+    (callers zero them first), or with ``accumulate=False`` writes them
+    (``MLPMK_BWD_WRITE_DW``: their prior contents do not matter), and
+    writes ``dx`` if given.
 
     ``x``, the weights, ``dout`` and ``dx`` are fp16, bf16 or fp32 (fp32
     tensors run with bf16 hi/lo split operands: fp32's exponent range).
@@ -378,7 +380,7 @@ def bwd(x, weights, stash, dout, dws, dx=None, workspace=True):
     """
     dev = x.device
     xd = x.dtype
-    code = _fwd_code(xd)
+    code = _fwd_code(xd) | (0 if accumulate else _lib.BWD_WRITE_DW)
     if not _ok(x, xd, dev):
         _require(x, "x", xd, dev)
     for i, w in enumerate(weights):

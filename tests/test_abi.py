@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     lib = _lib.get()
-    assert lib.mlpmk_version() >= 201  # MLPMK_DOUT_SCALAR
+    assert lib.mlpmk_version() >= 203  # MLPMK_DOUT_SCALAR (201), MLPMK_BWD_WRITE_DW (203)
     for code, text in [(0, b"ok"), (2, b"unsupported shape"), (5, b"no usable gfx950 device")]:
         assert lib.mlpmk_status_string(code) == text
     assert lib.mlpmk_status_string(99) == b"unknown status"
@@ -117,6 +117,13 @@ def test_bwd_validation_codes():
     # passes through the workspace: mlpmk_bwd (none) refuses them
     assert call(dtype=0) == INVALID and b"mlpmk_bwd_ws" in lib.mlpmk_last_error()
     assert call(dtype=3) == INVALID
+    # MLPMK_BWD_WRITE_DW (0x100) rides in the dtype argument: validated like the
+    # bare type, an unknown type with it is still invalid
+    assert call(dtype=1 | 0x100, m=-1) == INVALID and call(dtype=3 | 0x100) == INVALID
+    assert call(dtype=0 | 0x100) == INVALID and b"mlpmk_bwd_ws" in lib.mlpmk_last_error()
+    if not torch.cuda.is_available() and ops.bwd_supported(d):
+        # an empty batch with dW written still writes dW = 0: a launch, which needs the device
+        assert call(dtype=1 | 0x100, m=0) in (NODEV, HIPERR)
     if ops.bwd_supported(d):
         assert call(stride=64) == INVALID  # below the output width
         assert call(stride=130) == MISALIGNED
