@@ -392,8 +392,15 @@ struct WgSrc {
   uint32_t bytes;    // resource size from base
 };
 
-template <class N, int EM, int TQI, int TQO>
-__global__ __launch_bounds__(256) void tp_wgrad_kernel(TpParams p) {
+// MINW: waves per SIMD the register allocation must leave room for.  2 when
+// the grid has more workgroups than CUs: two workgroups per CU then keep
+// twice the rows in flight (fp32 3L-128 at 131072 rows 228 -> 217 us,
+// 128-256-256-128 400 -> 373 us per backward; the 128x128 blocks need 222-228
+// VGPRs + 64 AGPRs left to themselves, one workgroup per CU).  1 for grids of
+// at most one workgroup per CU (128-256-256-128 at 4096 rows: 38.2 us, 40.7
+// with the tighter budget).
+template <class N, int EM, int TQI, int TQO, int MINW>
+__global__ __launch_bounds__(256, MINW) void tp_wgrad_kernel(TpParams p) {
   using G = WgGeo<EM, TQI, TQO>;
   constexpr int F = G::F, RP = G::RP, NT = G::NT;
   __shared__ __attribute__((aligned(16))) char smem[G::LDS_BYTES];
@@ -670,9 +677,12 @@ void wgrad_chunks(int L, const int* dims, int64_t M, bool f32, int cus, int* S_o
 }
 
 template <class N, int EM, int TQ>
-int launch_wgrad(const TpParams& p, int S, int nqb, hipStream_t st) {
+int launch_wgrad(const TpParams& p, int S, int nqb, int cus, hipStream_t st) {
   (void)hipGetLastError();
-  hipLaunchKernelGGL((tp::tp_wgrad_kernel<N, EM, TQ, TQ>), dim3(S, nqb), dim3(256), 0, st, p);
+  if ((int64_t)S * nqb > cus)
+    hipLaunchKernelGGL((tp::tp_wgrad_kernel<N, EM, TQ, TQ, 2>), dim3(S, nqb), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((tp::tp_wgrad_kernel<N, EM, TQ, TQ, 1>), dim3(S, nqb), dim3(256), 0, st, p);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? MLPMK_OK : hip_fail(e, "two-pass wgrad kernel launch");
 }
@@ -730,9 +740,10 @@ int dispatch_l(const TpParams& p, const int* dims, int S, hipStream_t st) {
   const int nqb = quad_blocks(L, dims, tq);
   typedef typename GenTp<L>::W NW;
   if (L == 3 && is_3l128(L, dims))
-    rc = tq == 1 ? launch_wgrad<TNet3L128, EM, 1>(p, S, nqb, st) : launch_wgrad<TNet3L128, EM, 2>(p, S, nqb, st);
+    rc = tq == 1 ? launch_wgrad<TNet3L128, EM, 1>(p, S, nqb, cus, st)
+                 : launch_wgrad<TNet3L128, EM, 2>(p, S, nqb, cus, st);
   else
-    rc = tq == 1 ? launch_wgrad<NW, EM, 1>(p, S, nqb, st) : launch_wgrad<NW, EM, 2>(p, S, nqb, st);
+    rc = tq == 1 ? launch_wgrad<NW, EM, 1>(p, S, nqb, cus, st) : launch_wgrad<NW, EM, 2>(p, S, nqb, cus, st);
   return rc;
 }
 
