@@ -566,6 +566,11 @@ def main():
     ap.add_argument("--train-step", type=int, default=None, metavar="M",
                     help="counter-collection runs of the training kernels: only the WN training step at M rows "
                          "(3 layers; 5 with --config 5l128; no headline, no other legs); prints its timing JSON")
+    ap.add_argument("--fwd-step", type=int, default=None, metavar="M",
+                    help="counter-collection runs of one forward config: only the forward of --config at M rows "
+                         "(element type --fwd-dtype; buffers rotated as for the other configs); prints its JSON")
+    ap.add_argument("--fwd-dtype", choices=("fp16", "bf16", "fp32"), default="fp16",
+                    help="with --fwd-step: the tensors' element type")
     ap.add_argument("--train-dtype", choices=("fp16", "bf16", "fp32"), default="fp16",
                     help="with --train-step: x's type (fp32 runs the fp32-tensor kernels)")
     ap.add_argument("--train-hidden", type=int, default=128,
@@ -596,6 +601,14 @@ def main():
         with gc_paused():
             print(json.dumps({"latency_sweep": latency_sweep(torch, ops, CONFIG_DIMS[args.config]),
                               "config": args.config}))
+        return
+
+    if args.fwd_step:
+        fdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.fwd_dtype]
+        with gc_paused():
+            r = fwd_bench(torch, ops, CONFIG_DIMS[args.config], args.fwd_step, args.config == "narrow",
+                          steps=args.steps, warmup=args.warmup, dtype=fdt)
+        print(json.dumps({"forward": {f"{args.config} {args.fwd_dtype} M={args.fwd_step}": r}}))
         return
 
     if args.train_step:
