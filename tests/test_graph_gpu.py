@@ -124,6 +124,45 @@ def test_whole_training_step_graph(m):
         _check_oracle(got[2], o_dg, f"replay {r}: dg vs oracle", grad=True)
 
 
+@pytest.mark.parametrize("m", [4096, 131072])
+@pytest.mark.parametrize("kind", ["fp32", "h256"])
+def test_training_step_graph_two_pass_shapes(kind, m):
+    # The weight-norm module with fp32 tensors (bf16 hi/lo split operands)
+    # and with hidden width 256: both train through the two-pass backward at
+    # every M (dz through the workspace, weight gradients written by atomics
+    # after the data-gradient pass cleared dW).  Replays with fresh inputs and
+    # eager work in between, each against an eager copy of the model.
+    torch.manual_seed(1)
+    model = (fused_mlp.FusedMLPSoftplusWN() if kind == "fp32" else fused_mlp.FusedMLPSoftplusWN(H=256)).cuda()
+    ref_model = copy.deepcopy(model)
+    dt = torch.float32 if kind == "fp32" else torch.float16
+    static_x = _fresh_x(m, 0).to(dt)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            _eager_step(model, static_x)
+    torch.cuda.current_stream().wait_stream(side)
+    model.v_all.grad = None
+    model.g_all.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = model(static_x)
+        static_out.sum().backward()
+    static_dv, static_dg = model.v_all.grad, model.g_all.grad
+    assert static_out.dtype == dt and static_dv.dtype == torch.float32
+    for r in range(3):
+        static_x.copy_(_fresh_x(m, 200 + r).to(dt))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (static_out.clone(), static_dv.clone(), static_dg.clone())
+        ref = _eager_step(ref_model, static_x.clone())  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], ref[0]), f"{kind} replay {r}: out"
+        _same(got[1], ref[1], False, f"{kind} replay {r}: dv")
+        _same(got[2], ref[2], False, f"{kind} replay {r}: dg")
+
+
 def test_make_graphed_callables_training():
     m = 16384
     torch.manual_seed(1)
