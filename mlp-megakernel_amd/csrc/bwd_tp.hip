@@ -29,10 +29,13 @@
 // Pass 1, tp_dgrad_kernel (persistent over 32-row blocks, one workgroup per
 // block at a time): wave w owns output features [32w, 32w + 32) of every
 // data-gradient layer, with its A fragments (16 contiguous bytes of a W_l
-// row per lane) loaded once into registers; layers hand dz between waves
-// through two LDS tiles, and every dz_{l-1}, l >= 1, is also written to the
-// workspace.  At M = 4096 that is 128 workgroups each running a 3-layer
-// chain of 8-MFMA steps, instead of 32 running whole 128-row rounds.
+// row per lane) loaded once into registers for the 3-layer 128-wide network
+// -- which then loads the next block's stash rows while the current block
+// computes -- and read from L2 per block and layer otherwise; layers hand dz
+// between waves through two LDS tiles, and every dz_{l-1}, l >= 1, is also
+// written to the workspace.  When dw is to be written (MLPMK_BWD_WRITE_DW)
+// this pass also clears it.  At M = 4096 that is 128 workgroups each running
+// a chain of 8-MFMA steps, instead of 32 running whole 128-row rounds.
 //
 // Pass 2, tp_wgrad_kernel: a workgroup owns a TQI x TQO block of 64 x 64
 // "quads" of one dW_l and a chunk of rows; it stages a_l (from x or the
@@ -40,8 +43,9 @@
 // as 16-bit tiles [row][feature] in LDS, and its waves read both MFMA
 // operands with the transposing ds_read_b64_tr_b16, as bwd.hip's wgrad does.
 // Each wave adds its 32 x 32 tiles to dw with fp32 atomics: about two
-// workgroups per CU, each adding 4096 elements, so the atomics are spread
-// over the whole chip (measured at M = 4096 / 16384: 14.2 / 24.1 us per
+// workgroups per CU (with a register budget that lets both stay resident
+// when the grid exceeds the CU count), each adding 4096 elements, so the
+// atomics are spread over the whole chip (measured at M = 4096 / 16384: 14.2 / 24.1 us per
 // backward, against 16.4 / 31.0 us with per-chunk partial sums and a
 // combine kernel).  The summation order of dw is therefore not fixed.
 //
