@@ -102,14 +102,24 @@ struct DgGeo {
 // RES: every layer's fragments stay in registers for the whole kernel
 // (loaded once per workgroup); otherwise (widths above 128, whose fragments
 // would not fit beside the rest) each layer's are read from L2 right before
-// its MFMA chain, every block.
+// its MFMA chain, every block -- except, in the 16-bit kernels of widths up
+// to 256 (STG), those of the data-gradient layer with the most weights: each
+// wave copies its own into LDS once (NWV x 16 K-steps x 1 KiB = 128 KiB,
+// beside the 32 KiB exchange tiles: the workgroup's whole 160 KiB, which its
+// registers already hold to one workgroup per CU) and reads them from there.
+// 128-256-256-128 at 131072 rows: L2 reads of fragments per 32-row block
+// 192 -> 64 KiB.
 template <class N, int EM, bool DX, bool RES>
 struct DgWave {
   using G = DgGeo<N, DX>;
   static constexpr int L = N::L, CH = G::CH, NT = EM == EM_F32 ? 2 : 1;
+  static constexpr bool STG = !RES && EM != EM_F32 && G::NWV == 8;
+  static constexpr int STG_ELEMS = STG ? G::NWV * G::KSM * 64 : 1;  // f16x8 payloads
   const TpParams& p;
   f16x8 (*tile)[NT][32 * CH];  // [2][NT][32 * CH]
   int lane, n, g, w;
+  f16x8* stg = nullptr;               // STG: [NWV][KSM][64] fragments of layer stg_l
+  int stg_l = -1;
   int par = 0;                        // exchange tile of the next hand-over
   Opnd fr[RES ? L : 1][G::KSM];       // this wave's A fragments (output block w)
   Opnd B[G::KSM];                     // B operands of the current layer: dz_l of row n
@@ -129,10 +139,54 @@ struct DgWave {
 #pragma unroll
     for (int s = 0; s < G::ks(l); ++s) {
       const int c = 16 * s + 8 * g;
+      if (N::gen && 16 * s >= Nout) {  // a whole K-step past the true width: no load
+        f[s] = Opnd{f16x8{}, f16x8{}};
+        continue;
+      }
       f[s] = load_op<EM>(r, (uint32_t)(row * Nout + c));
       if (N::gen && c >= Nout) f[s] = Opnd{f16x8{}, f16x8{}};
     }
   }
+  // STG: copies this wave's fragments of the data-gradient layer with the
+  // most weights (true widths) into its LDS slots.
+  __device__ __forceinline__ void stage_largest() {
+    int64_t best = 0;
+    for (int l = G::LO; l < L; ++l) {
+      const int64_t e = (int64_t)dimw<N>(p, l) * dimw<N>(p, l + 1);
+      if (e > best) {
+        best = e;
+        stg_l = l;
+      }
+    }
+    stage_layer<G::LO>();
+  }
+  template <int l>
+  __device__ __forceinline__ void stage_layer() {
+    if constexpr (l < L) {
+      if (l == stg_l && owns(l)) {
+        Opnd f[G::KSM];
+        load_frags<l>(f);
+#pragma unroll
+        for (int s = 0; s < G::ks(l); ++s) stg[(w * G::KSM + s) * 64 + lane] = f[s].h;
+      }
+      stage_layer<l + 1>();
+    }
+  }
+  // Layer l's fragments: from the LDS copy if it holds them, else from L2.
+  template <int l>
+  __device__ __forceinline__ void frags_of(Opnd (&f)[G::KSM]) const {
+    if (STG && l == stg_l) {
+      const int Nout = dimw<N>(p, l + 1);
+#pragma unroll
+      for (int s = 0; s < G::ks(l); ++s) {
+        f[s].h = (N::gen && 16 * s >= Nout) ? f16x8{} : stg[(w * G::KSM + s) * 64 + lane];
+        f[s].l = f16x8{};
+      }
+      return;
+    }
+    load_frags<l>(f);
+  }
+
   template <int l = G::LO>
   __device__ __forceinline__ void load_all_frags() {
     if constexpr (l < L) {
@@ -245,7 +299,7 @@ struct DgWave {
           }
         } else {
           Opnd f[G::KSM];
-          load_frags<l>(f);
+          frags_of<l>(f);
           if constexpr (l >= 1) load_h_one<l>(row0, h);
 #pragma unroll
           for (int s = 0; s < G::ks(l); ++s) {
@@ -305,7 +359,12 @@ __global__ __launch_bounds__((DgGeo<N, DX>::NWV * 64)) void tp_dgrad_kernel(TpPa
   static_assert(G::valid(), "two-pass backward shape");
   __shared__ f16x8 tile[2][W::NT][32 * G::CH];  // two exchange tiles (hi, and lo with fp32 tensors)
   const int lane = threadIdx.x & 63;
+  __shared__ f16x8 stage[W::STG_ELEMS];  // STG: one layer's fragments
   W wv{p, tile, lane, lane & 31, lane >> 5, __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))};
+  if constexpr (W::STG) {
+    wv.stg = stage;
+    wv.stage_largest();  // (each wave reads back only what it wrote: no barrier)
+  }
   const int64_t nblk = (p.M + 31) / 32;
   if (p.zero_dw) {
     // Written (=) rather than accumulated dW: cleared here, before the
