@@ -460,8 +460,8 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype, hidde
         "graph_ms_per_step": round(gms, 5),
         "graph_rows_per_s": m / (gms * 1e-3),
         "graph_roofline_frac": round(nbytes * m / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "launches": "wn_fwd + fwd(stash) + dW zero-fill + bwd + wn_bwd" if n_layers == 3 else
-                    "wn_fwd + fwd(stash) + dW zero-fill + bwd (layers 4..3, then 2..0) + wn_bwd",
+        "launches": "wn_fwd + fwd(stash) + bwd (writes dW) + wn_bwd" if n_layers == 3 else
+                    "wn_fwd + fwd(stash) + bwd (layers 4..3 write dW, then 2..0) + wn_bwd",
         "x_buffers": nx,
         "recompute_h_last": rc,
         "dims": list(dims),
@@ -471,7 +471,7 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype, hidde
 
 def backward_comparison(torch, ops, m, steps=50, warmup=10):
     """The 3-layer backward at M rows, loss = out.sum(): the library's fused
-    backward (mlpmk_bwd_ws + combine, dW zero-filled first, as autograd does)
+    backward (mlpmk_bwd_ws + combine, writing dW, as the autograd Functions do)
     beside the reference's large-M fallback restated with PyTorch GPU ops
     (/root/reference/mlp_fused.md:114-146: data-gradient GEMMs on
     rocBLAS/hipBLASLt in fp16 with fp32 accumulation, weight-gradient GEMMs
@@ -488,9 +488,7 @@ def backward_comparison(torch, ops, m, steps=50, warmup=10):
     dws = [torch.zeros((128, 128), dtype=torch.float32, device="cuda") for _ in range(3)]
 
     def library(_):
-        for d in dws:
-            d.zero_()
-        ops.bwd(x, ws, hs, dout, dws)
+        ops.bwd(x, ws, hs, dout, dws, accumulate=False)
 
     h1, h2 = hs
     wts = [w.t().contiguous() for w in ws]  # W^T, as the fallback keeps them for dgrad
