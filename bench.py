@@ -434,12 +434,15 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype, hidde
         for i in range(3):
             step(i)
     torch.cuda.current_stream().wait_stream(side)
+    # The graphs share one memory pool, so their intermediates (stash, dz,
+    # output) reuse the same blocks as the eager steps do; they are replayed
+    # in capture order, which is what sharing a pool requires.
     graphs = []
     for k in range(nx):
         model.v_all.grad = None
         model.g_all.grad = None
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, pool=graphs[0].pool() if graphs else None):
             model(xs[k]).sum().backward()
         graphs.append(g)
     with gc_paused():
