@@ -25,13 +25,19 @@
 //    pre-permuted.  The chunk rows are XOR-swizzled by whole 16-byte pieces
 //    (piece p of row r at p ^ piece_swz(r)), which the loads apply by
 //    choosing each lane's source piece.
-//  * The weights are used as stored, so the base-2 scalings of the 128-wide
-//    kernels move to the accumulators: u = z log2 e on layer 0, out = acc ln 2
-//    (times the halving below) on the last.
+//  * The weights are used as stored, so the activations stay in natural
+//    units: u = z log2 e for the base-2 evaluation, h = ln 2 sp2(u).
 //  * Softplus in the exact form everywhere (sp2 with u substituted past 2^u's
-//    overflow, hidden operands handed on halved and every later accumulator
-//    doubled, so hidden values up to fp16's 65,504 survive): a wave cannot
+//    overflow, h rounded to the tensor format as the reference rounds its
+//    hidden h, so hidden values up to fp16's 65,504 survive): a wave cannot
 //    re-run a block on its own here, since the ring has moved on.
+//    (Measured and not kept, at 1M rows: the 128-wide kernels' fast form
+//    with a per-round exact re-run decided by a workgroup vote, and chunks
+//    run as straight-line code with the MFMA chain of block mb + 1 issued
+//    between block mb's softplus instructions: 0.3835 -> 0.371 ms together,
+//    at 2.5x the compile time.  The kernel issues VALU or MFMA work in only
+//    ~62 % of its cycles: its two waves per SIMD wait on the per-chunk
+//    barrier and on each MFMA's transposed fragment reads.)
 #include "device_common.h"
 #include "host_common.h"
 #include "params.h"
@@ -163,30 +169,27 @@ struct WideWave {
     return acc;
   }
 
-  // Hidden layer l, block mb: softplus in the exact form, operands halved
-  // into out[2mb], out[2mb + 1]; the fp32 stash (natural units) if asked.
+  // Hidden layer l, block mb: softplus into out[2mb], out[2mb + 1]; the
+  // fp32 stash if asked.  Natural units, as the reference keeps them:
+  // u = acc log2 e, h = ln 2 * sp2(u) with u substituted where 2^u overflows
+  // (softplus(z) = z there), handed on as h rounded to the tensor format --
+  // the rounding the reference applies to its hidden h (kernel.py:110), so
+  // hidden values up to fp16's 65,504 survive as they do there.
   template <int l, int mb>
   __device__ __forceinline__ void hidden(const f32x16& acc, f16x8 (&out)[kWideKS]) {
-    constexpr float kIn = l == 0 ? kLog2e : 2.0f;
-    float s[16];
+    float h[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float u = acc[e] * kIn;
-      s[e] = sp2_fix(u, sp2(u));
+      const float u = acc[e] * kLog2e;
+      h[e] = kLn2 * sp2_fix(u, sp2(u));
     }
-    out[2 * mb] = pack8<BF>(0.5f * s[0], 0.5f * s[1], 0.5f * s[2], 0.5f * s[3], 0.5f * s[4], 0.5f * s[5],
-                            0.5f * s[6], 0.5f * s[7]);
-    if (2 * mb + 1 < kWideKS)
-      out[2 * mb + 1] = pack8<BF>(0.5f * s[8], 0.5f * s[9], 0.5f * s[10], 0.5f * s[11], 0.5f * s[12], 0.5f * s[13],
-                                  0.5f * s[14], 0.5f * s[15]);
+    out[2 * mb] = pack8<BF>(h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]);
+    if (2 * mb + 1 < kWideKS) out[2 * mb + 1] = pack8<BF>(h[8], h[9], h[10], h[11], h[12], h[13], h[14], h[15]);
     if constexpr (STASH) {
       const int HW = d[l + 1], c = 32 * mb + 8 * g;
       if (p.stash[l]) {
         const rsrc_t sr = make_rsrc(p.stash[l] + row0 * HW, nrows() * (uint32_t)HW * 4u);
         const uint32_t e4 = (uint32_t)(n * HW + c) * 4;
-        float h[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) h[e] = s[e] * kLn2;
         if (c < HW) {
           buf_store16<kStashStore>((f32x4){h[0], h[1], h[2], h[3]}, sr, e4);
           buf_store16<kStashStore>((f32x4){h[4], h[5], h[6], h[7]}, sr, e4 + 16);
@@ -203,11 +206,10 @@ struct WideWave {
   // 32mb + 16 + 8g + [0..7].
   template <int mb>
   __device__ __forceinline__ void store_out(const f32x16& acc) const {
-    constexpr float kOut = 2.0f * kLn2;  // halved inputs, base-2 units
     const int OW = d[L], c = 32 * mb + 8 * g;
     const rsrc_t orr = make_rsrc(p.out + row0 * OW, nrows() * (uint32_t)OW * 2u);
     const uint32_t e = (uint32_t)(n * OW + c);
-    const f32x16 v = acc * kOut;
+    const f32x16& v = acc;  // natural units
     constexpr int P = kStashStore;  // rows of up to 512 bytes, written a piece at a time: let L2 merge them
     if (OW % 8 == 0) {
       if (c < OW) buf_store16<P>(pack8<BF>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), orr, e * 2);
@@ -269,10 +271,7 @@ struct WideRound {
       constexpr int mb = 4 * cc + mbl;
       if (kWideCols * cc + 32 * mbl < w.d[l + 1]) {
         const f32x16 acc = w.template chain<l>(sb, mbl, (l % 2 == 0) ? w.A : w.B);
-        if constexpr (l + 1 < L)
-          w.template hidden<l, mb>(acc, (l % 2 == 0) ? w.B : w.A);
-        else
-          w.template store_out<mb>(acc);
+        finish<l, mb>(w, acc);
       } else if constexpr (l + 1 < L) {
         // Past the layer's width: zero operands for the next layer's padded K-steps.
         auto& out = (l % 2 == 0) ? w.B : w.A;
@@ -281,6 +280,16 @@ struct WideRound {
       }
       block<l, cc, mbl + 1>(w, sb);
     }
+  }
+
+  // Softplus and hand-off (hidden layers) or output store (last layer) of
+  // global block mb.
+  template <int l, int mb>
+  static __device__ __forceinline__ void finish(W& w, const f32x16& acc) {
+    if constexpr (l + 1 < L)
+      w.template hidden<l, mb>(acc, (l % 2 == 0) ? w.B : w.A);
+    else
+      w.template store_out<mb>(acc);
   }
 
   // Layer l of the round: its chunks in order.  A chunk past the layer's
@@ -318,11 +327,12 @@ __global__ __launch_bounds__(NW * 64) void fwd_wide_kernel(FwdParams p) {
 #pragma unroll
   for (int i = 0; i <= L; ++i) w.d[i] = __builtin_amdgcn_readfirstlane(p.dims[i]);  // wave-uniform: SGPRs
   w.init();
+  using Round = WideRound<L, KS0, BF, STASH, NW>;
   const int64_t nrounds = (p.M + kRows - 1) / kRows;
   int64_t rnd = blockIdx.x;
   if (rnd >= nrounds) return;  // whole workgroup: no barrier follows
   w.template load_chunk<0>(0, 0);
-  WideRound<L, KS0, BF, STASH, NW>::sync();
+  Round::sync();
   int q = 0;
   for (; rnd < nrounds; rnd += gridDim.x) {
     // Opaque copies of the widths: everything derived from them (chunk
@@ -333,7 +343,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_wide_kernel(FwdParams p) {
     for (int i = 0; i <= L; ++i) asm volatile("" : "+s"(w.d[i]));
     w.row0 = rnd * kRows + 32 * w.wid;
     w.load_x();
-    WideRound<L, KS0, BF, STASH, NW>::template layer<0>(w, q, rnd + gridDim.x < nrounds);
+    Round::template layer<0>(w, q, rnd + gridDim.x < nrounds);
   }
 }
 

@@ -117,6 +117,61 @@ def test_wide_forward_large_preactivations_and_nonfinite_rows():
     assert np.all(err <= TOL + TOL * np.abs(ref[~bad]) + TOL * row_scale[~bad] * big[~bad][:, None]), float(err.max())
 
 
+# M = 4096: 4-wave rounds of 128 rows, one round per workgroup; M = 300,000:
+# 8-wave rounds of 256 rows, 4-5 rounds per workgroup, large rows in first,
+# middle and last rounds.
+@pytest.mark.parametrize("m", [4096, 300000])
+@pytest.mark.parametrize("stash", [False, True])
+def test_wide_large_preactivations_up_to_the_fp16_limit(stash, m):
+    # Identity weights padded to 256: out = softplus(softplus(x)) on the first
+    # 128 features.  Past z = 88.7, 2^u overflows fp32 and softplus(z) = z
+    # must come out, as the reference's z > 20 branch gives, up to the fp16
+    # limit of its hidden h (kernel.py:108,110): h = 65,504 stays finite
+    # (with hidden values carried at 1/2 of the base-2 value the rounding
+    # of 65,504 * 1.44 / 2 gave an output of 65,520, which is inf in fp16).
+    dims = (128, 256, 256, 128)
+    z = np.array([88.0, 88.8, 89.0, 100.0, 200.0, 1000.0, 3.0e4, 4.6e4, 5.0e4, 65504.0], dtype=np.float32)
+    rng = np.random.default_rng(23)
+    x = (rng.standard_normal((m, 128)) * 0.5).astype(np.float16)
+    rows = [3, 40, m - 1] + ([256 * 257 + 5, 256 * 600 + 255] if m > 200000 else [2000])
+    for r in rows:
+        x[r, : z.size] = z.astype(np.float16)
+    ws = [np.eye(dims[i], dims[i + 1], dtype=np.float16) for i in range(3)]
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    res = ops.fwd(xd, wd, stash=stash)
+    out = (res[0] if stash else res).float().cpu().numpy()
+    idx = np.unique(np.concatenate([rows, rng.choice(m, min(m, 4096), replace=False)]))
+    ref, ref_h = orc.forward(x[idx], ws, return_hidden=True)
+    _check(out[idx], ref, "identity weights, large z")
+    for r in rows:
+        np.testing.assert_allclose(out[r, : z.size], z, rtol=2e-3)
+    if stash:
+        for i, h in enumerate(res[1]):
+            ok, err, _ = orc.allclose_report(h.cpu().numpy()[idx], ref_h[i], 2e-3, 2e-3)
+            assert ok, f"stash h{i + 1}: max|err| {err}"
+        assert torch.equal(res[0], ops.fwd(xd, wd))
+
+
+@pytest.mark.parametrize("m", [4096, 131072])
+def test_wide_scaled_inputs_overflow_in_every_round(m):
+    # x scaled so that a large share of pre-activations pass z = 88.7 in
+    # every layer, in every round; every 7th row keeps its ordinary scale
+    # and shares those rounds.
+    dims = (128, 256, 256, 128)
+    x, ws = orc.make_inputs(dims, m, seed=29)
+    x = (x.astype(np.float32) * 300.0).astype(np.float16)
+    small = np.zeros(m, dtype=bool)
+    small[::7] = True
+    x[small] = (x[small].astype(np.float32) / 300.0).astype(np.float16)
+    out = ops.fwd(torch.from_numpy(x).cuda(), [torch.from_numpy(w).cuda() for w in ws]).float().cpu().numpy()
+    ref = orc.forward(x, ws, round_hidden=True)
+    assert np.isfinite(ref).all()
+    _check(out[small], ref[small], "ordinary rows in exact rounds")
+    big_err = np.abs(out[~small] - ref[~small]).max()
+    assert big_err <= 2e-3 * np.abs(ref[~small]).max(), (big_err, np.abs(ref[~small]).max())
+
+
 def test_wide_launcher_matches_model():
     dims, m = (128, 256, 256, 64), 4096
     x, ws = orc.make_inputs(dims, m, seed=19)
