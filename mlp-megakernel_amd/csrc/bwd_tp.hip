@@ -725,8 +725,19 @@ int quad_blocks(int L, const int* dims, int tq) {
 #define MLPMK_TP_WG_PER_CU 2
 #endif
 
+// Longest row chunk with fp32 tensors.  A chunk's products of split
+// operands accumulate in one MFMA chain per tile, three MFMAs per K-step, and
+// over long chains that sum drifts: the last layer's dW of a 40,000,037-row
+// batch (broadcast dout, so its exact value is a column sum) was off by
+// 1.6e-4 with chunks of 234 K rows and 6.9e-5 with chunks of 117 K rows;
+// the 16-bit one-pass kernel, one MFMA per K-step, stays at 1.6e-6 over
+// 156 K rows per workgroup.  Past this length the pass takes more chunks
+// (more atomics) instead.
+constexpr int64_t kF32MaxChunkRows = 8192;
+
 // Row chunks of the weight-gradient pass: enough chunks for about
-// MLPMK_TP_WG_PER_CU workgroups per CU, each a whole number of passes.
+// MLPMK_TP_WG_PER_CU workgroups per CU, each a whole number of passes (with
+// fp32 tensors, at most kF32MaxChunkRows rows).
 void wgrad_chunks(int L, const int* dims, int64_t M, bool f32, int cus, int* S_out, int64_t* rows_out) {
   const int tq = wgrad_tq(L, dims, M);
   const int rp = (tq == 1 ? 256 : 128) / (f32 ? 2 : 1);  // rows per pass (WgGeo::RP)
@@ -735,6 +746,7 @@ void wgrad_chunks(int L, const int* dims, int64_t M, bool f32, int cus, int* S_o
   if (smax < 1) smax = 1;
   int64_t rows = (M + smax - 1) / smax;
   rows = (rows + rp - 1) / rp * rp;
+  if (f32 && rows > kF32MaxChunkRows) rows = kF32MaxChunkRows;  // a multiple of every rp
   *rows_out = rows;
   *S_out = (int)((M + rows - 1) / rows);
 }
