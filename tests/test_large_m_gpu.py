@@ -4,9 +4,10 @@ network (x alone is 5.1 G fp16 elements, the fp32 stash 10.2 G), as the
 
 Row offsets inside the kernels are 64-bit; these tests run the forward, the
 training forward and the one-pass backward (fp16), the streamed-weight
-forward (hidden width 256), and the fp32 training forward and two-pass
-backward over such a batch on the GPU, and check rows on both sides of
-element 2^32 (row 2^25) against the CPU oracle.
+forward and training forward with the two-pass backward (hidden width 256),
+and the fp32 training forward and two-pass backward over such a batch on
+the GPU, and check rows on both sides of element 2^32 (row 2^25) against
+the CPU oracle.
 The weight gradient sums all 40 M rows, which the oracle cannot redo in a
 test's time, so it is checked through a size-independent identity instead:
 dW over the whole batch equals dW over its first half plus dW over its
@@ -152,4 +153,33 @@ def test_fp32_training_past_2_32_elements():
     ops.bwd(x[half:], wd, [h[half:] for h in hs], dout[half:], dwb, accumulate=False)
     _check_dw(dw, dwa, dwb, hs[-1], dout[0])
     del x, hs
+    torch.cuda.empty_cache()
+
+
+def test_wide_training_past_2_32_elements(batch):
+    # Hidden width 256, 16-bit tensors: the streamed-weight training forward
+    # (82 GB of fp32 stash) and the two-pass backward with 16-bit dz through
+    # the workspace, whose weight-gradient chunks run ~770 K rows each here.
+    x, _, _, idx, xs = batch
+    dims = (128, 256, 256, 128)
+    _, ws = orc.make_inputs(dims, 1, seed=35)
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    ti = torch.from_numpy(idx).cuda()
+    out, hs = ops.fwd(x, wd, stash=True)
+    ref, ref_h = orc.forward(xs, ws, round_hidden=True, return_hidden=True)
+    _check(out[ti].float().cpu().numpy(), ref, "sampled rows")
+    for i, h in enumerate(hs):
+        _check(h[ti].cpu().numpy(), ref_h[i], f"stash h{i + 1}")
+    del out
+    g = torch.Generator(device="cuda").manual_seed(36)
+    dout = torch.randn((1, dims[-1]), generator=g, device="cuda", dtype=torch.float16).expand(M, dims[-1])
+    dw = [torch.empty((dims[i], dims[i + 1]), device="cuda") for i in range(3)]
+    ops.bwd(x, wd, hs, dout, dw, accumulate=False)
+    half = M // 2
+    dwa = [torch.empty_like(d) for d in dw]
+    dwb = [torch.empty_like(d) for d in dw]
+    ops.bwd(x[:half], wd, [h[:half] for h in hs], dout[:half], dwa, accumulate=False)
+    ops.bwd(x[half:], wd, [h[half:] for h in hs], dout[half:], dwb, accumulate=False)
+    _check_dw(dw, dwa, dwb, hs[-1], dout[0])
+    del hs
     torch.cuda.empty_cache()
