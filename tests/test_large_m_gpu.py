@@ -183,3 +183,47 @@ def test_wide_training_past_2_32_elements(batch):
     _check_dw(dw, dwa, dwb, hs[-1], dout[0])
     del hs
     torch.cuda.empty_cache()
+
+
+def test_recompute_and_five_layers_past_2_32_elements(batch):
+    # The 3-layer backward that recomputes h2 instead of reading it (what
+    # the modules run from 2^18 rows) against the stashing one, and the
+    # 5-layer training step, whose backward hands dz between its two
+    # launches through the workspace (10 GB here).
+    x, wd, ws, idx, xs = batch
+    g = torch.Generator(device="cuda").manual_seed(37)
+    dout = torch.randn((1, DIMS[-1]), generator=g, device="cuda", dtype=torch.float16).expand(M, DIMS[-1])
+    _, hs = ops.fwd(x, wd, stash=True)
+    dw = [torch.empty((DIMS[i], DIMS[i + 1]), device="cuda") for i in range(3)]
+    ops.bwd(x, wd, hs, dout, dw, accumulate=False)
+    del hs
+    _, hr = ops.fwd(x, wd, stash=True, recompute=True)
+    assert hr[-1] is None
+    dwr = [torch.empty_like(d) for d in dw]
+    ops.bwd(x, wd, hr, dout, dwr, accumulate=False)
+    del hr
+    for i in range(3):
+        rel = ((dwr[i].double() - dw[i].double()).norm() / dw[i].double().norm()).item()
+        print(f"recompute dW{i + 1}: |recompute - stash| / |stash| = {rel:.3g}")
+        assert rel < 1e-3, (i, rel)
+
+    dims5 = (128,) * 6
+    _, ws5 = orc.make_inputs(dims5, 1, seed=38)
+    wd5 = [torch.from_numpy(w).cuda() for w in ws5]
+    out, hs = ops.fwd(x, wd5, stash=True)
+    ti = torch.from_numpy(idx).cuda()
+    ref, ref_h = orc.forward(xs, ws5, round_hidden=True, return_hidden=True)
+    _check(out[ti].float().cpu().numpy(), ref, "5 layers, sampled rows")
+    for i, h in enumerate(hs):
+        _check(h[ti].cpu().numpy(), ref_h[i], f"5 layers, stash h{i + 1}")
+    del out
+    dw5 = [torch.empty((128, 128), device="cuda") for _ in range(5)]
+    ops.bwd(x, wd5, hs, dout, dw5, accumulate=False)
+    half = M // 2
+    dwa = [torch.empty_like(d) for d in dw5]
+    dwb = [torch.empty_like(d) for d in dw5]
+    ops.bwd(x[:half], wd5, [h[:half] for h in hs], dout[:half], dwa, accumulate=False)
+    ops.bwd(x[half:], wd5, [h[half:] for h in hs], dout[half:], dwb, accumulate=False)
+    _check_dw(dw5, dwa, dwb, hs[-1], dout[0])
+    del hs
+    torch.cuda.empty_cache()
