@@ -125,7 +125,10 @@ def _train(dims, m, seed, dout_mode, with_dx, recompute=False, workspace=True):
     return [d.cpu().numpy() for d in dws], dx, rdws, rdx
 
 
-@pytest.mark.parametrize("dims", [D3, D5, NARROW, (64, 96, 96, 3)])
+# Widths up to 128 take the two-pass backward at 300 rows and the one-pass
+# megakernel above 16,384; 128-256-256-128 (streamed-weight forward) takes
+# the two-pass form at every size.
+@pytest.mark.parametrize("dims", [D3, D5, NARROW, (64, 96, 96, 3), (128, 256, 256, 128)])
 @pytest.mark.parametrize("m,dout_mode", [(300, "dense"), (20000, "ones"), (131072, "dense")])
 def test_bf16_backward_matches_oracle(dims, m, dout_mode):
     dws, dx, rdws, rdx = _train(dims, m, seed=m % 83, dout_mode=dout_mode, with_dx=True)
