@@ -92,6 +92,12 @@ const char* mlpmk_last_error(void);
  */
 int mlpmk_fwd_supported(int num_layers, const int* dims);
 
+/* mlpmk_fwd_supported for tensors of `dtype` (MLPMK_DTYPE_*): fp32 tensors
+ * take the shapes with every width at most 128 (bf16 hi/lo split operands);
+ * wider fp32 networks run layer by layer through mlpmk_softplus_f32 and
+ * library GEMMs (mlpmk.fallback).  Host only.  Since ABI version 204. */
+int mlpmk_fwd_supported_dtype(int num_layers, const int* dims, int dtype);
+
 /* 1 if a backward kernel exists for (num_layers, dims) with 16-bit tensors,
  * else 0.  Host only.  The shapes of mlpmk_fwd_supported with every width at
  * most 128, and those with widths up to 256 (input and hidden multiples of
@@ -320,6 +326,18 @@ int mlpmk_wn_bwd(int num_layers, const int* dims, int param_dtype, const float* 
  */
 int mlpmk_sigmoid_h_mul(const float* h, const void* dh, int dh_dtype, float* dz32, void* dz16, int dz16_dtype,
                         int64_t n, void* stream);
+
+/*
+ * The softplus of the reference's eager forward (/root/reference/kernel.py:168-171,
+ * torch's softplus: beta 1, threshold 20), elementwise in fp32:
+ *   h[i] = z[i] > 20 ? z[i] : log(1 + exp(z[i])),  i < n   (h may be z)
+ * evaluated as max(z, 0) + log1p(exp(-|z|)) to a few fp32 ulp.  The
+ * per-layer step of the library-GEMM forward in mlpmk.fallback, which runs
+ * fp32 tensors for networks the fused fp32 forward does not take (widths
+ * above 128), as the reference's INPUT_DTYPE = fp32 kernels take any width
+ * (mlp_fused.md:159-166).  z and h 16-byte aligned.  Since ABI version 204.
+ */
+int mlpmk_softplus_f32(const float* z, float* h, int64_t n, void* stream);
 
 /*
  * Diagnostic: a streaming copy of `bytes` bytes (multiple of 16) with the same

@@ -24,6 +24,7 @@ SIGNATURES = {
     "mlpmk_status_string": (c_char_p, [c_int]),
     "mlpmk_last_error": (c_char_p, []),
     "mlpmk_fwd_supported": (c_int, [c_int, P_INT]),
+    "mlpmk_fwd_supported_dtype": (c_int, [c_int, P_INT, c_int]),
     "mlpmk_bwd_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_recompute_supported": (c_int, [c_int, P_INT]),
     "mlpmk_bwd_supported_dtype": (c_int, [c_int, P_INT, c_int]),
@@ -50,6 +51,7 @@ SIGNATURES = {
     ),
     "mlpmk_copy": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "mlpmk_sigmoid_h_mul": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64, c_void_p]),
+    "mlpmk_softplus_f32": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
 }
 
 STATUS = {

@@ -21,7 +21,10 @@ Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
   Outside autocast the tensors keep their own type, as the reference's
   INPUT_DTYPE kernels do (mlp_fused.md:159-166): fp32 parameters and an fp32
   ``x`` run the fp32-tensor kernels (bf16 hi/lo split operands: fp32's
-  exponent range) and return an fp32 ``out``.
+  exponent range) and return an fp32 ``out``; fp32 networks wider than 128,
+  which those kernels do not take, run layer by layer (``fallback.fwd``:
+  fp32 library GEMMs, the library's fp32 softplus kernel) and train through
+  the fallback backward in fp32.
 * inference: ``fused_mlp`` / ``fused_mlp_wn`` (and the modules) call the plain
   forward, without the fp32 stash, whenever autograd will not need it -- grad
   disabled (``torch.no_grad`` / ``inference_mode``) or nothing requiring grad.
@@ -29,7 +32,10 @@ Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
   ``ctx.needs_input_grad`` reflects ``requires_grad`` only, so that choice is
   made before ``apply``.
 
-Every launch goes through ``libmlpmk.so``; there is no PyTorch fallback.
+Every kernel of the fused paths is ``libmlpmk.so``'s and there is no CPU
+path; the layer-by-layer fp32 forward and the fallback backward issue their
+GEMMs as library GEMMs (rocBLAS / hipBLASLt through torch) around the
+library's elementwise kernels.
 """
 from __future__ import annotations
 
@@ -107,18 +113,33 @@ def _use_recompute(dims, m, need_dx, dtype=torch.float16):
 
 
 def kernel_dtype(x, dims=None):
-    """Element type the megakernels run in for input ``x``: the autocast dtype
+    """Element type the network runs in for input ``x``: the autocast dtype
     when autocast is on (fp16 unless it is bf16); else ``x``'s own type --
-    bf16, fp16, or fp32 where the fp32-tensor kernels take the network
-    (every width at most 128; wider networks run fp32 ``x`` in fp16) -- and
-    fp16 for anything else."""
+    bf16, fp16 or fp32 (the fp32-tensor kernels for widths up to 128, the
+    layer-by-layer fp32 path of ``mlpmk.fallback`` above) -- and fp16 for
+    anything else.  ``dims`` is accepted for the callers' convenience."""
+    del dims
     if torch.is_autocast_enabled("cuda"):
         return torch.bfloat16 if torch.get_autocast_dtype("cuda") == torch.bfloat16 else torch.float16
-    if x.dtype == torch.bfloat16:
-        return torch.bfloat16
-    if x.dtype == torch.float32 and (dims is None or max(dims) <= 128):
-        return torch.float32
+    if x.dtype in (torch.bfloat16, torch.float32):
+        return x.dtype
     return torch.float16
+
+
+_fwd_shapes = {}
+
+
+def _layerwise(dims, dtype):
+    """True when no fused forward takes ``dims`` for ``dtype`` tensors: fp32
+    networks wider than 128 run layer by layer (``fallback.fwd``: fp32
+    library GEMMs and the library's fp32 softplus kernel)."""
+    if dtype != torch.float32:
+        return False
+    key = tuple(dims)
+    ok = _fwd_shapes.get(key)
+    if ok is None:
+        ok = _fwd_shapes[key] = ops.fwd_supported(list(key), torch.float32)
+    return not ok
 
 
 def _needs_graph(*tensors):
@@ -157,10 +178,19 @@ class FusedMLPFunction(torch.autograd.Function):
         weights = [w.to(dt).contiguous() for w in weights]
         if any(ctx.needs_input_grad):
             rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0], dt)
-            out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
+            if _layerwise(dims, dt):
+                from . import fallback
+
+                out, hs = fallback.fwd(x, weights, stash=True)
+            else:
+                out, hs = ops.fwd(x, weights, stash=True, recompute=rc)
             ctx.save_for_backward(x, *weights, *[h for h in hs if h is not None])
             ctx.dims = dims
             ctx.recompute = rc
+        elif _layerwise(dims, dt):
+            from . import fallback
+
+            out = fallback.fwd(x, weights)
         else:
             out = ops.fwd(x, weights)
         return out
@@ -230,6 +260,16 @@ class FusedMLPWNFunction(torch.autograd.Function):
         wb, es = w_all.data_ptr(), w_all.element_size()
         w_ptrs = [wb + es * o for o in woff]
         M = int(x.shape[0])
+        if _layerwise(dims, x.dtype):
+            from . import fallback
+
+            if any(ctx.needs_input_grad):
+                out, hs = fallback.fwd(x, _split(w_all, dims), stash=True)
+                ctx.save_for_backward(x, v_all, g_all, w_all, inv_all, *hs)
+                ctx.dims = dims
+                ctx.recompute = False
+                return out
+            return fallback.fwd(x, _split(w_all, dims))
         out = torch.empty((M, dims[-1]), dtype=x.dtype, device=dev)
         if any(ctx.needs_input_grad):
             rc = _use_recompute(dims, M, ctx.needs_input_grad[0], x.dtype)
@@ -310,8 +350,15 @@ def fused_mlp(x, *weights):
     launch."""
     if _needs_graph(x, *weights):
         return FusedMLPFunction.apply(x, *weights)
-    dt = kernel_dtype(x, (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights))
-    return ops.fwd(x.to(dt).contiguous(), [w.to(dt).contiguous() for w in weights])
+    dims = (int(x.shape[1]),) + tuple(int(w.shape[1]) for w in weights)
+    dt = kernel_dtype(x, dims)
+    x = x.to(dt).contiguous()
+    weights = [w.to(dt).contiguous() for w in weights]
+    if _layerwise(dims, dt):
+        from . import fallback
+
+        return fallback.fwd(x, weights)
+    return ops.fwd(x, weights)
 
 
 def fused_mlp_wn(x, v_all, g_all, dims):
@@ -324,4 +371,8 @@ def fused_mlp_wn(x, v_all, g_all, dims):
     w_all = torch.empty(sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1)), dtype=x.dtype, device=x.device)
     inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=x.device)
     ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
+    if _layerwise(dims, x.dtype):
+        from . import fallback
+
+        return fallback.fwd(x, _split(w_all, dims))
     return ops.fwd(x, _split(w_all, dims))

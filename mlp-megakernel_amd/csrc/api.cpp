@@ -13,6 +13,7 @@
 namespace mlpmk {
 
 bool fwd_supported_dims(int L, const int* dims);
+bool fwd_supported_dtype(int L, const int* dims, int dtype);
 int fwd_dispatch(int L, const int* dims, const FwdParams& p, bool stash, int dtype, hipStream_t st, LaunchInfo* info);
 bool bwd_supported_dims(int L, const int* dims);
 bool bwd_supported_dtype(int L, const int* dims, int dtype);
@@ -26,6 +27,7 @@ int wn_fwd_dispatch(int L, const int* dims, int dtype, int w_dtype, const void* 
 int wn_bwd_dispatch(int L, const int* dims, int dtype, const float* dw, const void* v, const void* g,
                     const float* inv_norm, void* dv, void* dg, hipStream_t st);
 int copy_dispatch(const void* src, void* dst, int64_t bytes, hipStream_t st);
+int softplus_f32_dispatch(const float* z, float* h, int64_t n, hipStream_t st);
 int sigmoid_h_mul_dispatch(const float* h, const void* dh, int dh_dtype, float* dz32, void* dz16, int dz16_dtype,
                            int64_t n, hipStream_t st);
 
@@ -114,7 +116,7 @@ using namespace mlpmk;
 
 extern "C" {
 
-int mlpmk_version(void) { return 203; }  // 2.03: MLPMK_BWD_WRITE_DW (2.02: fp32 backward, mlpmk_bwd_supported_dtype)
+int mlpmk_version(void) { return 204; }  // 2.04: mlpmk_softplus_f32, mlpmk_fwd_supported_dtype (2.03: MLPMK_BWD_WRITE_DW)
 
 const char* mlpmk_status_string(int status) {
   switch (status) {
@@ -133,6 +135,12 @@ const char* mlpmk_last_error(void) { return g_last_error; }
 int mlpmk_fwd_supported(int num_layers, const int* dims) {
   if (!dims || num_layers < 2 || num_layers > kMaxLayersHost) return 0;
   return fwd_supported_dims(num_layers, dims) ? 1 : 0;
+}
+
+int mlpmk_fwd_supported_dtype(int num_layers, const int* dims, int dtype) {
+  if (!dims || num_layers < 2 || num_layers > kMaxLayersHost) return 0;
+  if (dtype != MLPMK_DTYPE_F16 && dtype != MLPMK_DTYPE_BF16 && dtype != MLPMK_DTYPE_F32) return 0;
+  return fwd_supported_dtype(num_layers, dims, dtype) ? 1 : 0;
 }
 
 int mlpmk_bwd_supported(int num_layers, const int* dims) {
@@ -381,6 +389,15 @@ int mlpmk_sigmoid_h_mul(const float* h, const void* dh, int dh_dtype, float* dz3
   if ((rc = check_ptr(h, "h")) || (rc = check_ptr(dh, "dh")) || (rc = check_ptr(dz32, "dz32"))) return rc;
   if (dz16 && (rc = check_ptr(dz16, "dz16"))) return rc;
   return sigmoid_h_mul_dispatch(h, dh, dh_dtype, dz32, dz16, dz16_dtype, n, static_cast<hipStream_t>(stream));
+}
+
+int mlpmk_softplus_f32(const float* z, float* h, int64_t n, void* stream) {
+  g_last_error[0] = 0;
+  if (n < 0) return fail(MLPMK_ERR_INVALID_ARG, "n=%lld is negative", (long long)n);
+  if (n == 0) return MLPMK_OK;
+  int rc;
+  if ((rc = check_ptr(z, "z")) || (rc = check_ptr(h, "h"))) return rc;
+  return softplus_f32_dispatch(z, h, n, static_cast<hipStream_t>(stream));
 }
 
 int mlpmk_copy(const void* src, void* dst, int64_t bytes, void* stream) {

@@ -32,6 +32,13 @@ bool fwd_supported_dims(int L, const int* dims) {
          dims_match<NetNarrow>(L, dims) || fwd_generic_dims(L, dims) || fwd_wide_dims(L, dims);
 }
 
+// The same for tensors of one element type: fp32 tensors run the split-operand
+// kernels of fwd_x3.hip, whose widths are at most 128 (fwd_dispatch_f32).
+bool fwd_supported_dtype(int L, const int* dims, int dtype) {
+  if (dtype == MLPMK_DTYPE_F32) return dims_match<Net3L128>(L, dims) || fwd_generic_dims(L, dims);
+  return fwd_supported_dims(L, dims);
+}
+
 int fwd_split_dispatch(int L, const int* dims, const FwdParams& p, bool stash, bool bf, hipStream_t st, int cus,
                        LaunchInfo* info);
 

@@ -23,6 +23,11 @@ MI355X -- it needs no atomics in its workspace form and was measured 4.6-21x
 faster at M = 4K..1M -- so autograd uses it unless ``autograd.BACKWARD`` is
 set to ``"fallback"``; this path is kept as the reference's alternative and as
 a comparator.  Same arguments and results as ``ops.bwd``.
+
+For fp32 tensors at widths the fused fp32 kernels do not take (above 128),
+:func:`fwd` is the matching forward (fp32 library GEMMs and this library's
+fp32 softplus kernel, ``mlpmk_softplus_f32``), and :func:`bwd` runs every
+GEMM in fp32.
 """
 from __future__ import annotations
 
@@ -49,6 +54,42 @@ def sigmoid_h_mul(h, dh, dz16_dtype=None):
                  dz16.data_ptr() if dz16 is not None else None, dz16_code, h.numel())
     _check("mlpmk_sigmoid_h_mul", rc)
     return (dz32, dz16) if dz16_dtype is not None else dz32
+
+
+def softplus_f32(z, out=None):
+    """``h = softplus(z)`` elementwise in fp32 (``mlpmk_softplus_f32``: torch's
+    softplus with beta 1 and threshold 20, kernel.py:168-171).  ``z`` fp32,
+    contiguous, on a GPU; ``out`` may be ``z`` itself (default: a new tensor)."""
+    if z.dtype != torch.float32 or not z.is_contiguous() or z.device.type != "cuda":
+        raise ValueError("z must be a contiguous fp32 tensor on a GPU")
+    h = torch.empty_like(z) if out is None else out
+    if h.shape != z.shape or h.dtype != torch.float32 or not h.is_contiguous() or h.device != z.device:
+        raise ValueError("out must be a contiguous fp32 tensor shaped like z on its GPU")
+    rc = _launch(z.device, _lib.get().mlpmk_softplus_f32, z.data_ptr(), h.data_ptr(), z.numel())
+    _check("mlpmk_softplus_f32", rc)
+    return h
+
+
+def fwd(x, weights, stash=False):
+    """Forward of fp32 tensors layer by layer, for the networks the fused
+    fp32 forward does not take (widths above 128): ``z = a @ W_l`` as an fp32
+    library GEMM (rocBLAS / hipBLASLt through torch), then the fp32 softplus
+    kernel in place on every hidden layer.  The reference's INPUT_DTYPE = fp32
+    kernels take any width (mlp_fused.md:159-166); this keeps fp32's range
+    and precision for them.  Returns ``out`` or ``(out, [h1 .. h_{L-1}])``
+    (the fp32 stash that :func:`bwd` reads)."""
+    if x.dtype != torch.float32 or any(w.dtype != torch.float32 for w in weights):
+        raise ValueError("the layer-by-layer forward takes fp32 x and weights")
+    a = x.contiguous()
+    hs = []
+    for i, w in enumerate(weights):
+        z = a @ w.contiguous()
+        if i + 1 < len(weights):
+            a = softplus_f32(z, out=z)
+            hs.append(a)
+        else:
+            a = z
+    return (a, hs) if stash else a
 
 
 def bwd(x, weights, hs, dout, dws, dx=None):

@@ -43,10 +43,14 @@ def _dims_of(x, weights):
     return dims
 
 
-def fwd_supported(dims):
+def fwd_supported(dims, dtype=None):
+    """True if a fused forward kernel takes ``dims`` (for tensors of
+    ``dtype``; default: any element type, ``mlpmk_fwd_supported``)."""
     lib = _lib.get()
     p, _keep = _lib.int_array(dims)
-    return bool(lib.mlpmk_fwd_supported(len(dims) - 1, p))
+    if dtype is None:
+        return bool(lib.mlpmk_fwd_supported(len(dims) - 1, p))
+    return bool(lib.mlpmk_fwd_supported_dtype(len(dims) - 1, p, _fwd_code(dtype)))
 
 
 def bwd_supported(dims, dtype=None):

@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     lib = _lib.get()
-    assert lib.mlpmk_version() >= 203  # MLPMK_DOUT_SCALAR (201), MLPMK_BWD_WRITE_DW (203)
+    assert lib.mlpmk_version() >= 204  # MLPMK_DOUT_SCALAR (201), MLPMK_BWD_WRITE_DW (203), mlpmk_softplus_f32 (204)
     for code, text in [(0, b"ok"), (2, b"unsupported shape"), (5, b"no usable gfx950 device")]:
         assert lib.mlpmk_status_string(code) == text
     assert lib.mlpmk_status_string(99) == b"unknown status"

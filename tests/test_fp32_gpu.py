@@ -264,11 +264,11 @@ def _torch64(x, ws, wn_v=None, wn_g=None, dims=None):
     return a.detach().numpy(), xd.grad.numpy(), [p.grad.numpy() for p in params]
 
 
-def _module_step(m, wn, big_rows):
+def _module_step(m, wn, big_rows, H=128, n_layers=3):
     import fused_mlp
 
     torch.manual_seed(11)
-    model = (fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus)().cuda()
+    model = (fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus)(H=H, n_layers=n_layers).cuda()
     x = torch.randn(m, 128, device="cuda")
     if big_rows:
         x[::5] *= 1e5  # rows past fp16's 65,504
@@ -317,3 +317,74 @@ def test_fp32_modules_with_rows_past_fp16_range(wn):
         g = gr.cpu().numpy().reshape(rg.shape).astype(np.float64)
         frob = np.linalg.norm(g - rg) / np.linalg.norm(rg)
         assert frob < 5e-3, f"module grad {i} wn={wn}: rel frob {frob:.3g}"
+
+
+# ---------------------------------------------------------------------------
+# fp32 networks wider than 128: no fused fp32 kernel takes them, so they run
+# layer by layer (mlpmk.fallback.fwd: fp32 library GEMMs and the library's
+# fp32 softplus kernel, mlpmk_softplus_f32) and train through the fallback
+# backward with every GEMM in fp32 -- fp32 in, fp32 out, fp32's range, as the
+# reference's INPUT_DTYPE = fp32 kernels take any width (mlp_fused.md:159-166).
+# ---------------------------------------------------------------------------
+
+def test_softplus_f32_kernel_matches_torch_softplus():
+    import torch.nn.functional as F
+    from mlpmk import fallback
+
+    edge = [-np.inf, -1000.0, -104.0, -88.0, -50.0, -20.0, -17.0, -10.0, -1e-3, -0.0, 0.0, 1e-3, 1.0, 10.0,
+            19.99, 20.0, 20.01, 88.0, 1000.0, np.inf, np.nan]
+    rng = np.random.default_rng(5)
+    z = np.concatenate([np.array(edge, np.float32), (rng.standard_normal(10001) * 30).astype(np.float32)])
+    zd = torch.from_numpy(z).cuda()
+    got = fallback.softplus_f32(zd).cpu().numpy().astype(np.float64)
+    ref = F.softplus(torch.from_numpy(z).double()).numpy()  # beta 1, threshold 20, as kernel.py:168-171
+    assert np.isnan(got[20]) and got[0] == 0.0 and got[19] == np.inf
+    fin = np.isfinite(ref)
+    np.testing.assert_allclose(got[fin], ref[fin], rtol=1e-6, atol=1e-37)
+    assert np.all(got[fin] >= 0.0)
+    # in place, and a length that leaves a tail past the 4-element steps
+    zin = zd[:10003].clone()
+    fallback.softplus_f32(zin, out=zin)
+    np.testing.assert_array_equal(zin.cpu().numpy(), got[:10003].astype(np.float32))
+
+
+@pytest.mark.parametrize("wn", [False, True])
+@pytest.mark.parametrize("H,n_layers,m", [(256, 3, 4096), (192, 5, 2000)])
+def test_fp32_modules_wider_than_128_train_in_fp32(wn, H, n_layers, m):
+    from mlpmk import ops as _o
+
+    dims = [128] + [H] * (n_layers - 1) + [128]
+    assert not _o.fwd_supported(dims, torch.float32) and _o.fwd_supported(dims, torch.float16)
+    out, gx, grads, ref_out, ref_dx, ref_g = _module_step(m, wn, big_rows=False, H=H, n_layers=n_layers)
+    _check_rows(out.detach().cpu().numpy(), ref_out, f"module out H={H} wn={wn}", tol=1e-5)
+    _check_rows(gx.cpu().numpy(), ref_dx, f"module dx H={H} wn={wn}", tol=1e-5)
+    for i, (gr, rg) in enumerate(zip(grads, ref_g)):
+        g = gr.cpu().numpy().reshape(rg.shape).astype(np.float64)
+        frob = np.linalg.norm(g - rg) / np.linalg.norm(rg)
+        assert frob < 1e-4, f"module grad {i} H={H} wn={wn}: rel frob {frob:.3g}"
+
+
+def test_fp32_module_wider_than_128_keeps_rows_past_fp16_range():
+    # Rows scaled by 1e5 stay finite in fp32 (in fp16 they would overflow).
+    out, gx, grads, ref_out, ref_dx, ref_g = _module_step(4096, False, big_rows=True, H=256)
+    assert float(out.detach().abs().max()) > 65504.0
+    _check_rows(out.detach().cpu().numpy(), ref_out, "module out, rows past fp16 range", tol=1e-5)
+    assert np.all(np.isfinite(gx.cpu().numpy()))
+    for i, (gr, rg) in enumerate(zip(grads, ref_g)):
+        g = gr.cpu().numpy().reshape(rg.shape).astype(np.float64)
+        frob = np.linalg.norm(g - rg) / np.linalg.norm(rg)
+        assert frob < 1e-4, f"module grad {i}: rel frob {frob:.3g}"
+
+
+def test_fp32_launcher_wider_than_128_matches_model():
+    rng = np.random.default_rng(9)
+    dims = (128, 256, 256, 128)
+    x = torch.from_numpy(rng.standard_normal((3000, 128)).astype(np.float32)).cuda()
+    ws = [torch.from_numpy((rng.standard_normal((dims[i], dims[i + 1])) / np.sqrt(dims[i])).astype(np.float32)).cuda()
+          for i in range(3)]
+    out = kernel._fused_mlp_fwd(x, *ws)
+    assert out.dtype == torch.float32
+    ref = orc.forward(x.cpu().numpy(), [w.cpu().numpy() for w in ws], dtype=np.float64)
+    _check_rows(out.cpu().numpy(), ref, "launcher fp32 H=256", tol=1e-5)
+    eager = kernel.Model()(x, *ws)
+    _check_rows(out.cpu().numpy(), eager.double().cpu().numpy(), "launcher fp32 H=256 vs eager Model", tol=1e-5)
