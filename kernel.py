@@ -93,7 +93,9 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
     (``mlpmk_fwd_launch_info``); otherwise from the mirror above with
     ``num_cus`` CUs (MI355X's 256 by default).  ``fp32`` inputs (fp32 x, W
     and out; bf16 hi/lo split MFMA operands) always take their feature-split
-    kernel: 32-row blocks, 4 waves.
+    kernel: 32-row blocks, 4 waves.  fp32 networks wider than 128 have no
+    fused kernel (``_fused_mlp_fwd`` runs them layer by layer): the library
+    query raises ``MlpmkError`` for them.
     """
     dims = (K1, N1, N2, N3)
     if num_cus is None and torch.cuda.is_available():
