@@ -44,11 +44,12 @@ class FusedMLPSoftplus(nn.Module):
         )
 
     def forward(self, x):
-        # The kernels run in mlpmk.autograd.kernel_dtype(x): the autocast
-        # dtype under autocast, else x's own type -- bf16, fp16, or fp32
-        # (bf16 hi/lo split operands) for networks of widths up to 128 --
-        # and fp16 for anything else; autograd carries the gradient back
-        # through the casts.  Without autograd (no_grad, inference_mode, or
+        # The network runs in mlpmk.autograd.kernel_dtype(x): the autocast
+        # dtype under autocast, else x's own type (bf16, fp16 or fp32; fp32
+        # through bf16 hi/lo split operands) and fp16 for anything else;
+        # networks no fused kernel takes (fp32 wider than 128, any wider
+        # than 256) run layer by layer in that type; autograd carries the
+        # gradient back through the casts.  Without autograd (no_grad, inference_mode, or
         # nothing requiring grad) this is one plain forward launch, no stash.
         return fused_mlp(x, *self.weights)
 

@@ -107,15 +107,15 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
 
 def _fused_mlp_fwd(x, w1, w2, w3):
     """Inference forward: one kernel launch, no intermediate in global memory
-    (fp32 tensors wider than 128, which no fused fp32 kernel takes, run layer
-    by layer: mlpmk.fallback.fwd)."""
+    (networks no fused kernel takes -- fp32 ones wider than 128, any wider
+    than 256 -- run layer by layer: mlpmk.fallback.fwd)."""
     x = x.contiguous()
     w1, w2, w3 = w1.contiguous(), w2.contiguous(), w3.contiguous()
     M = x.shape[0]
     N3 = w3.shape[1]
-    if x.dtype == torch.float32:
+    if x.dtype in (torch.float32, torch.float16, torch.bfloat16):
         dims = [x.shape[1], w1.shape[1], w2.shape[1], N3]
-        if not _ops.fwd_supported(dims, torch.float32):
+        if not _ops.fwd_supported(dims, x.dtype):
             from mlpmk import fallback
 
             return fallback.fwd(x, [w1, w2, w3])

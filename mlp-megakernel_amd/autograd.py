@@ -21,10 +21,11 @@ Training path of the reference's ``FusedMLPSoftplus`` / ``FusedMLPSoftplusWN``
   Outside autocast the tensors keep their own type, as the reference's
   INPUT_DTYPE kernels do (mlp_fused.md:159-166): fp32 parameters and an fp32
   ``x`` run the fp32-tensor kernels (bf16 hi/lo split operands: fp32's
-  exponent range) and return an fp32 ``out``; fp32 networks wider than 128,
-  which those kernels do not take, run layer by layer (``fallback.fwd``:
-  fp32 library GEMMs, the library's fp32 softplus kernel) and train through
-  the fallback backward in fp32.
+  exponent range) and return an fp32 ``out``.  Networks no fused forward
+  takes (fp32 ones wider than 128, any wider than 256) run layer by layer
+  (``fallback.fwd``: fp32 library GEMMs, the library's fp32 softplus kernel,
+  hidden values rounded to the tensor format between layers) and train
+  through the fallback backward.
 * inference: ``fused_mlp`` / ``fused_mlp_wn`` (and the modules) call the plain
   forward, without the fp32 stash, whenever autograd will not need it -- grad
   disabled (``torch.no_grad`` / ``inference_mode``) or nothing requiring grad.
@@ -130,15 +131,14 @@ _fwd_shapes = {}
 
 
 def _layerwise(dims, dtype):
-    """True when no fused forward takes ``dims`` for ``dtype`` tensors: fp32
-    networks wider than 128 run layer by layer (``fallback.fwd``: fp32
+    """True when no fused forward takes ``dims`` for ``dtype`` tensors (fp32
+    networks wider than 128, any network wider than 256 or deeper than the
+    kernels' 5 layers): they run layer by layer (``fallback.fwd``: fp32
     library GEMMs and the library's fp32 softplus kernel)."""
-    if dtype != torch.float32:
-        return False
-    key = tuple(dims)
+    key = (tuple(dims), dtype)
     ok = _fwd_shapes.get(key)
     if ok is None:
-        ok = _fwd_shapes[key] = ops.fwd_supported(list(key), torch.float32)
+        ok = _fwd_shapes[key] = ops.fwd_supported(list(key[0]), dtype)
     return not ok
 
 

@@ -24,10 +24,10 @@ faster at M = 4K..1M -- so autograd uses it unless ``autograd.BACKWARD`` is
 set to ``"fallback"``; this path is kept as the reference's alternative and as
 a comparator.  Same arguments and results as ``ops.bwd``.
 
-For fp32 tensors at widths the fused fp32 kernels do not take (above 128),
-:func:`fwd` is the matching forward (fp32 library GEMMs and this library's
-fp32 softplus kernel, ``mlpmk_softplus_f32``), and :func:`bwd` runs every
-GEMM in fp32.
+For networks no fused forward takes (fp32 tensors wider than 128, any
+tensors wider than 256), :func:`fwd` is the matching forward: fp32 library
+GEMMs and this library's fp32 softplus kernel (``mlpmk_softplus_f32``);
+:func:`bwd` then runs the backward (every GEMM in fp32 for fp32 tensors).
 """
 from __future__ import annotations
 
@@ -71,24 +71,29 @@ def softplus_f32(z, out=None):
 
 
 def fwd(x, weights, stash=False):
-    """Forward of fp32 tensors layer by layer, for the networks the fused
-    fp32 forward does not take (widths above 128): ``z = a @ W_l`` as an fp32
-    library GEMM (rocBLAS / hipBLASLt through torch), then the fp32 softplus
-    kernel in place on every hidden layer.  The reference's INPUT_DTYPE = fp32
-    kernels take any width (mlp_fused.md:159-166); this keeps fp32's range
-    and precision for them.  Returns ``out`` or ``(out, [h1 .. h_{L-1}])``
-    (the fp32 stash that :func:`bwd` reads)."""
-    if x.dtype != torch.float32 or any(w.dtype != torch.float32 for w in weights):
-        raise ValueError("the layer-by-layer forward takes fp32 x and weights")
-    a = x.contiguous()
+    """Forward layer by layer, for the networks no fused forward takes: fp32
+    tensors wider than 128, and any tensors wider than 256.  ``z = a @ W_l``
+    as an fp32 library GEMM (rocBLAS / hipBLASLt through torch; 16-bit
+    values are exact in fp32, so this is the fused kernels' fp32
+    accumulation), then the fp32 softplus kernel on every hidden layer, whose
+    output is rounded to the tensor format before the next GEMM as the
+    reference's kernel rounds its h (kernel.py:110,117).  The reference's
+    kernels take any width (kernel.py:60-63; INPUT_DTYPE = fp32,
+    mlp_fused.md:159-166).  Returns ``out`` in x's dtype, or ``(out, [h1 ..
+    h_{L-1}])`` with the fp32 stash that :func:`bwd` reads."""
+    dt = x.dtype
+    if dt not in (torch.float32, torch.float16, torch.bfloat16) or any(w.dtype != dt for w in weights):
+        raise ValueError("x and the weights must share one of fp32, fp16 or bf16")
+    a = x.contiguous() if dt == torch.float32 else x.float()
     hs = []
     for i, w in enumerate(weights):
-        z = a @ w.contiguous()
+        z = a @ (w.contiguous() if dt == torch.float32 else w.float())
         if i + 1 < len(weights):
-            a = softplus_f32(z, out=z)
-            hs.append(a)
+            h = softplus_f32(z, out=z)
+            hs.append(h)
+            a = h if dt == torch.float32 else h.to(dt).float()
         else:
-            a = z
+            a = z if dt == torch.float32 else z.to(dt)
     return (a, hs) if stash else a
 
 

@@ -349,12 +349,12 @@ def test_softplus_f32_kernel_matches_torch_softplus():
 
 
 @pytest.mark.parametrize("wn", [False, True])
-@pytest.mark.parametrize("H,n_layers,m", [(256, 3, 4096), (192, 5, 2000)])
+@pytest.mark.parametrize("H,n_layers,m", [(256, 3, 4096), (192, 5, 2000), (320, 3, 1500)])
 def test_fp32_modules_wider_than_128_train_in_fp32(wn, H, n_layers, m):
     from mlpmk import ops as _o
 
     dims = [128] + [H] * (n_layers - 1) + [128]
-    assert not _o.fwd_supported(dims, torch.float32) and _o.fwd_supported(dims, torch.float16)
+    assert not _o.fwd_supported(dims, torch.float32) and _o.fwd_supported(dims, torch.float16) == (H <= 256)
     out, gx, grads, ref_out, ref_dx, ref_g = _module_step(m, wn, big_rows=False, H=H, n_layers=n_layers)
     _check_rows(out.detach().cpu().numpy(), ref_out, f"module out H={H} wn={wn}", tol=1e-5)
     _check_rows(gx.cpu().numpy(), ref_dx, f"module dx H={H} wn={wn}", tol=1e-5)

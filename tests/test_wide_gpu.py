@@ -172,6 +172,17 @@ def test_wide_scaled_inputs_overflow_in_every_round(m):
     assert big_err <= 2e-3 * np.abs(ref[~small]).max(), (big_err, np.abs(ref[~small]).max())
 
 
+def test_launcher_wider_than_256_runs_layer_by_layer():
+    dims, m = (128, 320, 320, 128), 1000
+    x, ws = orc.make_inputs(dims, m, seed=23)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    assert not ops.fwd_supported(list(dims))
+    out = kernel._fused_mlp_fwd(xd, *wd)
+    assert out.dtype == torch.float16 and tuple(out.shape) == (m, 128)
+    _check(out.float().cpu().numpy(), orc.forward(x, ws, round_hidden=True), "layer by layer, H = 320")
+
+
 def test_wide_launcher_matches_model():
     dims, m = (128, 256, 256, 64), 4096
     x, ws = orc.make_inputs(dims, m, seed=19)
@@ -204,14 +215,19 @@ def _check_grad(got, ref, what):
     assert worst <= 0 and frob < 1e-2, f"{what}: worst excess {worst:.3g}, rel frob {frob:.3g}"
 
 
-@pytest.mark.parametrize("H,n_layers,out_f", [(256, 3, 128), (192, 5, 128), (256, 3, 100)])
+@pytest.mark.parametrize("H,n_layers,out_f", [(256, 3, 128), (192, 5, 128), (256, 3, 100), (320, 3, 128), (512, 2, 64)])
 def test_module_with_wide_hidden_trains(H, n_layers, out_f):
-    # (out_features 100, not a multiple of 8: the library-GEMM fallback backward)
+    # (out_features 100, not a multiple of 8: the library-GEMM fallback
+    # backward; H = 320 and 512: no fused forward takes widths above 256,
+    # so these run layer by layer -- fp32 library GEMMs, the library's fp32
+    # softplus kernel, h rounded to fp16 between layers -- and train through
+    # the fallback backward)
     from mlpmk import autograd as mag
 
     torch.manual_seed(3)
     model = fused_mlp.FusedMLPSoftplus(D=128, H=H, out_features=out_f, n_layers=n_layers).cuda().half()
-    assert mag._fused_bwd_supported(tuple(model.dims)) == (out_f % 8 == 0)
+    assert mag._fused_bwd_supported(tuple(model.dims)) == (out_f % 8 == 0 and H <= 256)
+    assert mag._layerwise(tuple(model.dims), torch.float16) == (H > 256)
     x = torch.randn(4096, 128, device="cuda").half().requires_grad_(True)
     out = model(x)
     out.sum().backward()
