@@ -86,14 +86,15 @@ def fwd(x, weights, stash=False):
         raise ValueError("x and the weights must share one of fp32, fp16 or bf16")
     a = x.contiguous() if dt == torch.float32 else x.float()
     hs = []
-    for i, w in enumerate(weights):
-        z = a @ (w.contiguous() if dt == torch.float32 else w.float())
-        if i + 1 < len(weights):
-            h = softplus_f32(z, out=z)
-            hs.append(h)
-            a = h if dt == torch.float32 else h.to(dt).float()
-        else:
-            a = z if dt == torch.float32 else z.to(dt)
+    with torch.autocast("cuda", enabled=False):  # the GEMMs stay fp32 under a caller's autocast
+        for i, w in enumerate(weights):
+            z = a @ (w.contiguous() if dt == torch.float32 else w.float())
+            if i + 1 < len(weights):
+                h = softplus_f32(z, out=z)
+                hs.append(h)
+                a = h if dt == torch.float32 else h.to(dt).float()
+            else:
+                a = z if dt == torch.float32 else z.to(dt)
     return (a, hs) if stash else a
 
 
@@ -106,6 +107,12 @@ def bwd(x, weights, hs, dout, dws, dx=None):
     L = len(weights)
     if len(hs) != L - 1 or any(h is None for h in hs):
         raise ValueError("the fallback backward reads every hidden activation from the stash (no recompute)")
+    with torch.autocast("cuda", enabled=False):  # GEMMs in the types below, whatever the caller's autocast
+        return _bwd(x, weights, hs, dout, dws, dx)
+
+
+def _bwd(x, weights, hs, dout, dws, dx):
+    L = len(weights)
     dt = x.dtype
     dz16 = dout.to(dt).contiguous() if dout.stride(0) != 0 else dout[:1].to(dt).expand_as(dout).contiguous()
     dz32 = dz16.float()

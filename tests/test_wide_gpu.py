@@ -238,6 +238,37 @@ def test_module_with_wide_hidden_trains(H, n_layers, out_f):
     _check(x.grad.float().cpu().numpy(), ref_dx, "dx")
 
 
+@pytest.mark.parametrize("wn", [False, True])
+def test_modules_deeper_than_five_layers_train(wn):
+    # 7 layers: the fused kernels take 2..5, so the forward runs layer by
+    # layer and the backward is the fallback (weight norm: the library's
+    # single-launch kernels, which take up to 8 layers).
+    from mlpmk import autograd as mag
+
+    torch.manual_seed(6)
+    cls = fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus
+    model = cls(D=64, H=96, out_features=32, n_layers=7).cuda()
+    assert mag._layerwise(tuple(model.dims), torch.float16)
+    x = torch.randn(1500, 64, device="cuda").half().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.float16):
+        out = model(x)
+    assert out.dtype == torch.float16
+    out.float().sum().backward()
+    if wn:
+        ws = [model.v(i).detach() * (model.g(i).detach() / model.v(i).detach().norm(dim=0)) for i in range(7)]
+        ws16 = [w.half() for w in ws]
+    else:
+        ws16 = [w.detach().half() for w in model.weights]
+    ref_out, ref_dx, ref_dws = _torch_ref(x, ws16)
+    _check(out.detach().float().cpu().numpy(), ref_out, "out")
+    _check(x.grad.float().cpu().numpy(), ref_dx, "dx")
+    if not wn:
+        for i, w in enumerate(model.weights):
+            _check_grad(w.grad.float().cpu().numpy(), ref_dws[i], f"dW{i + 1}")
+    else:
+        assert torch.isfinite(model.v_all.grad).all() and torch.isfinite(model.g_all.grad).all()
+
+
 def test_weight_norm_module_with_wide_hidden_trains():
     torch.manual_seed(4)
     model = fused_mlp.FusedMLPSoftplusWN(D=128, H=256, out_features=128).cuda()
