@@ -117,13 +117,17 @@ def kernel_dtype(x, dims=None):
     """Element type the network runs in for input ``x``: the autocast dtype
     when autocast is on (fp16 unless it is bf16); else ``x``'s own type --
     bf16, fp16 or fp32 (the fp32-tensor kernels for widths up to 128, the
-    layer-by-layer fp32 path of ``mlpmk.fallback`` above) -- and fp16 for
-    anything else.  ``dims`` is accepted for the callers' convenience."""
+    layer-by-layer fp32 path of ``mlpmk.fallback`` above) --, fp32 for
+    float64 (the widest type the library computes in: the range stays), and
+    fp16 for anything else.  ``dims`` is accepted for the callers'
+    convenience."""
     del dims
     if torch.is_autocast_enabled("cuda"):
         return torch.bfloat16 if torch.get_autocast_dtype("cuda") == torch.bfloat16 else torch.float16
     if x.dtype in (torch.bfloat16, torch.float32):
         return x.dtype
+    if x.dtype == torch.float64:
+        return torch.float32
     return torch.float16
 
 

@@ -103,3 +103,15 @@ def test_product_path_refuses_cpu_tensors():
     # The eager reference model of kernel.py stays available and runs anywhere.
     ref = kernel.Model()(x.float(), *[w.float() for w in ws])
     assert ref.shape == (4, 128)
+
+
+def test_kernel_dtype_keeps_the_input_type():
+    # Outside autocast the network runs in x's own type (the reference's
+    # INPUT_DTYPE kernels, mlp_fused.md:159-166): bf16, fp16 and fp32 as
+    # they are, float64 in fp32 (keeping the range), other types in fp16.
+    from mlpmk.autograd import kernel_dtype
+
+    for dt, want in ((torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                     (torch.float32, torch.float32), (torch.float64, torch.float32),
+                     (torch.int32, torch.float16)):
+        assert kernel_dtype(torch.empty(2, 2, dtype=dt), (2, 256, 2)) == want, dt
