@@ -388,3 +388,22 @@ def test_fp32_launcher_wider_than_128_matches_model():
     _check_rows(out.cpu().numpy(), ref, "launcher fp32 H=256", tol=1e-5)
     eager = kernel.Model()(x, *ws)
     _check_rows(out.cpu().numpy(), eager.double().cpu().numpy(), "launcher fp32 H=256 vs eager Model", tol=1e-5)
+
+
+def test_float64_module_runs_in_fp32():
+    # float64 parameters and x: the network runs in fp32 (the widest type the
+    # library computes in) and autograd hands float64 gradients back.
+    import fused_mlp
+
+    torch.manual_seed(12)
+    model = fused_mlp.FusedMLPSoftplus().cuda().double()
+    x = torch.randn(2048, 128, device="cuda", dtype=torch.float64).requires_grad_(True)
+    out = model(x)
+    assert out.dtype == torch.float32
+    out.sum().backward()
+    assert x.grad.dtype == torch.float64 and all(w.grad.dtype == torch.float64 for w in model.weights)
+    ref_out, ref_dx, ref_g = _torch64(x, list(model.weights))
+    _check_rows(out.detach().cpu().numpy(), ref_out, "fp64 module out")
+    _check_rows(x.grad.cpu().numpy(), ref_dx, "fp64 module dx")
+    for i, (w, rg) in enumerate(zip(model.weights, ref_g)):
+        _check_dw32(w.grad.cpu().numpy(), rg, f"fp64 module dW{i + 1}")
