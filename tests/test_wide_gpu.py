@@ -239,23 +239,25 @@ def test_module_with_wide_hidden_trains(H, n_layers, out_f):
 
 
 @pytest.mark.parametrize("wn", [False, True])
-def test_modules_deeper_than_five_layers_train(wn):
-    # 7 layers: the fused kernels take 2..5, so the forward runs layer by
-    # layer and the backward is the fallback (weight norm: the library's
-    # single-launch kernels, which take up to 8 layers).
+@pytest.mark.parametrize("D,H,out_f,n_layers", [(64, 96, 32, 7), (3, 64, 4, 3)])
+def test_modules_no_fused_kernel_takes_train(wn, D, H, out_f, n_layers):
+    # 7 layers (the fused kernels take 2..5) and a 3-wide input (xyz of a
+    # neural field; the fused kernels take input widths in multiples of 16):
+    # the forward runs layer by layer and the backward is the fallback
+    # (weight norm: the library's single-launch kernels, up to 8 layers).
     from mlpmk import autograd as mag
 
     torch.manual_seed(6)
     cls = fused_mlp.FusedMLPSoftplusWN if wn else fused_mlp.FusedMLPSoftplus
-    model = cls(D=64, H=96, out_features=32, n_layers=7).cuda()
+    model = cls(D=D, H=H, out_features=out_f, n_layers=n_layers).cuda()
     assert mag._layerwise(tuple(model.dims), torch.float16)
-    x = torch.randn(1500, 64, device="cuda").half().requires_grad_(True)
+    x = torch.randn(1500, D, device="cuda").half().requires_grad_(True)
     with torch.autocast("cuda", dtype=torch.float16):
         out = model(x)
     assert out.dtype == torch.float16
     out.float().sum().backward()
     if wn:
-        ws = [model.v(i).detach() * (model.g(i).detach() / model.v(i).detach().norm(dim=0)) for i in range(7)]
+        ws = [model.v(i).detach() * (model.g(i).detach() / model.v(i).detach().norm(dim=0)) for i in range(n_layers)]
         ws16 = [w.half() for w in ws]
     else:
         ws16 = [w.detach().half() for w in model.weights]
