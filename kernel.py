@@ -107,7 +107,8 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
 
 def _fused_mlp_fwd(x, w1, w2, w3):
     """Inference forward: one kernel launch, no intermediate in global memory
-    (networks no fused kernel takes -- fp32 ones wider than 128, any wider
+    (an input width that is not a multiple of 16 is zero-padded to one first;
+    networks no fused kernel takes -- fp32 ones wider than 128, any wider
     than 256 -- run layer by layer: mlpmk.fallback.fwd)."""
     x = x.contiguous()
     w1, w2, w3 = w1.contiguous(), w2.contiguous(), w3.contiguous()
@@ -116,9 +117,15 @@ def _fused_mlp_fwd(x, w1, w2, w3):
     if x.dtype in (torch.float32, torch.float16, torch.bfloat16):
         dims = [x.shape[1], w1.shape[1], w2.shape[1], N3]
         if not _ops.fwd_supported(dims, x.dtype):
-            from mlpmk import fallback
+            pad = -dims[0] % 16
+            if pad and _ops.fwd_supported([dims[0] + pad] + dims[1:], x.dtype):
+                # Input width not a multiple of 16: zero columns of x and zero
+                # rows of W1 add nothing to x @ W1.
+                x, w1 = F.pad(x, (0, pad)), F.pad(w1, (0, 0, 0, pad))
+            else:
+                from mlpmk import fallback
 
-            return fallback.fwd(x, [w1, w2, w3])
+                return fallback.fwd(x, [w1, w2, w3])
     out = torch.empty((M, N3), device=x.device, dtype=x.dtype)
     _ops.fwd_into(x, [w1, w2, w3], out)
     return out

@@ -41,6 +41,7 @@ library's elementwise kernels.
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib, ops
 
@@ -146,6 +147,24 @@ def _layerwise(dims, dtype):
     return not ok
 
 
+def _input_pad(dims, dtype):
+    """Zero columns to append to ``x`` (and zero rows to W_1) so that a
+    fused forward takes the network: input widths that are not multiples of
+    16 (e.g. the 3 coordinates of a neural field) where the padded network
+    is otherwise a fused one; 0 if none is needed or none helps.  The
+    padding adds nothing to any product; dx and dW_1 drop it again."""
+    d0 = dims[0]
+    if d0 % 16 == 0:
+        return 0
+    pad = -d0 % 16
+    return 0 if _layerwise((d0 + pad,) + tuple(dims[1:]), dtype) else pad
+
+
+def _padded(x, w0, pad):
+    """``x`` with ``pad`` zero columns and ``w0`` with ``pad`` zero rows."""
+    return F.pad(x, (0, pad)), F.pad(w0, (0, 0, 0, pad))
+
+
 def _needs_graph(*tensors):
     """True when autograd will run a backward through this call."""
     return torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
@@ -180,6 +199,11 @@ class FusedMLPFunction(torch.autograd.Function):
         dt = kernel_dtype(x, dims)
         x = x.to(dt).contiguous()
         weights = [w.to(dt).contiguous() for w in weights]
+        pad = _input_pad(dims, dt)
+        if pad:
+            x, w0 = _padded(x, weights[0], pad)
+            weights = [w0] + weights[1:]
+            dims = (dims[0] + pad,) + dims[1:]
         if any(ctx.needs_input_grad):
             rc = _use_recompute(dims, int(x.shape[0]), ctx.needs_input_grad[0], dt)
             if _layerwise(dims, dt):
@@ -191,6 +215,7 @@ class FusedMLPFunction(torch.autograd.Function):
             ctx.save_for_backward(x, *weights, *[h for h in hs if h is not None])
             ctx.dims = dims
             ctx.recompute = rc
+            ctx.pad = pad
         elif _layerwise(dims, dt):
             from . import fallback
 
@@ -223,6 +248,10 @@ class FusedMLPFunction(torch.autograd.Function):
         else:
             dws = [torch.zeros(w.shape, dtype=torch.float32, device=w.device) for w in weights]
             _run_bwd(x, weights, hs, dout, dws, dx)
+        if ctx.pad:  # drop the zero columns of x (rows of W_1) the forward appended
+            d0 = dims[0] - ctx.pad
+            dx = dx[:, :d0] if dx is not None else None
+            dws[0] = dws[0][:d0]
         return (dx, *[d if need else None for d, need in zip(dws, ctx.needs_input_grad[1:])])
 
 
@@ -264,6 +293,22 @@ class FusedMLPWNFunction(torch.autograd.Function):
         wb, es = w_all.data_ptr(), w_all.element_size()
         w_ptrs = [wb + es * o for o in woff]
         M = int(x.shape[0])
+        ctx.pad = pad = _input_pad(dims, x.dtype)
+        if pad:
+            # Input width padded to a multiple of 16 (zero columns of x, zero
+            # rows of W_1) so that the fused kernels take the network.
+            ws = _split(w_all, dims)
+            xp, w0 = _padded(x, ws[0], pad)
+            ws = [w0] + ws[1:]
+            if any(ctx.needs_input_grad):
+                pdims = (dims[0] + pad,) + dims[1:]
+                rc = _use_recompute(pdims, M, ctx.needs_input_grad[0], x.dtype)
+                out, hs = ops.fwd(xp, ws, stash=True, recompute=rc)
+                ctx.save_for_backward(xp, v_all, g_all, w_all, inv_all, *[h for h in hs if h is not None])
+                ctx.dims = dims
+                ctx.recompute = rc
+                return out
+            return ops.fwd(xp, ws)
         if _layerwise(dims, x.dtype):
             from . import fallback
 
@@ -301,7 +346,26 @@ class FusedMLPWNFunction(torch.autograd.Function):
         M = int(x.shape[0])
         dout = _as_row_broadcast(dout.to(x.dtype))
         dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        if _backward_impl() == "fused" and _fused_bwd_supported(dims, x.dtype):
+        if ctx.pad:
+            # x was saved padded: W_1 padded the same way, dW_1 computed padded
+            # and its first rows copied into the flat block, dx cut back.
+            pdims = (dims[0] + ctx.pad,) + dims[1:]
+            ws = _split(w_all, dims)
+            ws = [F.pad(ws[0], (0, 0, 0, ctx.pad))] + ws[1:]
+            dw_all = torch.empty(nw, dtype=torch.float32, device=dev)
+            dws = _split(dw_all, dims)
+            dw0 = torch.empty((pdims[0], dims[1]), dtype=torch.float32, device=dev)
+            if _backward_impl() == "fused" and _fused_bwd_supported(pdims, x.dtype):
+                ops.bwd(x, ws, hs, dout, [dw0] + dws[1:], dx, accumulate=False)
+            else:
+                dw0.zero_()
+                for d in dws[1:]:
+                    d.zero_()
+                _run_bwd(x, ws, hs, dout, [dw0] + dws[1:], dx)
+            dws[0].copy_(dw0[: dims[0]])
+            if dx is not None:
+                dx = dx[:, : dims[0]]
+        elif _backward_impl() == "fused" and _fused_bwd_supported(dims, x.dtype):
             # dW written by the library (MLPMK_BWD_WRITE_DW): no zero-fill launch.
             dw_all = torch.empty(nw, dtype=torch.float32, device=dev)
             dout, row_stride = ops._dout_rows(dout, M, dims[-1], x.dtype, dev)
@@ -358,6 +422,10 @@ def fused_mlp(x, *weights):
     dt = kernel_dtype(x, dims)
     x = x.to(dt).contiguous()
     weights = [w.to(dt).contiguous() for w in weights]
+    pad = _input_pad(dims, dt)
+    if pad:
+        x, w0 = _padded(x, weights[0], pad)
+        return ops.fwd(x, [w0] + weights[1:])
     if _layerwise(dims, dt):
         from . import fallback
 
@@ -375,6 +443,11 @@ def fused_mlp_wn(x, v_all, g_all, dims):
     w_all = torch.empty(sum(dims[i] * dims[i + 1] for i in range(len(dims) - 1)), dtype=x.dtype, device=x.device)
     inv_all = torch.empty(sum(dims[1:]), dtype=torch.float32, device=x.device)
     ops.wn_fwd(dims, v_all.contiguous(), g_all.contiguous(), w_all, inv_all)
+    pad = _input_pad(dims, x.dtype)
+    if pad:
+        ws = _split(w_all, dims)
+        xp, w0 = _padded(x, ws[0], pad)
+        return ops.fwd(xp, [w0] + ws[1:])
     if _layerwise(dims, x.dtype):
         from . import fallback
 

@@ -115,3 +115,20 @@ def test_kernel_dtype_keeps_the_input_type():
                      (torch.float32, torch.float32), (torch.float64, torch.float32),
                      (torch.int32, torch.float16)):
         assert kernel_dtype(torch.empty(2, 2, dtype=dt), (2, 256, 2)) == want, dt
+
+
+def test_input_pad_rule():
+    # Input widths that are not multiples of 16 are zero-padded to the next
+    # one where the padded network has a fused forward; otherwise (too deep,
+    # fp32 wider than 128, any width above 256) nothing is padded.
+    from mlpmk.autograd import _input_pad
+
+    f16, f32 = torch.float16, torch.float32
+    assert _input_pad((3, 64, 64, 4), f16) == 13
+    assert _input_pad((63, 128, 128, 8), torch.bfloat16) == 1
+    assert _input_pad((5, 256, 256, 256, 16), f16) == 11
+    assert _input_pad((3, 64, 64, 64, 16), f32) == 13
+    assert _input_pad((16, 64, 64, 4), f16) == 0
+    assert _input_pad((3,) + (64,) * 7 + (4,), f16) == 0
+    assert _input_pad((3, 256, 256, 16), f32) == 0
+    assert _input_pad((3, 320, 320, 16), f16) == 0
