@@ -124,19 +124,33 @@ def test_whole_training_step_graph(m):
         _check_oracle(got[2], o_dg, f"replay {r}: dg vs oracle", grad=True)
 
 
+def _fresh_x_d(m, seed, d):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(m, d, device="cuda", generator=g).half()
+
+
 @pytest.mark.parametrize("m", [4096, 131072])
-@pytest.mark.parametrize("kind", ["fp32", "h256"])
+@pytest.mark.parametrize("kind", ["fp32", "h256", "d3"])
 def test_training_step_graph_two_pass_shapes(kind, m):
     # The weight-norm module with fp32 tensors (bf16 hi/lo split operands)
     # and with hidden width 256: both train through the two-pass backward at
     # every M (dz through the workspace, weight gradients written by atomics
-    # after the data-gradient pass cleared dW).  Replays with fresh inputs and
-    # eager work in between, each against an eager copy of the model.
+    # after the data-gradient pass cleared dW).  "d3": a 3-wide input, padded
+    # inside the step to 16 columns (torch's pad kernels captured with the
+    # library's).  Replays with fresh inputs and eager work in between, each
+    # against an eager copy of the model.
     torch.manual_seed(1)
-    model = (fused_mlp.FusedMLPSoftplusWN() if kind == "fp32" else fused_mlp.FusedMLPSoftplusWN(H=256)).cuda()
+    if kind == "fp32":
+        model = fused_mlp.FusedMLPSoftplusWN()
+    elif kind == "h256":
+        model = fused_mlp.FusedMLPSoftplusWN(H=256)
+    else:
+        model = fused_mlp.FusedMLPSoftplusWN(D=3, out_features=16)
+    model = model.cuda()
     ref_model = copy.deepcopy(model)
     dt = torch.float32 if kind == "fp32" else torch.float16
-    static_x = _fresh_x(m, 0).to(dt)
+    width = 3 if kind == "d3" else 128
+    static_x = _fresh_x_d(m, 0, width).to(dt)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -152,7 +166,7 @@ def test_training_step_graph_two_pass_shapes(kind, m):
     static_dv, static_dg = model.v_all.grad, model.g_all.grad
     assert static_out.dtype == dt and static_dv.dtype == torch.float32
     for r in range(3):
-        static_x.copy_(_fresh_x(m, 200 + r).to(dt))
+        static_x.copy_(_fresh_x_d(m, 200 + r, width).to(dt))
         graph.replay()
         torch.cuda.synchronize()
         got = (static_out.clone(), static_dv.clone(), static_dg.clone())

@@ -333,6 +333,17 @@ def test_modules_padded_input_train(wn, D, H, out_f, n_layers, dtype):
         _check_grad(model.g_all.grad[:H].double().cpu().numpy(), dg0.numpy(), "dg1", k)
 
 
+def test_padded_input_empty_batch():
+    # M = 0 through the padded path: empty output, empty gradients.
+    model = fused_mlp.FusedMLPSoftplus(D=3, H=64, out_features=16).cuda().half()
+    x = torch.zeros(0, 3, device="cuda", dtype=torch.float16, requires_grad=True)
+    out = model(x)
+    assert out.shape == (0, 16)
+    out.sum().backward()
+    assert x.grad.shape == (0, 3)
+    assert model.weights[0].grad.shape == (3, 64) and not model.weights[0].grad.any()
+
+
 def test_launcher_padded_input():
     # kernel.py's launcher pads K1 the same way.
     torch.manual_seed(8)
