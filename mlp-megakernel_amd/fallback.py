@@ -25,9 +25,10 @@ set to ``"fallback"``; this path is kept as the reference's alternative and as
 a comparator.  Same arguments and results as ``ops.bwd``.
 
 For networks no fused forward takes (fp32 tensors wider than 128, any
-tensors wider than 256), :func:`fwd` is the matching forward: fp32 library
-GEMMs and this library's fp32 softplus kernel (``mlpmk_softplus_f32``);
-:func:`bwd` then runs the backward (every GEMM in fp32 for fp32 tensors).
+tensors wider than 256 or deeper than 5 layers), :func:`fwd` is the matching
+forward: fp32 library GEMMs and this library's fp32 softplus kernel
+(``mlpmk_softplus_f32``); :func:`bwd` then runs the backward (every GEMM in
+fp32 for fp32 tensors).
 """
 from __future__ import annotations
 
@@ -72,7 +73,8 @@ def softplus_f32(z, out=None):
 
 def fwd(x, weights, stash=False):
     """Forward layer by layer, for the networks no fused forward takes: fp32
-    tensors wider than 128, and any tensors wider than 256.  ``z = a @ W_l``
+    tensors wider than 128, any tensors wider than 256, more than 5 layers,
+    hidden widths that are not multiples of 16.  ``z = a @ W_l``
     as an fp32 library GEMM (rocBLAS / hipBLASLt through torch; 16-bit
     values are exact in fp32, so this is the fused kernels' fp32
     accumulation), then the fp32 softplus kernel on every hidden layer, whose
