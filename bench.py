@@ -445,8 +445,12 @@ def _train_step_bench(torch, fused_mlp, m, steps, warmup, n_layers, dtype, hidde
         with torch.cuda.graph(g, pool=graphs[0].pool() if graphs else None):
             model(xs[k]).sum().backward()
         graphs.append(g)
-    with gc_paused():
-        gms = time_launches(torch, lambda i: graphs[i % nx].replay(), steps, warmup)
+    def replay(i):
+        graphs[i % nx].replay()
+
+    with gc_paused():  # the captures idled the GPU: ramp its clock again first
+        ramp_clock(torch, replay, seconds=0.2)
+        gms = time_launches(torch, replay, steps, warmup)
     # per row: x + out + stash written in the forward; dout, stash, x read
     # back (no dx).  Flops: forward 2*sum(in*out), dgrad of layers 1.., wgrad
     # (+ the recomputed layer).
@@ -523,7 +527,8 @@ def backward_comparison(torch, ops, m, steps=50, warmup=10):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             fn(0)
-        with gc_paused():
+        with gc_paused():  # the capture idled the GPU: ramp its clock again first
+            ramp_clock(torch, lambda i: graph.replay(), seconds=0.1)
             replay = time_launches(torch, lambda i: graph.replay(), steps, warmup)
         res[name] = {"eager_ms": round(eager, 5), "graph_ms": round(replay, 5)}
     torch.cuda.synchronize()
