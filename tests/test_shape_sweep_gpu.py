@@ -13,6 +13,9 @@ The reference's kernel takes any tile-multiple width as constexpr tile loops
 (/root/reference/kernel.py:60-63,86-87,121-123) and its modules take D, H,
 out_features (/root/reference/README.md:62,68).
 
+A second sweep draws fp32-tensor networks (widths up to 128, the split-
+operand kernels).
+
 Tolerances are those of the per-dtype files: outputs at atol = rtol = 1e-2
 (fp16) and 3e-2 (bf16); weight gradients per entry within 2e-2 |ref| + 2e-3
 max|ref| and relative Frobenius 1e-2 (fp16), 4e-2 |ref| + (L + 1) 1e-3
@@ -102,3 +105,42 @@ def test_random_shape_train_matches_oracle(case):
     if with_dx:
         ok, err, excess = orc.allclose_report(dx.float().cpu().numpy(), rdx, tol, tol)
         assert ok, f"dx: max|err|={err:.4g}, worst excess {excess:.4g}"
+
+
+def _draw_cases_f32(n, seed=2027):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        L = int(rng.integers(2, 6))
+        dims = [16 * int(rng.integers(1, 9)) for _ in range(L)]
+        dims.append(int(rng.integers(1, 129)) if rng.random() < 0.4 else 8 * int(rng.integers(1, 17)))
+        m = int(rng.choice([1, 33, 777, 4099, 20000]))
+        if ops.fwd_supported(dims, torch.float32):
+            cases.append((tuple(dims), m))
+    return cases
+
+
+CASES_F32 = _draw_cases_f32(24)
+
+
+@pytest.mark.parametrize("dims,m", CASES_F32, ids=[f"{'-'.join(map(str, d))}_M{m}" for d, m in CASES_F32])
+def test_random_shape_fp32_matches_oracle(dims, m):
+    # fp32 tensors (bf16 hi/lo split operands) at the tolerances of
+    # test_fp32_gpu.py: outputs and dx within 2e-4 of their row's scale,
+    # weight gradients within 1e-3 |ref| + 1e-4 max|ref|, relative Frobenius
+    # 5e-4, against the oracle in float64.
+    from test_fp32_gpu import _check_dw32, _check_rows, _inputs, _train32
+
+    print(f"case fp32 {dims} M={m}", flush=True)
+    x, ws = _inputs(dims, m, seed=sum(dims) + m)
+    xd = torch.from_numpy(x).cuda()
+    wd = [torch.from_numpy(w).cuda() for w in ws]
+    out = ops.fwd(xd, wd)
+    assert out.dtype == torch.float32 and out.shape == (m, dims[-1])
+    _check_rows(out.cpu().numpy(), orc.forward(x, ws, dtype=np.float64), "out")
+    if not ops.bwd_supported(list(dims), torch.float32):
+        return  # fp32 output widths not a multiple of 8: the library-GEMM backward (test_fp32_gpu.py)
+    dws, dx, rdws, rdx = _train32(dims, m, seed=sum(dims) + m, dout_mode="dense", with_dx=True)
+    for i in range(len(dims) - 1):
+        _check_dw32(dws[i].cpu().numpy(), rdws[i], f"dW{i + 1}")
+    _check_rows(dx.cpu().numpy(), rdx, "dx")
