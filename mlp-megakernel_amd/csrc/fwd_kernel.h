@@ -512,9 +512,11 @@ constexpr bool kPropagate = N::L <= 3;
 // consecutive lanes and stream past L2 (nt); wider rows are written a piece
 // at a time, so they keep the default policy and L2 merges the pieces into
 // whole lines before they go to HBM (5-layer 128-wide at 1M rows: WRITE_SIZE
-// 1.44x -> 1.00x the output bytes, 201.3 -> 194.5 us, same box).
-template <int ROW_BYTES>
-constexpr int kDirectOutStore = ROW_BYTES > 64 ? kStashStore : kStreamStore;
+// 1.44x -> 1.00x the output bytes, 201.3 -> 194.5 us, same box).  The
+// training forward's outputs keep the default policy at any width
+// (kOutStore).
+template <int ROW_BYTES, bool STASH>
+constexpr int kDirectOutStore = ROW_BYTES > 64 ? kStashStore : kOutStore<STASH>;
 
 // Stores the staged 128-byte segment mb (fp32 features [32 mb, 32 mb + 32))
 // of the wave's 32 stash rows of width W: 8 rows x 128 bytes (8 whole cache
@@ -574,7 +576,7 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       const f16x8 hi = pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]);
       // The compile-time width (128) bounds the row: wide rows use the
       // merging policy, as below.
-      constexpr int P = kDirectOutStore<N::d[N::L] * 2>;
+      constexpr int P = kDirectOutStore<N::d[N::L] * 2, STASH>;
       if (OW % 8 == 0) {
         if (c < OW) buf_store16<P>(lo, io.out, e * 2);
         if (c + 16 < OW) buf_store16<P>(hi, io.out, e * 2 + 32);
@@ -593,7 +595,7 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
       }
     } else if constexpr (LAST) {
       const f32x16 v = acc[nb] * kIn;  // ln 2 is folded into the staged W_L
-      constexpr int P = kDirectOutStore<Nout * 2>;
+      constexpr int P = kDirectOutStore<Nout * 2, STASH>;
       if (lo_ok) buf_store16<P>(pack8<N::bf>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]), io.out, elem * 2);
       if (hi_ok) buf_store16<P>(pack8<N::bf>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]), io.out, elem * 2 + 32);
     } else {
@@ -669,8 +671,8 @@ __device__ __forceinline__ void epilogue(const BlockIO& io, const f32x16 (&acc)[
 
 // Stores the staged 128-byte row segments of output features
 // [64 seg, 64 seg + 64) with 16-byte stores, 8 rows x 128 bytes (8 whole cache
-// lines) per instruction.
-template <class N, int NB>
+// lines) per instruction, with cache policy POL.
+template <class N, int NB, int POL>
 __device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane) {
   constexpr int Nout = N::d[N::L];
   constexpr int TC = LdsPlan<N, NB, 1>::kTileChunks;
@@ -684,7 +686,7 @@ __device__ __forceinline__ void flush_stage(const BlockIO& io, int seg, int lane
     const int q = 64 * i + lane;  // linear 16-byte chunk of the tile
     const int row = q >> 3, c = q & 7;
     const i32x4 v = io.stage[stage_slot(row, c)];
-    __builtin_amdgcn_raw_buffer_store_b128(v, io.out, row * Nout * 2 + seg * 128 + c * 16, 0, kStreamStore);
+    __builtin_amdgcn_raw_buffer_store_b128(v, io.out, row * Nout * 2 + seg * 128 + c * 16, 0, POL);
   }
   // The next writes into the tile must stay behind these reads.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -753,7 +755,7 @@ __device__ __forceinline__ void step(const FwdParams& p, const BlockIO& io, Chai
   }
   epilogue<N, l, NB, STASH, STAGE, EXACT, KSM>(io, c.acc[t & 1], mb, c.template out<l>(), c.bad, c.ovf, lane);
   if constexpr (l == N::L - 1 && STAGE) {
-    if (mb & 1) flush_stage<N, NB>(io, mb >> 1, lane);
+    if (mb & 1) flush_stage<N, NB, kOutStore<STASH>>(io, mb >> 1, lane);
   }
   if constexpr (t + 1 < T && !same) {
     chain<N, TN, RF, EARLY, KS1, NB>(c.acc[(t + 1) & 1], c.fr, c.template in<l + 1>(), fb, c.rf);

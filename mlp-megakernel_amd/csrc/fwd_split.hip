@@ -238,8 +238,8 @@ __device__ __forceinline__ void layer(const FwdParams& p, const Frags<N>& f, con
       tout[slot<CH>(n, 4 * w + 2 + g)] = __builtin_bit_cast(i32x4, hi);
     } else {
       const rsrc_t orr = make_rsrc(p.out + row0 * Nout, rows * Nout * 2u);
-      if (lo_ok) buf_store16<kStreamStore>(lo, orr, elem * 2);
-      if (hi_ok) buf_store16<kStreamStore>(hi, orr, elem * 2 + 32);
+      if (lo_ok) buf_store16<kOutStore<STASH>>(lo, orr, elem * 2);
+      if (hi_ok) buf_store16<kOutStore<STASH>>(hi, orr, elem * 2 + 32);
     }
   } else {
     const f32x16 u = acc * kIn;  // log2 e is folded into the staged W_1: u in base-2 units
@@ -287,7 +287,7 @@ __device__ __forceinline__ void layers(const FwdParams& p, const Frags<N>& f, i3
 
 // Output rows of the block from the output tile, whole rows per instruction:
 // wave w stores rows [w * 32 / NWV, (w + 1) * 32 / NWV).
-template <class N>
+template <class N, bool STASH>
 __device__ __forceinline__ void store_rows(const FwdParams& p, const i32x4* tile, int64_t row0, uint32_t rows,
                                            int w, int lane) {
   using G = Geo<N>;
@@ -298,7 +298,7 @@ __device__ __forceinline__ void store_rows(const FwdParams& p, const i32x4* tile
     const int q = 64 * k + lane;
     const int row = w * RPW + q / OC, c = q % OC;
     __builtin_amdgcn_raw_buffer_store_b128(tile[slot<G::CH>(row, c)], orr, (row * OUT + 8 * c) * 2, 0,
-                                           kStreamStore);
+                                           kOutStore<STASH>);
   }
 }
 
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(Geo<N>::NWV * 64) void fwd_split_kernel(FwdParams p
       layers<N, STASH, true>(p, f, tiles, row0, rows, w, n, g, m);
       __syncthreads();
     }
-    if constexpr (G::STAGE_OUT) store_rows<N>(p, tiles + OUTT, row0, rows, w, lane);
+    if constexpr (G::STAGE_OUT) store_rows<N, STASH>(p, tiles + OUTT, row0, rows, w, lane);
     par ^= 1;
     b = next;
     if (b >= nblk) break;
