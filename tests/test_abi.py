@@ -199,6 +199,35 @@ def test_wn_and_copy_validation_codes():
     assert lib.mlpmk_copy(A, A, 0, None) == OK
 
 
+def test_elementwise_validation_codes():
+    lib = _lib.get()
+    assert lib.mlpmk_softplus_f32(A, A, -1, None) == INVALID
+    assert lib.mlpmk_softplus_f32(A, A, 0, None) == OK
+    assert lib.mlpmk_softplus_f32(None, A, 4, None) == INVALID
+    assert lib.mlpmk_softplus_f32(A, A + 4, 4, None) == MISALIGNED
+    assert b"h=" in lib.mlpmk_last_error()
+    assert lib.mlpmk_sigmoid_h_mul(A, A, 7, A, None, 1, 4, None) == INVALID  # dh fp32, fp16 or bf16
+    assert lib.mlpmk_sigmoid_h_mul(A, A, 1, A, A, 0, 4, None) == INVALID  # dz16 is a 16-bit copy
+    assert lib.mlpmk_sigmoid_h_mul(A, A, 1, A, None, 1, -1, None) == INVALID
+    assert lib.mlpmk_sigmoid_h_mul(A, A, 1, A, None, 1, 0, None) == OK
+    assert lib.mlpmk_sigmoid_h_mul(A, A + 2, 1, A, None, 1, 4, None) == MISALIGNED
+
+
+@pytest.mark.parametrize("dims,f16,f32", [((128, 128, 128, 128), 1, 1), ((64, 96, 3), 1, 1),
+                                          ((128, 256, 128), 1, 0), ((128, 320, 128), 0, 0),
+                                          ((3, 64, 64), 0, 0), ((16,) * 7, 0, 0)])
+def test_forward_support_by_dtype(dims, f16, f32):
+    # fp32 tensors have fused kernels up to width 128; 16-bit ones up to 256.
+    lib = _lib.get()
+    p, _k = _lib.int_array(list(dims))
+    L = len(dims) - 1
+    assert lib.mlpmk_fwd_supported_dtype(L, p, _lib.DTYPE_F16) == f16
+    assert lib.mlpmk_fwd_supported_dtype(L, p, _lib.DTYPE_BF16) == f16
+    assert lib.mlpmk_fwd_supported_dtype(L, p, _lib.DTYPE_F32) == f32
+    assert lib.mlpmk_fwd_supported_dtype(L, p, 7) == 0
+    assert ops.fwd_supported(list(dims), torch.float32) is bool(f32)
+
+
 def test_python_wrappers_validate_before_the_library():
     x = torch.zeros((4, 128), dtype=torch.float16)
     ws = [torch.zeros((128, 128), dtype=torch.float16) for _ in range(3)]
