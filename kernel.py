@@ -105,6 +105,23 @@ def _pick_config(M, K1, N1, N2, N3, fp32=False, num_cus=None):
     return bm, N3, 16, 16, 16, warps
 
 
+# (K1, N1, N2, N3, dtype) -> how _fused_mlp_fwd runs it: 0 one fused launch
+# (also every other dtype, which fwd_into rejects with its own message), a
+# positive count of zero columns to pad x with first, -1 layer by layer.  The
+# library's answer is cached: asking it costs ~2 us of ctypes per call.
+_ROUTES = {}
+
+
+def _route(key):
+    *dims, dt = key
+    if dt not in (torch.float32, torch.float16, torch.bfloat16) or _ops.fwd_supported(dims, dt):
+        return 0
+    pad = -dims[0] % 16
+    if pad and _ops.fwd_supported([dims[0] + pad] + dims[1:], dt):
+        return pad
+    return -1
+
+
 def _fused_mlp_fwd(x, w1, w2, w3):
     """Inference forward: one kernel launch, no intermediate in global memory
     (an input width that is not a multiple of 16 is zero-padded to one first;
@@ -114,18 +131,18 @@ def _fused_mlp_fwd(x, w1, w2, w3):
     w1, w2, w3 = w1.contiguous(), w2.contiguous(), w3.contiguous()
     M = x.shape[0]
     N3 = w3.shape[1]
-    if x.dtype in (torch.float32, torch.float16, torch.bfloat16):
-        dims = [x.shape[1], w1.shape[1], w2.shape[1], N3]
-        if not _ops.fwd_supported(dims, x.dtype):
-            pad = -dims[0] % 16
-            if pad and _ops.fwd_supported([dims[0] + pad] + dims[1:], x.dtype):
-                # Input width not a multiple of 16: zero columns of x and zero
-                # rows of W1 add nothing to x @ W1.
-                x, w1 = F.pad(x, (0, pad)), F.pad(w1, (0, 0, 0, pad))
-            else:
-                from mlpmk import fallback
+    key = (x.shape[1], w1.shape[1], w2.shape[1], N3, x.dtype)
+    route = _ROUTES.get(key)
+    if route is None:
+        route = _ROUTES[key] = _route(key)
+    if route > 0:
+        # Input width not a multiple of 16: zero columns of x and zero rows of
+        # W1 add nothing to x @ W1.
+        x, w1 = F.pad(x, (0, route)), F.pad(w1, (0, 0, 0, route))
+    elif route < 0:
+        from mlpmk import fallback
 
-                return fallback.fwd(x, [w1, w2, w3])
+        return fallback.fwd(x, [w1, w2, w3])
     out = torch.empty((M, N3), device=x.device, dtype=x.dtype)
     _ops.fwd_into(x, [w1, w2, w3], out)
     return out
