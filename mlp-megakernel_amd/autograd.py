@@ -42,6 +42,7 @@ from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
+from torch.autograd.function import once_differentiable
 
 from . import _lib, ops
 
@@ -226,6 +227,7 @@ class FusedMLPFunction(torch.autograd.Function):
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
+    @once_differentiable  # the library's gradients carry no graph: a second derivative raises
     def backward(ctx, dout):
         dims = ctx.dims
         L = len(dims) - 1
@@ -336,6 +338,7 @@ class FusedMLPWNFunction(torch.autograd.Function):
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
+    @once_differentiable  # the library's gradients carry no graph: a second derivative raises
     def backward(ctx, dout):
         dims = ctx.dims
         nw, ng, woff = _layout(dims)

@@ -342,3 +342,18 @@ def test_empty_batch_trains_to_zero_gradients(wn):
         assert torch.count_nonzero(p_.grad) == 0
     with torch.no_grad():
         assert tuple(model(x).shape) == (0, 128)
+
+
+@pytest.mark.parametrize("wn", [False, True])
+def test_second_derivative_raises_instead_of_returning_zeros(wn):
+    # The library's gradients are written through raw pointers and carry no
+    # autograd graph, so a double backward would silently treat them as
+    # constants where dL/dout itself depends on the inputs (loss = sum(out^2));
+    # the backward is marked once-differentiable and raises instead.
+    model = (fused_mlp.FusedMLPSoftplusWN() if wn else fused_mlp.FusedMLPSoftplus()).cuda()
+    x = torch.randn(64, 128, device="cuda").half().requires_grad_(True)
+    out = model(x)
+    (gx,) = torch.autograd.grad((out.float() ** 2).sum(), x, create_graph=True)
+    assert gx.shape == x.shape
+    with pytest.raises(RuntimeError, match="differentiate twice"):
+        gx.float().sum().backward()
