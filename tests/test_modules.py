@@ -132,3 +132,16 @@ def test_input_pad_rule():
     assert _input_pad((3,) + (64,) * 7 + (4,), f16) == 0
     assert _input_pad((3, 256, 256, 16), f32) == 0
     assert _input_pad((3, 320, 320, 16), f16) == 0
+
+
+def test_launcher_route_rule():
+    # kernel._fused_mlp_fwd's cached route per (K1, N1, N2, N3, dtype): one
+    # fused launch (0), zero columns to pad x with first (> 0), or layer by
+    # layer (-1); other dtypes go to the launch, which rejects them.
+    f16, f32 = torch.float16, torch.float32
+    assert kernel._route((128, 128, 128, 128, f16)) == 0
+    assert kernel._route((3, 128, 128, 64, f16)) == 13
+    assert kernel._route((3, 128, 128, 64, f32)) == 13
+    assert kernel._route((3, 256, 256, 64, f32)) == -1  # fp32 wider than 128
+    assert kernel._route((128, 320, 128, 128, f16)) == -1  # wider than 256
+    assert kernel._route((128, 128, 128, 128, torch.int32)) == 0
