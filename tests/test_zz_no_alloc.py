@@ -26,14 +26,14 @@ def _ptrs(ts):
     return _lib.ptr_array([t.data_ptr() if t is not None else None for t in ts])
 
 
-def _call(entry, dims, x, ws, hs, dout, dws, dx, workspace=None):
+def _call(entry, dims, x, ws, hs, dout, dws, dx, workspace=None, dtype=_lib.DTYPE_F16):
     lib = _lib.get()
     pd, _k1 = _lib.int_array(dims)
     pw, _k2 = _ptrs(ws)
     ph, _k3 = _ptrs(hs)
     pdw, _k4 = _ptrs(dws)
     stream = torch.cuda.current_stream().cuda_stream
-    args = [len(dims) - 1, pd, _lib.DTYPE_F16, x.data_ptr(), pw, ph, dout.data_ptr(), 0,
+    args = [len(dims) - 1, pd, dtype, x.data_ptr(), pw, ph, dout.data_ptr(), 0,
             dx.data_ptr() if dx is not None else None, pdw]
     if entry == "ws":
         args += [workspace.data_ptr(), workspace.numel()]
@@ -214,3 +214,51 @@ def test_first_noalloc_call_inside_a_graph_capture():
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0 and "capture ok" in r.stdout, r.stdout[-2000:] + r.stderr[-4000:]
+
+
+_CODES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+
+
+@pytest.mark.parametrize("dims,dt,m1,m2,with_dx", [
+    ((128, 256, 256, 128), torch.float16, 16384, 4096, True),  # widths above 128: the two-pass form
+    ((128, 128, 128, 128), torch.float32, 32768, 4096, True),  # fp32 tensors: fp32 dz in the scratch
+    ((64, 96, 48, 16), torch.bfloat16, 20000, 3000, False),    # bf16, one-pass then two-pass
+])
+def test_noalloc_other_types_and_widths_on_two_calls(dims, dt, m1, m2, with_dx):
+    # The same two-call check for the element types and widths whose
+    # backward hands dz through the scratch (two-pass) or sums partials there.
+    code = _CODES[dt]
+    for call, m in enumerate((m1, m2)):
+        x, ws = orc.make_inputs(dims, m, seed=20 + call, elem="bf16" if dt == torch.bfloat16 else "f16")
+        xd = torch.from_numpy(x).cuda().to(dt)
+        wd = [torch.from_numpy(w).cuda().to(dt) for w in ws]
+        _, hs = ops.fwd(xd, wd, stash=True)
+        dout = torch.ones((1, dims[-1]), dtype=dt, device="cuda")
+        got = []
+        for entry in ("noalloc", "ws"):
+            dws = [torch.zeros((dims[i], dims[i + 1]), dtype=torch.float32, device="cuda") for i in range(len(dims) - 1)]
+            dx = torch.empty_like(xd) if with_dx else None
+            ws_t = None
+            if entry == "ws":
+                nbytes = ops.bwd_workspace_bytes(dims, m, with_dx, dtype=dt)
+                ws_t = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+            rc, err = _call(entry, dims, xd, wd, hs, dout, dws, dx, ws_t, dtype=code)
+            assert rc == 0, f"{entry} call {call}: {err}"
+            torch.cuda.synchronize()
+            got.append((dws, dx))
+        (a_dws, a_dx), (b_dws, b_dx) = got
+        for i, (a, b) in enumerate(zip(a_dws, b_dws)):
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-6 * float(b.abs().max())), f"call {call}: dW{i + 1}"
+        if with_dx:
+            assert torch.equal(a_dx, b_dx), f"call {call}: dx differs from mlpmk_bwd_ws"
+        # and the oracle, on the same (16-bit or fp32) values
+        ref_h = orc.forward(x, ws, return_hidden=True, round_hidden=dt != torch.float32,
+                            elem="bf16" if dt == torch.bfloat16 else "f16")[1]
+        rdws, _ = orc.backward(x, ws, ref_h, np.ones((m, dims[-1]), np.float32), need_dx=False)
+        k = 2.0 if dt == torch.bfloat16 else 1.0
+        for i, (g, r) in enumerate(zip(a_dws, rdws)):
+            g = g.cpu().numpy().astype(np.float64)
+            scale = np.abs(r).max()
+            worst = np.max(np.abs(g - r) - k * (2e-2 * np.abs(r) + 2e-3 * scale))
+            frob = np.linalg.norm(g - r) / np.linalg.norm(r)
+            assert worst <= 0 and frob < k * 1e-2, f"call {call} dW{i + 1}: worst excess {worst:.3g}, frob {frob:.3g}"
